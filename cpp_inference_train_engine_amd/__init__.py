@@ -1,0 +1,97 @@
+"""MI355X-native MLA cached-decode backend: Python binding of ``libmla_hip.so``.
+
+The product is the C ABI declared in ``include/mla_hip.h`` (HIP kernels for
+gfx950).  This module binds it with ctypes so tests and ``bench.py`` can drive
+it with torch-allocated device buffers; torch is only plumbing for device
+memory and streams.  There is no CPU fallback: every entry point raises when
+the library is missing or a call fails.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libmla_hip.so")
+
+MLA_OK = 0
+ERROR_NAMES = {1: "invalid_argument", 2: "io_error", 3: "unsupported", 4: "out_of_memory",
+               5: "gpu_error", 6: "numerical_error"}
+DTYPE_F16, DTYPE_BF16 = 0, 1
+DECODE_FORCE_GENERIC = 1
+
+
+class MlaError(RuntimeError):
+    """A failed C-ABI call; ``code`` is the reference ErrorCode name."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.code = ERROR_NAMES.get(status, f"status{status}")
+        super().__init__(f"{self.code}: {message}")
+
+
+_lib = None
+
+_SIGNATURES = {
+    "mla_last_error": (C.c_char_p, []),
+    "mla_abi_version": (C.c_int, []),
+    "mla_build_metadata": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 4 +
+                           [C.c_int] * 7 + [C.c_void_p] * 9),
+    "mla_read_metadata_info": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "mla_append_latent": (C.c_int, [C.c_void_p] + [C.c_int] * 5 + [C.c_void_p] * 3 +
+                          [C.c_int, C.c_void_p]),
+    "mla_decode_workspace_bytes": (C.c_size_t, [C.c_int] * 3),
+    "mla_decode_attention": (C.c_int, [C.c_void_p] + [C.c_int] * 6 + [C.c_float] +
+                             [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_void_p] * 8 +
+                             [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                              C.c_int]),
+}
+
+
+def lib() -> C.CDLL:
+    """Load the HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return sorted(_SIGNATURES)
+
+
+def check(status: int) -> None:
+    if status != MLA_OK:
+        msg = lib().mla_last_error().decode(errors="replace")
+        raise MlaError(status, msg)
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a torch tensor / numpy array, None for None."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+def stream_handle(stream=None) -> int | None:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+from .ops import (  # noqa: E402  (re-exported operator interface)
+    PagedLatentCache, RaggedBatch, append_latent, build_metadata, decode_attention,
+    decode_workspace_bytes)
+
+__all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
+           "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",
+           "DTYPE_BF16"]

@@ -1,0 +1,156 @@
+// C ABI of the kernel-level entry points (include/mla_hip.h).  Host-side
+// validation, error capture (thread-local message) and kernel launches.
+#include "mla_capi_util.hpp"
+#include "mla_hip.h"
+#include "mla_internal.hpp"
+
+#include <cstdio>
+#include <cstring>
+
+namespace mla {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int gpu_status(hipError_t e, const char* what) {
+    if (e == hipSuccess)
+        return MLA_OK;
+    return fail(e == hipErrorOutOfMemory ? MLA_ERR_OUT_OF_MEMORY : MLA_ERR_GPU,
+                std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" {
+
+const char* mla_last_error(void) { return g_last_error.c_str(); }
+
+int mla_abi_version(void) { return 1; }
+
+int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
+                       const int32_t* cu_pages, const int32_t* page_ids, int page_size,
+                       int max_pages, int num_pool_pages, int split_pages, int target_blocks,
+                       int max_work, int max_rows, int32_t* cu_seqlens_q,
+                       int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
+                       int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
+                       int32_t* work_split, int32_t* info) {
+    if (B < 0 || page_size < 1 || max_pages < 0 || num_pool_pages < 0 || split_pages < 0 ||
+        target_blocks < 1 || max_work < 0 || max_rows < 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: invalid scalar argument");
+    if (!info || !cu_seqlens_q || !cu_seqlens_k || !cu_splits || !cu_pages ||
+        (B > 0 && (!ctx_len || !q_len || !num_splits || (max_pages > 0 && !page_table))) ||
+        (max_work > 0 && (!work_session || !work_split)) || (max_rows > 0 && !slot_mapping))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: null buffer");
+    if ((long long)B * max_pages > (1LL << 40))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: page table too large");
+    MetadataArgs a{B, ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num_pool_pages,
+                   split_pages, target_blocks, max_work, max_rows, cu_seqlens_q, cu_seqlens_k,
+                   page_table, slot_mapping, num_splits, cu_splits, work_session, work_split,
+                   info};
+    return gpu_status(launch_build_metadata(a, static_cast<hipStream_t>(stream)),
+                      "mla_build_metadata");
+}
+
+int mla_read_metadata_info(void* stream, const int32_t* info, int32_t* host_info) {
+    if (!info || !host_info)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_read_metadata_info: null buffer");
+    auto s = static_cast<hipStream_t>(stream);
+    int st = gpu_status(hipMemcpyAsync(host_info, info, 4 * sizeof(int32_t),
+                                       hipMemcpyDeviceToHost, s),
+                        "mla_read_metadata_info");
+    if (st)
+        return st;
+    st = gpu_status(hipStreamSynchronize(s), "mla_read_metadata_info");
+    if (st)
+        return st;
+    if (host_info[0] < 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "invalid ragged batch: session " + std::to_string(host_info[1]) +
+                        " has a bad length, page list or page id, or a capacity was exceeded");
+    return MLA_OK;
+}
+
+int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_size, int dtype,
+                      const float* ckv, const float* krope, const int32_t* slot_mapping,
+                      int num_pool_pages, void* pages) {
+    if (T < 0 || kv_rank < 1 || rope_dim < 0 || page_size < 1 || num_pool_pages < 0 ||
+        (dtype != MLA_DTYPE_F16 && dtype != MLA_DTYPE_BF16))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_append_latent: invalid argument");
+    if (T > 0 && (!ckv || (rope_dim > 0 && !krope) || !slot_mapping || !pages))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_append_latent: null buffer");
+    AppendArgs a{T, kv_rank, rope_dim, page_size, num_pool_pages, ckv, krope, slot_mapping,
+                 static_cast<uint16_t*>(pages)};
+    return gpu_status(launch_append(a, dtype, static_cast<hipStream_t>(stream)),
+                      "mla_append_latent");
+}
+
+size_t mla_decode_workspace_bytes(int max_work, int n_heads, int kv_rank) {
+    if (max_work <= 0 || n_heads <= 0 || kv_rank <= 0)
+        return 0;
+    return (size_t)max_work * n_heads * ((size_t)kv_rank + 2) * sizeof(float);
+}
+
+int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
+                         int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, const int32_t* page_table, int max_pages,
+                         int num_pool_pages, const void* pages, const void* q_latent,
+                         const void* q_rope, const int32_t* num_splits, const int32_t* cu_splits,
+                         const int32_t* work_session, const int32_t* work_split,
+                         const int32_t* info, int max_work, float* out, float* lse,
+                         void* workspace, size_t workspace_bytes, int flags) {
+    if (B < 0 || n_heads < 1 || kv_rank < 1 || kv_rank > 1024 || rope_dim < 0 ||
+        page_size < 1 || max_pages < 0 || num_pool_pages < 0 || max_work < 0 ||
+        (dtype != MLA_DTYPE_F16 && dtype != MLA_DTYPE_BF16) || !(scale > 0.0f))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: invalid argument");
+    if (B == 0 || max_work == 0)
+        return MLA_OK;
+    if (!cu_seqlens_q || !cu_seqlens_k || !page_table || !pages || !q_latent ||
+        (rope_dim > 0 && !q_rope) || !num_splits || !cu_splits || !work_session ||
+        !work_split || !info || !out)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: null buffer");
+    const size_t need = mla_decode_workspace_bytes(max_work, n_heads, kv_rank);
+    if (!workspace || workspace_bytes < need)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "mla_decode_attention: workspace needs " + std::to_string(need) + " bytes");
+    const float* ws = static_cast<const float*>(workspace);
+    DecodeArgs a{};
+    a.B = B;
+    a.H = n_heads;
+    a.kv_rank = kv_rank;
+    a.rope_dim = rope_dim;
+    a.page_size = page_size;
+    a.max_pages = max_pages;
+    a.num_pool_pages = num_pool_pages;
+    a.max_work = max_work;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.cu_q = cu_seqlens_q;
+    a.cu_k = cu_seqlens_k;
+    a.page_table = page_table;
+    a.num_splits = num_splits;
+    a.cu_splits = cu_splits;
+    a.work_session = work_session;
+    a.work_split = work_split;
+    a.info = info;
+    a.pages = static_cast<const uint16_t*>(pages);
+    a.q_latent = static_cast<const uint16_t*>(q_latent);
+    a.q_rope = static_cast<const uint16_t*>(q_rope);
+    a.out = out;
+    a.lse = lse;
+    a.part_o = const_cast<float*>(ws);
+    a.part_ml = const_cast<float*>(ws) + (size_t)max_work * n_heads * kv_rank;
+    // The MFMA kernel issues 16-byte loads of q and of cache rows.
+    const bool aligned = ((reinterpret_cast<uintptr_t>(pages) | reinterpret_cast<uintptr_t>(q_latent) |
+                           reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out) |
+                           reinterpret_cast<uintptr_t>(workspace)) & 15) == 0;
+    const bool generic = (flags & MLA_DECODE_FORCE_GENERIC) || !aligned;
+    return gpu_status(launch_decode(a, dtype, generic, static_cast<hipStream_t>(stream)),
+                      "mla_decode_attention");
+}
+
+}  // extern "C"

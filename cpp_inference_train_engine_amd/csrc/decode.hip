@@ -1,0 +1,417 @@
+// (c) Absorbed MLA decode attention over the paged latent cache, gfx950.
+//
+// Math (src/infer/inference.cpp:116-153; mps_backend.mm:556-572), per session
+// b with one query row and per head h:
+//     s_i   = (q_latent[h] . c_i + q_rope[h] . k_i) * scale,   i < k_len
+//     out_h = sum_i softmax(s)_i c_i,      lse_h = ln sum_i exp(s_i)
+//
+// Work decomposition: the metadata's work items (session, split) each cover
+// `split` pages of one session (split-K).  Every item produces the online-
+// softmax state (m, l, o) of its pages; sessions with one item write the
+// final row directly, the rest are combined by merge_kernel (log-sum-exp).
+//
+// decode_mfma_kernel -- one wave per work item, pages of 64 tokens:
+//   S^T[tok][head] = K[tok][:] . Q^T  on v_mfma_f32_16x16x32 (latent) and
+//   16x16x16 (rope): the cache tile is the A operand straight from HBM (each
+//   lane loads 16 contiguous bytes of one token row) and Q^T (heads padded to
+//   16) is the B operand held in registers for the whole item.  The S^T
+//   output layout puts, in lane (g, n), head n and tokens 16t+4g+{0..3}: for a
+//   32-token block those 8 probabilities are exactly the lane's B operand of
+//   O^T = C^T . P^T, so P never leaves registers.  Only C^T needs a transpose:
+//   the already-loaded latent rows are written to LDS (32 tokens at a time) and
+//   read back column-wise.  Online softmax runs in the log2 domain with
+//   cross-lane max/sum over the 4 lanes that share a head (xor 16, 32).
+// decode_generic_kernel -- any H / kv_rank / rope / page size: one 256-thread
+//   block per (work item, head), VALU fp32.
+#include "mla_common.hpp"
+#include "mla_internal.hpp"
+
+#include <cmath>
+
+namespace mla {
+namespace {
+
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------- MFMA ----
+template <typename T, int KV, int RP, int PS>
+__global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeArgs a) {
+    static_assert(KV % 32 == 0 && RP % 16 == 0 && PS % 32 == 0, "tile shape");
+    constexpr int TILES = PS / 16;  // 16-token tiles per page
+    constexpr int KS = KV / 32;     // latent K-steps of S^T
+    constexpr int RS = RP / 16;     // rope K-steps of S^T
+    constexpr int RT = KV / 16;     // 16-row tiles of O^T
+    constexpr int STRIDE = KV + 4;  // LDS row pitch in 16-bit words (bank spread)
+    using V8 = typename T::vec8;
+    using V4 = typename T::vec4;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[32 * STRIDE];
+
+    const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+    const int W = a.info[0];
+    if (W <= 0)
+        return;
+    const int split = a.info[1];
+    const long long rec = (long long)PS * (KV + RP);
+    for (int w = blockIdx.x; w < W; w += gridDim.x) {
+        const int s = a.work_session[w], sp = a.work_split[w];
+        const int row = a.cu_q[s];
+        if (a.cu_q[s + 1] - row != 1)
+            continue;
+        const int kl = a.cu_k[s + 1] - a.cu_k[s];
+        const int need = (kl + PS - 1) / PS;
+        const int p_begin = sp * split;
+        const int p_end = min(need, p_begin + split);
+
+        // Q^T operands (B of S^T): lane (g, n) = head n, latent k 32j+8g.., rope 16k+4g..
+        V8 bq[KS];
+        V4 bqr[RS];
+        const bool head_ok = n < a.H;
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+            u32x4 v = {0, 0, 0, 0};
+            if (head_ok)
+                v = *reinterpret_cast<const u32x4*>(a.q_latent + ((long long)row * a.H + n) * KV +
+                                                    32 * j + 8 * g);
+            bq[j] = __builtin_bit_cast(V8, v);
+        }
+#pragma unroll
+        for (int k = 0; k < RS; ++k) {
+            u32x2 v = {0, 0};
+            if (head_ok)
+                v = *reinterpret_cast<const u32x2*>(a.q_rope + ((long long)row * a.H + n) * RP +
+                                                    16 * k + 4 * g);
+            bqr[k] = __builtin_bit_cast(V4, v);
+        }
+
+        float m_run = -INFINITY, l_run = 0.0f;
+        floatx4 acc[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+            acc[r] = floatx4{0, 0, 0, 0};
+
+        for (int p = p_begin; p < p_end; ++p) {
+            const int page = a.page_table[(long long)s * a.max_pages + p];
+            const bool page_ok = (unsigned)page < (unsigned)a.num_pool_pages;
+            const uint16_t* base = a.pages + (page_ok ? page : 0) * rec;
+            const int tok0 = p * PS;
+            // A operands of S^T straight from HBM: token 16t+n, 16 bytes per K-step.
+            u32x4 lat[TILES][KS];
+            u32x2 rop[TILES][RS];
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) {
+                const int r = 16 * t + n;
+                const bool ok = page_ok && tok0 + r < kl;
+#pragma unroll
+                for (int j = 0; j < KS; ++j)
+                    lat[t][j] = ok ? *reinterpret_cast<const u32x4*>(base + r * KV + 32 * j + 8 * g)
+                                   : u32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int k = 0; k < RS; ++k)
+                    rop[t][k] = ok ? *reinterpret_cast<const u32x2*>(base + PS * KV + r * RP +
+                                                                     16 * k + 4 * g)
+                                   : u32x2{0, 0};
+            }
+            // Scores S^T[16t + 4g + i][head n].
+            floatx4 sc[TILES];
+#pragma unroll
+            for (int t = 0; t < TILES; ++t) {
+                floatx4 c = {0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < KS; ++j)
+                    c = T::mma32(__builtin_bit_cast(V8, lat[t][j]), bq[j], c);
+#pragma unroll
+                for (int k = 0; k < RS; ++k)
+                    c = T::mma16(__builtin_bit_cast(V4, rop[t][k]), bqr[k], c);
+                sc[t] = c;
+            }
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < TILES; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tok = tok0 + 16 * t + 4 * g + i;
+                    const float x = (page_ok && tok < kl) ? sc[t][i] * a.scale_log2 : -INFINITY;
+                    sc[t][i] = x;
+                    mloc = fmaxf(mloc, x);
+                }
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m_run - m_new);
+            float psum = 0.0f;
+#pragma unroll
+            for (int t = 0; t < TILES; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float e = m_new == -INFINITY ? 0.0f : exp2_fast(sc[t][i] - m_new);
+                    sc[t][i] = e;
+                    psum += e;
+                }
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+                acc[r] *= alpha;
+            // O^T += C^T . P^T, 32 tokens (tiles 2kb, 2kb+1) per MFMA K-block.
+#pragma unroll
+            for (int kb = 0; kb < TILES / 2; ++kb) {
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int j = 0; j < KS; ++j) {
+                        uint16_t* dst = lds + (16 * tt + n) * STRIDE + 32 * j + 8 * g;
+                        const u32x4 v = lat[2 * kb + tt][j];
+                        *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
+                        *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
+                    }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                V8 pb;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pb[i] = static_cast<typename T::scalar>(sc[2 * kb][i]);
+                    pb[4 + i] = static_cast<typename T::scalar>(sc[2 * kb + 1][i]);
+                }
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    V8 ac;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        ac[i] = __builtin_bit_cast(typename T::scalar,
+                                                   lds[(4 * g + i) * STRIDE + 16 * rt + n]);
+                        ac[4 + i] = __builtin_bit_cast(typename T::scalar,
+                                                       lds[(16 + 4 * g + i) * STRIDE + 16 * rt + n]);
+                    }
+                    acc[rt] = T::mma32(ac, pb, acc[rt]);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+        }
+        l_run += __shfl_xor(l_run, 16, 64);
+        l_run += __shfl_xor(l_run, 32, 64);
+        if (!head_ok)
+            continue;
+        // Lane (g, n) holds O^T[16rt + 4g + i][head n].
+        if (a.num_splits[s] == 1) {
+            const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+            float* o = a.out + ((long long)row * a.H + n) * KV;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt] * inv;
+            if (a.lse && g == 0)
+                a.lse[(long long)row * a.H + n] = (m_run + __log2f(l_run)) * kLn2;
+        } else {
+            float* o = a.part_o + ((long long)w * a.H + n) * KV;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt];
+            if (g == 0) {
+                a.part_ml[((long long)w * a.H + n) * 2] = m_run;
+                a.part_ml[((long long)w * a.H + n) * 2 + 1] = l_run;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------- generic ----
+constexpr int kGenThreads = 256;
+constexpr int kGenChunk = 1024;   // tokens scored per LDS pass
+constexpr int kGenMaxAcc = 4;     // kv_rank <= 4 * 256
+
+__device__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0)
+        red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int i = 1; i < kGenThreads / 64; ++i)
+        r = fmaxf(r, red[i]);
+    __syncthreads();
+    return r;
+}
+__device__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0)
+        red[wave] = v;
+    __syncthreads();
+    float r = 0.0f;
+    for (int i = 0; i < kGenThreads / 64; ++i)
+        r += red[i];
+    __syncthreads();
+    return r;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs a) {
+    extern __shared__ float smem[];
+    float* qs = smem;                         // kv_rank + rope_dim
+    float* sc = smem + a.kv_rank + a.rope_dim;  // kGenChunk
+    float* red = sc + kGenChunk;              // 4
+    const int tid = threadIdx.x, h = blockIdx.y;
+    const int W = a.info[0];
+    if (W <= 0)
+        return;
+    const int split = a.info[1];
+    const int KV = a.kv_rank, RP = a.rope_dim, PS = a.page_size;
+    const long long rec = (long long)PS * (KV + RP);
+    for (int w = blockIdx.x; w < W; w += gridDim.x) {
+        const int s = a.work_session[w], sp = a.work_split[w];
+        const int row = a.cu_q[s];
+        if (a.cu_q[s + 1] - row != 1)
+            continue;
+        const int kl = a.cu_k[s + 1] - a.cu_k[s];
+        const int need = (kl + PS - 1) / PS;
+        const int p_begin = sp * split, p_end = min(need, p_begin + split);
+        const int t_begin = p_begin * PS, t_end = min(kl, p_end * PS);
+        for (int i = tid; i < KV + RP; i += kGenThreads)
+            qs[i] = i < KV ? T::to_float(a.q_latent[((long long)row * a.H + h) * KV + i])
+                           : T::to_float(a.q_rope[((long long)row * a.H + h) * RP + i - KV]);
+        __syncthreads();
+        float m_run = -INFINITY, l_run = 0.0f, acc[kGenMaxAcc] = {0, 0, 0, 0};
+        for (int c0 = t_begin; c0 < t_end; c0 += kGenChunk) {
+            const int cn = min(kGenChunk, t_end - c0);
+            float lmax = -INFINITY;
+            for (int t = tid; t < cn; t += kGenThreads) {
+                const int tok = c0 + t;
+                const int page = a.page_table[(long long)s * a.max_pages + tok / PS];
+                float x = -INFINITY;
+                if ((unsigned)page < (unsigned)a.num_pool_pages) {
+                    const uint16_t* base = a.pages + page * rec;
+                    const uint16_t* c = base + (long long)(tok % PS) * KV;
+                    const uint16_t* k = base + (long long)PS * KV + (long long)(tok % PS) * RP;
+                    float d = 0.0f, dr = 0.0f;
+                    for (int r = 0; r < KV; ++r)
+                        d += T::to_float(c[r]) * qs[r];
+                    for (int j = 0; j < RP; ++j)
+                        dr += T::to_float(k[j]) * qs[KV + j];
+                    x = (dr + d) * a.scale_log2;
+                }
+                sc[t] = x;
+                lmax = fmaxf(lmax, x);
+            }
+            const float cmax = block_max(lmax, red);
+            const float m_new = fmaxf(m_run, cmax);
+            const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m_run - m_new);
+            float lsum = 0.0f;
+            for (int t = tid; t < cn; t += kGenThreads) {
+                const float e = m_new == -INFINITY ? 0.0f : exp2_fast(sc[t] - m_new);
+                sc[t] = e;
+                lsum += e;
+            }
+            const float csum = block_sum(lsum, red);  // also orders the sc[] writes
+            l_run = l_run * alpha + csum;
+            m_run = m_new;
+            for (int k = 0; k < kGenMaxAcc; ++k) {
+                const int r = tid + k * kGenThreads;
+                if (r >= KV)
+                    break;
+                float v = acc[k] * alpha;
+                for (int t = 0; t < cn; ++t) {
+                    const int tok = c0 + t;
+                    const int page = a.page_table[(long long)s * a.max_pages + tok / PS];
+                    if ((unsigned)page < (unsigned)a.num_pool_pages && sc[t] != 0.0f)
+                        v += sc[t] * T::to_float(a.pages[page * rec + (long long)(tok % PS) * KV + r]);
+                }
+                acc[k] = v;
+            }
+            __syncthreads();
+        }
+        if (a.num_splits[s] == 1) {
+            const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+            for (int k = 0; k < kGenMaxAcc; ++k) {
+                const int r = tid + k * kGenThreads;
+                if (r < KV)
+                    a.out[((long long)row * a.H + h) * KV + r] = acc[k] * inv;
+            }
+            if (a.lse && tid == 0)
+                a.lse[(long long)row * a.H + h] = (m_run + __log2f(l_run)) * kLn2;
+        } else {
+            for (int k = 0; k < kGenMaxAcc; ++k) {
+                const int r = tid + k * kGenThreads;
+                if (r < KV)
+                    a.part_o[((long long)w * a.H + h) * KV + r] = acc[k];
+            }
+            if (tid == 0) {
+                a.part_ml[((long long)w * a.H + h) * 2] = m_run;
+                a.part_ml[((long long)w * a.H + h) * 2 + 1] = l_run;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// --------------------------------------------------------------- merge ----
+// Log-sum-exp combine of a session's split partials (log2 domain).
+__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+    const int W = a.info[0];
+    if (W <= 0)
+        return;
+    for (int s = blockIdx.x; s < a.B; s += gridDim.x) {
+        const int row = a.cu_q[s];
+        const int ns = a.num_splits[s];
+        if (a.cu_q[s + 1] - row != 1 || ns <= 1)
+            continue;
+        const int w0 = a.cu_splits[s];
+        for (int e = threadIdx.x; e < a.H * a.kv_rank; e += 256) {
+            const int h = e / a.kv_rank, r = e % a.kv_rank;
+            float m = -INFINITY;
+            for (int i = 0; i < ns; ++i)
+                m = fmaxf(m, a.part_ml[((long long)(w0 + i) * a.H + h) * 2]);
+            float l = 0.0f, o = 0.0f;
+            for (int i = 0; i < ns; ++i) {
+                const long long idx = (long long)(w0 + i) * a.H + h;
+                const float f = m == -INFINITY ? 0.0f : exp2_fast(a.part_ml[idx * 2] - m);
+                l += f * a.part_ml[idx * 2 + 1];
+                o += f * a.part_o[idx * a.kv_rank + r];
+            }
+            a.out[((long long)row * a.H + h) * a.kv_rank + r] = l > 0.0f ? o / l : 0.0f;
+            if (a.lse && r == 0)
+                a.lse[(long long)row * a.H + h] = (m + __log2f(l)) * kLn2;
+        }
+    }
+}
+
+template <typename T>
+hipError_t launch_mfma(const DecodeArgs& a, int grid, hipStream_t stream) {
+    if (a.kv_rank == 128 && a.rope_dim == 16 && a.page_size == 64)
+        hipLaunchKernelGGL((decode_mfma_kernel<T, 128, 16, 64>), dim3(grid), dim3(64), 0, stream, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool decode_mfma_supported(int H, int kv_rank, int rope_dim, int page_size) {
+    return H <= 16 && page_size == 64 && kv_rank == 128 && rope_dim == 16;
+}
+
+hipError_t launch_decode(const DecodeArgs& a, int dtype, bool force_generic, hipStream_t stream) {
+    if (a.max_work <= 0 || a.B <= 0)
+        return hipSuccess;
+    const int grid = a.max_work < 65535 ? a.max_work : 65535;
+    hipError_t err;
+    if (!force_generic && decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size)) {
+        err = dtype == 0 ? launch_mfma<F16>(a, grid, stream) : launch_mfma<BF16>(a, grid, stream);
+    } else {
+        const size_t shmem = (a.kv_rank + a.rope_dim + kGenChunk + 8) * sizeof(float);
+        const dim3 g(grid, a.H);
+        if (dtype == 0)
+            hipLaunchKernelGGL(decode_generic_kernel<F16>, g, dim3(kGenThreads), shmem, stream, a);
+        else
+            hipLaunchKernelGGL(decode_generic_kernel<BF16>, g, dim3(kGenThreads), shmem, stream, a);
+        err = hipGetLastError();
+    }
+    if (err != hipSuccess)
+        return err;
+    const int mgrid = a.B < 4096 ? a.B : 4096;
+    hipLaunchKernelGGL(merge_kernel, dim3(mgrid), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace mla

@@ -1,0 +1,233 @@
+// (a) Ragged-batch metadata and (b) paged latent append, gfx950.
+//
+// The metadata build runs as ONE workgroup of 1024 threads: batches are at
+// most a few thousand sessions, so a single-block scan beats a multi-kernel
+// device-wide scan (no inter-block traffic, one launch).  All arithmetic is
+// int32/int64 and bit-exact with the CPU builder in the oracle.
+#include "mla_common.hpp"
+#include "mla_internal.hpp"
+
+#include <climits>
+
+namespace mla {
+namespace {
+
+constexpr int kMetaThreads = 1024;
+constexpr int kMetaWaves = kMetaThreads / 64;
+
+// Inclusive block scan of three int64 values; returns the chunk totals in tot[].
+__device__ void block_scan3(long long v[3], long long tot[3], long long* lds) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+        for (int off = 1; off < 64; off <<= 1) {
+            const long long up = __shfl_up(v[k], off, 64);
+            if (lane >= off)
+                v[k] += up;
+        }
+    if (lane == 63)
+        for (int k = 0; k < 3; ++k)
+            lds[k * kMetaWaves + wave] = v[k];
+    __syncthreads();
+    if (wave == 0) {
+        for (int k = 0; k < 3; ++k) {
+            long long x = lane < kMetaWaves ? lds[k * kMetaWaves + lane] : 0;
+            for (int off = 1; off < kMetaWaves; off <<= 1) {
+                const long long up = __shfl_up(x, off, 64);
+                if (lane >= off)
+                    x += up;
+            }
+            if (lane < kMetaWaves)
+                lds[k * kMetaWaves + lane] = x;
+        }
+    }
+    __syncthreads();
+    for (int k = 0; k < 3; ++k) {
+        if (wave > 0)
+            v[k] += lds[k * kMetaWaves + wave - 1];
+        tot[k] = lds[k * kMetaWaves + kMetaWaves - 1];
+    }
+    __syncthreads();
+}
+
+// Largest b in [0, n] with a[b] <= x  (a non-decreasing, a[0] <= x).
+__device__ int upper_index(const int32_t* a, int n, long long x) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a[mid] <= x)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataArgs a) {
+    __shared__ long long lds[3 * kMetaWaves];
+    __shared__ long long carry[3];
+    __shared__ int err;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        carry[0] = carry[1] = carry[2] = 0;
+        err = INT_MAX;
+        a.cu_seqlens_q[0] = 0;
+        a.cu_seqlens_k[0] = 0;
+        a.cu_splits[0] = 0;
+    }
+    __syncthreads();
+    // Phase 1: cu_seqlens_q/k, validation, total pages of sessions with queries.
+    for (int base = 0; base < a.B; base += kMetaThreads) {
+        const int b = base + tid;
+        long long v[3] = {0, 0, 0}, tot[3];
+        int bad = 0;
+        if (b < a.B) {
+            const long long q = a.q_len[b], ctx = a.ctx_len[b];
+            const long long npages = (long long)a.cu_pages[b + 1] - a.cu_pages[b];
+            const long long kl = ctx + q;
+            const long long need = (kl + a.page_size - 1) / a.page_size;
+            bad = q < 0 || ctx < 0 || npages < 0 || npages > a.max_pages || need > npages;
+            for (long long j = 0; !bad && j < npages; ++j) {
+                const int32_t pid = a.page_ids[a.cu_pages[b] + j];
+                bad = pid < 0 || pid >= a.num_pool_pages;
+            }
+            v[0] = q;
+            v[1] = kl;
+            v[2] = q > 0 ? need : 0;
+        }
+        block_scan3(v, tot, lds);
+        if (b < a.B) {
+            const long long iq = v[0] + carry[0], ik = v[1] + carry[1];
+            if (bad || iq > INT_MAX || ik > INT_MAX || iq > a.max_rows)
+                atomicMin(&err, b);
+            a.cu_seqlens_q[b + 1] = (int32_t)iq;
+            a.cu_seqlens_k[b + 1] = (int32_t)ik;
+        }
+        __syncthreads();
+        if (tid == 0)
+            for (int k = 0; k < 3; ++k)
+                carry[k] += tot[k];
+        __syncthreads();
+    }
+    if (err != INT_MAX) {
+        if (tid == 0) {
+            a.info[0] = -1;
+            a.info[1] = err;
+            a.info[2] = 0;
+            a.info[3] = 0;
+        }
+        return;
+    }
+    const long long total_q = carry[0], total_k = carry[1], total_pages = carry[2];
+    long long split = a.split_pages;
+    if (split == 0) {
+        split = (total_pages + a.target_blocks - 1) / a.target_blocks;
+        if (split < 1)
+            split = 1;
+    }
+    __syncthreads();
+    if (tid == 0)
+        carry[0] = 0;
+    __syncthreads();
+    // Phase 2: split-K work items per session.
+    for (int base = 0; base < a.B; base += kMetaThreads) {
+        const int b = base + tid;
+        long long v[3] = {0, 0, 0}, tot[3];
+        if (b < a.B && a.q_len[b] > 0) {
+            const long long kl = (long long)a.ctx_len[b] + a.q_len[b];
+            const long long need = (kl + a.page_size - 1) / a.page_size;
+            v[0] = (need + split - 1) / split;
+        }
+        const long long ns = v[0];
+        block_scan3(v, tot, lds);
+        if (b < a.B) {
+            const long long w = v[0] + carry[0];
+            if (w > a.max_work)
+                atomicMin(&err, b);
+            a.num_splits[b] = (int32_t)ns;
+            a.cu_splits[b + 1] = (int32_t)w;
+        }
+        __syncthreads();
+        if (tid == 0)
+            carry[0] += tot[0];
+        __syncthreads();
+    }
+    if (err != INT_MAX) {
+        if (tid == 0) {
+            a.info[0] = -1;
+            a.info[1] = err;
+            a.info[2] = 0;
+            a.info[3] = 0;
+        }
+        return;
+    }
+    const long long W = carry[0];
+    // Phase 3: block-to-session map, padded page table, slot mapping.
+    for (long long w = tid; w < W; w += kMetaThreads) {
+        const int b = upper_index(a.cu_splits, a.B, w);
+        a.work_session[w] = b;
+        a.work_split[w] = (int32_t)(w - a.cu_splits[b]);
+    }
+    const long long entries = (long long)a.B * a.max_pages;
+    for (long long e = tid; e < entries; e += kMetaThreads) {
+        const int b = (int)(e / a.max_pages), j = (int)(e % a.max_pages);
+        const int npages = a.cu_pages[b + 1] - a.cu_pages[b];
+        a.page_table[e] = j < npages ? a.page_ids[a.cu_pages[b] + j] : -1;
+    }
+    for (long long i = tid; i < total_q; i += kMetaThreads) {
+        const int b = upper_index(a.cu_seqlens_q, a.B, i);
+        const long long pos = (long long)a.ctx_len[b] + (i - a.cu_seqlens_q[b]);
+        const int32_t page = a.page_ids[a.cu_pages[b] + pos / a.page_size];
+        a.slot_mapping[i] = (int32_t)(page * (long long)a.page_size + pos % a.page_size);
+    }
+    if (tid == 0) {
+        a.info[0] = (int32_t)W;
+        a.info[1] = (int32_t)split;
+        a.info[2] = (int32_t)total_q;
+        a.info[3] = (int32_t)total_k;
+    }
+}
+
+// One thread per element of the appended rows; RNE rounding to 16 bits.
+template <typename T>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+    const int width = a.kv_rank + a.rope_dim;
+    const long long total = (long long)a.T * width;
+    const long long rec = (long long)a.page_size * width;
+    for (long long e = blockIdx.x * 256LL + threadIdx.x; e < total; e += 256LL * gridDim.x) {
+        const int t = (int)(e / width), c = (int)(e % width);
+        const int slot = a.slot_mapping[t];
+        const int page = slot / a.page_size, off = slot % a.page_size;
+        if (slot < 0 || page >= a.num_pool_pages)
+            continue;
+        uint16_t* base = a.pages + page * rec;
+        if (c < a.kv_rank)
+            base[(long long)off * a.kv_rank + c] = T::from_float(a.ckv[(long long)t * a.kv_rank + c]);
+        else {
+            const int j = c - a.kv_rank;
+            base[(long long)a.page_size * a.kv_rank + (long long)off * a.rope_dim + j] =
+                T::from_float(a.krope[(long long)t * a.rope_dim + j]);
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(build_metadata_kernel, dim3(1), dim3(kMetaThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_append(const AppendArgs& a, int dtype, hipStream_t stream) {
+    const long long total = (long long)a.T * (a.kv_rank + a.rope_dim);
+    if (total == 0)
+        return hipSuccess;
+    const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+    if (dtype == 0)
+        hipLaunchKernelGGL(append_kernel<F16>, dim3(blocks), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(append_kernel<BF16>, dim3(blocks), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace mla

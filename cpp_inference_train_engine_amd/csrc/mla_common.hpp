@@ -1,0 +1,77 @@
+// Shared device helpers for the gfx950 MLA kernels: 16-bit element types,
+// MFMA operand vectors, RNE conversions and wave reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mla {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element-type traits: 16-bit storage dtype code 0 = fp16, 1 = bf16 (the cache
+// stores raw 16-bit words; the tag picks the MFMA flavour and conversions).
+struct F16 {
+    using scalar = _Float16;
+    using vec8 = half8;
+    using vec4 = half4;
+    static constexpr int code = 0;
+    __device__ static float to_float(uint16_t bits) {
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    }
+    __device__ static uint16_t from_float(float x) {  // IEEE RNE (v_cvt_f16_f32)
+        return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+    }
+    __device__ static floatx4 mma32(vec8 a, vec8 b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    __device__ static floatx4 mma16(vec4 a, vec4 b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+struct BF16 {
+    using scalar = __bf16;
+    using vec8 = bf8;
+    using vec4 = bf4;
+    static constexpr int code = 1;
+    __device__ static float to_float(uint16_t bits) {
+        return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
+    }
+    __device__ static uint16_t from_float(float x) {  // RNE, quiet NaN
+        uint32_t u = __builtin_bit_cast(uint32_t, x);
+        if ((u & 0x7fffffffu) > 0x7f800000u)
+            return static_cast<uint16_t>((u >> 16) | 0x40u);
+        u += 0x7fffu + ((u >> 16) & 1u);
+        return static_cast<uint16_t>(u >> 16);
+    }
+    __device__ static floatx4 mma32(vec8 a, vec8 b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static floatx4 mma16(vec4 a, vec4 b, floatx4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
+};
+
+__device__ inline float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1)
+        v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ inline float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1)
+        v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace mla

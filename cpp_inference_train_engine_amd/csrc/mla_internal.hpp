@@ -1,0 +1,45 @@
+// Kernel argument blocks and launchers shared between the .hip translation
+// units and the C ABI (capi.hip).  Host-visible, no device code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace mla {
+
+struct MetadataArgs {
+    int B;
+    const int32_t *ctx_len, *q_len, *cu_pages, *page_ids;
+    int page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows;
+    int32_t *cu_seqlens_q, *cu_seqlens_k, *page_table, *slot_mapping, *num_splits, *cu_splits,
+        *work_session, *work_split, *info;
+};
+
+struct AppendArgs {
+    int T, kv_rank, rope_dim, page_size, num_pool_pages;
+    const float *ckv, *krope;
+    const int32_t* slot_mapping;
+    uint16_t* pages;
+};
+
+// Absorbed decode attention.  Partials live in the workspace:
+//   part_o [max_work][H][kv_rank] fp32 (unnormalised), part_ml [max_work][H][2]
+//   (running max in log2 units, running denominator).
+struct DecodeArgs {
+    int B, H, kv_rank, rope_dim, page_size, max_pages, num_pool_pages, max_work;
+    float scale_log2;  // softmax scale * log2(e)
+    const int32_t *cu_q, *cu_k, *page_table, *num_splits, *cu_splits, *work_session,
+        *work_split, *info;
+    const uint16_t *pages, *q_latent, *q_rope;
+    float *out, *lse, *part_o, *part_ml;
+};
+
+hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
+hipError_t launch_append(const AppendArgs& a, int dtype, hipStream_t stream);
+// Returns hipErrorNotSupported-free status; picks MFMA or generic kernels.
+hipError_t launch_decode(const DecodeArgs& a, int dtype, bool force_generic, hipStream_t stream);
+bool decode_mfma_supported(int H, int kv_rank, int rope_dim, int page_size);
+
+}  // namespace mla

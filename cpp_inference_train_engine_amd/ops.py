@@ -1,0 +1,146 @@
+"""Operator interface over the C ABI for the paged, ragged MLA decode path.
+
+Mirrors the three subsystems of the path:
+  (a) ``build_metadata``   -> ``mla_build_metadata``   (GPU ragged-batch metadata)
+  (b) ``append_latent``    -> ``mla_append_latent``    (paged latent/rope append)
+  (c) ``decode_attention`` -> ``mla_decode_attention`` (absorbed split-K decode)
+All tensors are torch CUDA (HIP) tensors; calls are stream-ordered on the
+current torch stream unless ``stream`` is given.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from . import DTYPE_BF16, DTYPE_F16, check, lib, ptr, stream_handle
+
+
+def _torch():
+    import torch
+    return torch
+
+
+@dataclass
+class RaggedBatch:
+    """Device metadata of one continuous-batching step (all int32 tensors)."""
+
+    B: int
+    page_size: int
+    max_pages: int
+    num_pool_pages: int
+    max_work: int
+    max_rows: int
+    cu_seqlens_q: object
+    cu_seqlens_k: object
+    page_table: object
+    slot_mapping: object
+    num_splits: object
+    cu_splits: object
+    work_session: object
+    work_split: object
+    info: object
+    host_info: list = field(default_factory=list)
+
+    def read_info(self, stream=None):
+        """Synchronise and return [W, split, total_q, total_k]; raises on a bad batch."""
+        import numpy as np
+        h = np.zeros(4, np.int32)
+        check(lib().mla_read_metadata_info(stream_handle(stream), ptr(self.info), h.ctypes.data))
+        self.host_info = h.tolist()
+        return self.host_info
+
+
+def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size: int, max_pages: int,
+                   num_pool_pages: int, split_pages: int = 0, target_blocks: int = 1024,
+                   max_work: int | None = None, max_rows: int | None = None,
+                   stream=None) -> RaggedBatch:
+    """(a) Build cu_seqlens, padded page tables, slot mapping and the block-to-session
+    map on the GPU (one launch).  Inputs are device int32 tensors."""
+    torch = _torch()
+    dev = ctx_len.device
+    B = int(ctx_len.numel())
+    if max_rows is None:
+        max_rows = max(1, 4 * B)
+    if max_work is None:
+        max_work = max(1, target_blocks + 2 * B)
+    i32 = dict(dtype=torch.int32, device=dev)
+    rb = RaggedBatch(
+        B=B, page_size=page_size, max_pages=max_pages, num_pool_pages=num_pool_pages,
+        max_work=max_work, max_rows=max_rows,
+        cu_seqlens_q=torch.empty(B + 1, **i32), cu_seqlens_k=torch.empty(B + 1, **i32),
+        page_table=torch.empty(max(1, B * max_pages), **i32),
+        slot_mapping=torch.empty(max_rows, **i32), num_splits=torch.empty(max(B, 1), **i32),
+        cu_splits=torch.empty(B + 1, **i32), work_session=torch.empty(max_work, **i32),
+        work_split=torch.empty(max_work, **i32), info=torch.empty(4, **i32))
+    check(lib().mla_build_metadata(
+        stream_handle(stream), B, ptr(ctx_len), ptr(q_len), ptr(cu_pages), ptr(page_ids),
+        page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows,
+        ptr(rb.cu_seqlens_q), ptr(rb.cu_seqlens_k), ptr(rb.page_table), ptr(rb.slot_mapping),
+        ptr(rb.num_splits), ptr(rb.cu_splits), ptr(rb.work_session), ptr(rb.work_split),
+        ptr(rb.info)))
+    return rb
+
+
+class PagedLatentCache:
+    """Device page pool: [layers, pages, page_size * (kv_rank + rope_dim)] 16-bit words.
+    Each page record is latent [page_size][kv_rank] followed by rope [page_size][rope_dim]."""
+
+    def __init__(self, n_layers: int, num_pages: int, page_size: int, kv_rank: int,
+                 rope_dim: int, dtype: int = DTYPE_F16, device="cuda", storage=None):
+        torch = _torch()
+        self.n_layers, self.num_pages, self.page_size = n_layers, num_pages, page_size
+        self.kv_rank, self.rope_dim, self.dtype = kv_rank, rope_dim, dtype
+        tdt = torch.float16 if dtype == DTYPE_F16 else torch.bfloat16
+        rec = page_size * (kv_rank + rope_dim)
+        if storage is None:
+            storage = torch.zeros((n_layers, num_pages, rec), dtype=tdt, device=device)
+        assert storage.shape == (n_layers, num_pages, rec) and storage.dtype == tdt
+        self.pages = storage
+
+    def layer(self, l: int):
+        return self.pages[l]
+
+    @property
+    def record_words(self) -> int:
+        return self.page_size * (self.kv_rank + self.rope_dim)
+
+
+def append_latent(cache: PagedLatentCache, layer: int, ckv, krope, slot_mapping,
+                  stream=None) -> None:
+    """(b) Round ckv [T x kv_rank] / krope [T x rope_dim] (fp32) to the cache dtype and
+    write row t to flat slot slot_mapping[t] of ``layer``'s page pool."""
+    T = int(ckv.shape[0])
+    assert ckv.is_contiguous() and krope.is_contiguous()
+    check(lib().mla_append_latent(stream_handle(stream), T, cache.kv_rank, cache.rope_dim,
+                                  cache.page_size, cache.dtype, ptr(ckv), ptr(krope),
+                                  ptr(slot_mapping), cache.num_pages, ptr(cache.layer(layer))))
+
+
+def decode_workspace_bytes(max_work: int, n_heads: int, kv_rank: int) -> int:
+    return int(lib().mla_decode_workspace_bytes(max_work, n_heads, kv_rank))
+
+
+def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
+                     kv_rank: int, rope_dim: int, dtype: int = DTYPE_F16, out=None, lse=None,
+                     workspace=None, flags: int = 0, stream=None):
+    """(c) Absorbed MLA decode attention for every session with one query row.
+    q_latent [rows, H, kv_rank], q_rope [rows, H, rope_dim] in the cache dtype;
+    returns out [rows, H, kv_rank] fp32 (and fills lse [rows, H] if given)."""
+    torch = _torch()
+    rows, H = int(q_latent.shape[0]), int(q_latent.shape[1])
+    if out is None:
+        out = torch.zeros((rows, H, kv_rank), dtype=torch.float32, device=q_latent.device)
+    if workspace is None:
+        nbytes = decode_workspace_bytes(batch.max_work, H, kv_rank)
+        workspace = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q_latent.device)
+    check(lib().mla_decode_attention(
+        stream_handle(stream), batch.B, H, kv_rank, rope_dim, batch.page_size, dtype,
+        float(scale), ptr(batch.cu_seqlens_q), ptr(batch.cu_seqlens_k), ptr(batch.page_table),
+        batch.max_pages, batch.num_pool_pages, ptr(pages), ptr(q_latent), ptr(q_rope),
+        ptr(batch.num_splits), ptr(batch.cu_splits), ptr(batch.work_session),
+        ptr(batch.work_split), ptr(batch.info), batch.max_work, ptr(out), ptr(lse),
+        ptr(workspace), int(workspace.numel()), flags))
+    return out
+
+
+__all__ = ["RaggedBatch", "build_metadata", "PagedLatentCache", "append_latent",
+           "decode_workspace_bytes", "decode_attention", "DTYPE_F16", "DTYPE_BF16"]

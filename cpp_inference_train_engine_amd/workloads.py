@@ -1,0 +1,116 @@
+"""Synthetic ragged decode batches of the benchmark configurations.
+
+Session lengths and the physical page permutation follow the reference's Rng
+(SplitMix64, include/mini_mla/rng.hpp:9-28: ``bounded`` with rejection, Fisher-
+Yates shuffle), so the batch shape for a seed is the same on every host.  The
+bulk cache/query contents are N(0, 1) from numpy's PCG64 (seeded) and rounded
+once to the 16-bit cache dtype; both the GPU and any CPU checker consume the
+same rounded bits.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+M64 = (1 << 64) - 1
+
+
+class SplitMix64:
+    """Integer part of the reference Rng (rng.hpp:11-28)."""
+
+    def __init__(self, seed: int):
+        self.state = seed & M64
+
+    def next(self) -> int:
+        self.state = (self.state + 0x9E3779B97F4A7C15) & M64
+        z = self.state
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M64
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M64
+        return z ^ (z >> 31)
+
+    def bounded(self, bound: int) -> int:
+        if bound == 0:
+            return 0
+        threshold = ((1 << 64) - bound) % bound
+        while True:
+            r = self.next()
+            if r >= threshold:
+                return r % bound
+
+
+def to_bits(x: np.ndarray, dtype: int) -> np.ndarray:
+    """Round fp32 to 16-bit words (RNE) of dtype 0 = fp16, 1 = bf16."""
+    x = np.ascontiguousarray(x, np.float32)
+    if dtype == 0:
+        return x.astype(np.float16).view(np.uint16)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        r[nan] = ((x.view(np.uint32)[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+@dataclass
+class DecodeBatch:
+    """One ragged decode step: every session appends one token (q_len = 1)."""
+
+    ctx_len: np.ndarray   # int32 [B] tokens already cached
+    q_len: np.ndarray     # int32 [B]
+    cu_pages: np.ndarray  # int32 [B+1]
+    page_ids: np.ndarray  # int32 [sum pages]
+    num_pages: int        # pool size
+    max_pages: int
+    pages: np.ndarray     # uint16 [L, num_pages, page_size*(kv+rope)]
+    q_latent: np.ndarray  # uint16 [B, H, kv]
+    q_rope: np.ndarray    # uint16 [B, H, rope]
+    page_size: int
+    kv_rank: int
+    rope_dim: int
+    n_heads: int
+    dtype: int
+
+    @property
+    def k_len(self) -> np.ndarray:
+        return self.ctx_len + self.q_len
+
+    def cache_bytes_per_layer(self) -> int:
+        """Algorithmic bytes one decode-attention launch must read (one layer)."""
+        return int(self.k_len.sum()) * (self.kv_rank + self.rope_dim) * 2
+
+
+def ragged_decode_batch(B=64, min_len=128, max_len=4096, page_size=64, n_heads=8, kv_rank=128,
+                        rope_dim=16, n_layers=1, dtype=0, seed=0, spare_pages=0,
+                        lengths=None) -> DecodeBatch:
+    """Config-3-style batch: context lengths (after the append) uniform in
+    [min_len, max_len], pages of ``page_size`` tokens at a random permutation of the
+    pool, N(0,1) cache and query contents."""
+    rng = SplitMix64(seed)
+    if lengths is None:
+        k_len = np.array([min_len + rng.bounded(max_len - min_len + 1) for _ in range(B)],
+                         np.int64)
+    else:
+        k_len = np.asarray(lengths, np.int64)
+        B = k_len.size
+    need = (k_len + page_size - 1) // page_size
+    counts = need + spare_pages
+    P = int(counts.sum())
+    perm = list(range(P))
+    for i in range(P - 1, 0, -1):  # Fisher-Yates with the reference Rng
+        j = rng.bounded(i + 1)
+        perm[i], perm[j] = perm[j], perm[i]
+    page_ids = np.array(perm, np.int32)
+    cu_pages = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    gen = np.random.default_rng(seed)
+    rec = page_size * (kv_rank + rope_dim)
+    pages = np.empty((n_layers, P, rec), np.uint16)
+    for l in range(n_layers):
+        pages[l] = to_bits(gen.standard_normal((P, rec), dtype=np.float32), dtype)
+    q_latent = to_bits(gen.standard_normal((B, n_heads, kv_rank), dtype=np.float32), dtype)
+    q_rope = to_bits(gen.standard_normal((B, n_heads, rope_dim), dtype=np.float32), dtype)
+    return DecodeBatch(ctx_len=(k_len - 1).astype(np.int32), q_len=np.ones(B, np.int32),
+                       cu_pages=cu_pages, page_ids=page_ids, num_pages=P,
+                       max_pages=int(counts.max()), pages=pages, q_latent=q_latent,
+                       q_rope=q_rope, page_size=page_size, kv_rank=kv_rank, rope_dim=rope_dim,
+                       n_heads=n_heads, dtype=dtype)

@@ -1,0 +1,139 @@
+/*
+ * mla_hip.h -- C ABI of the MI355X (gfx950) MLA cached-decode backend.
+ *
+ * This is the drop-in boundary for the reference engine's inference backend
+ * (Astrowebdeving/cpp_inference_train_engine).  The reference's backend plugin
+ * interface is the C++ class `mini_mla::Execution`
+ * (include/mini_mla/execution.hpp:28-62) with the factory `make_execution`
+ * (execution.hpp:63-66, src/infer/inference.cpp:314-329) dispatching to
+ * `make_mps_execution` (execution.hpp:67-68, src/backends/mps_backend.mm:1943-1977).
+ * A C++ adapter (cpp_inference_train_engine_amd/host) implements that
+ * interface over these functions; other hosts bind them with ctypes / FFI.
+ *
+ * Conventions
+ *  - Every function returns an int status: MLA_OK or MLA_ERR_* (the reference
+ *    ErrorCode values of include/mini_mla/result.hpp:12-19, plus one).  The
+ *    message of the last failure on the calling thread is mla_last_error().
+ *  - Pointers named d_* / documented "device" are device (HBM) pointers;
+ *    `stream` is a hipStream_t (NULL = the default stream).  Work is
+ *    stream-ordered and asynchronous unless stated.
+ *  - Output buffers are owned by the caller.  No call is thread-safe against
+ *    another call on the same objects; distinct streams/objects may be used
+ *    from different threads (the reference's fork-per-thread rule,
+ *    docs/architecture.md:37).
+ *  - 16-bit element dtype codes: MLA_DTYPE_F16 (0), MLA_DTYPE_BF16 (1).
+ *
+ * Paged latent cache layout (one pool per layer): page p is one contiguous
+ * record of page_size * (kv_rank + rope_dim) 16-bit words:
+ *     latent [page_size][kv_rank]  then  rope key [page_size][rope_dim]
+ * Token position t of session b lives in page page_table[b][t / page_size],
+ * slot t % page_size.  The cache holds the kv_norm-ed latent and the RoPE-ed
+ * key exactly as the reference's CpuDecoder cache does
+ * (src/infer/inference.cpp:91-103), rounded once to 16 bits.
+ */
+#ifndef MLA_HIP_H
+#define MLA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLA_OK 0
+#define MLA_ERR_INVALID_ARGUMENT 1 /* ErrorCode::invalid_argument */
+#define MLA_ERR_IO 2               /* ErrorCode::io_error */
+#define MLA_ERR_UNSUPPORTED 3      /* ErrorCode::unsupported */
+#define MLA_ERR_OUT_OF_MEMORY 4    /* ErrorCode::out_of_memory */
+#define MLA_ERR_GPU 5              /* ErrorCode::gpu_error */
+#define MLA_ERR_NUMERICAL 6        /* ErrorCode::numerical_error */
+
+#define MLA_DTYPE_F16 0
+#define MLA_DTYPE_BF16 1
+
+/* Decode-attention flags. */
+#define MLA_DECODE_FORCE_GENERIC 1 /* use the portable VALU kernel even when the MFMA one fits */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mla_last_error(void);
+/* ABI version of this library. */
+int mla_abi_version(void);
+
+/* ------------------------------------------------------------------ (a)
+ * Ragged-batch metadata, built on the GPU in one launch.  No reference
+ * function: the reference keeps one contiguous cache per session
+ * (src/infer/inference.cpp:15-18).  Nearest precedent: the Gemma engine's
+ * per-row lengths/cursors/write slots (src/infer/gemma.cpp:383-427).
+ *
+ * Inputs (device): ctx_len[B] tokens already cached per session, q_len[B]
+ * tokens appended this step, cu_pages[B+1] + page_ids[] the per-session
+ * physical page lists.  Scalars: page_size, max_pages (columns of the padded
+ * table), num_pool_pages (valid page ids are [0, num_pool_pages)),
+ * split_pages (>0 fixed pages per work item; 0 = auto, ceil(total pages of
+ * sessions with q_len>0 / target_blocks)), max_work / max_rows capacities.
+ * Outputs (device): cu_seqlens_q[B+1], cu_seqlens_k[B+1],
+ * page_table[B * max_pages] (-1 padded), slot_mapping[max_rows] (flat slot
+ * page*page_size+offset of every appended token), num_splits[B],
+ * cu_splits[B+1], work_session[max_work], work_split[max_work] (the
+ * block-to-session map) and info[4]:
+ *     ok:    {W (work items), split_pages used, total_q, total_k}
+ *     error: {-1, first offending session, 0, 0}
+ * A session is invalid when q_len<0, ctx_len<0, it lists more than
+ * max_pages pages or fewer than ceil((ctx+q)/page_size), a page id is out of
+ * range, a running total exceeds INT32_MAX, or the work/row capacity is
+ * exceeded.  Errors are reported through info (read it with
+ * mla_read_metadata_info); every consumer kernel treats info[0] < 0 as an
+ * empty batch. */
+int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
+                       const int32_t* cu_pages, const int32_t* page_ids, int page_size,
+                       int max_pages, int num_pool_pages, int split_pages, int target_blocks,
+                       int max_work, int max_rows, int32_t* cu_seqlens_q,
+                       int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
+                       int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
+                       int32_t* work_split, int32_t* info);
+
+/* Synchronises `stream`, copies info[4] to host_info and returns
+ * MLA_ERR_INVALID_ARGUMENT (naming the session) if the build failed. */
+int mla_read_metadata_info(void* stream, const int32_t* info, int32_t* host_info);
+
+/* ------------------------------------------------------------------ (b)
+ * Paged latent append; refines the reference's contiguous append
+ * `latent_[l][pos,:] = c_kv; rope_[l][pos,:] = k_rope`
+ * (src/infer/inference.cpp:100-103; MPS scatter mps_backend.mm:542-555).
+ * Row t of ckv [T x kv_rank] and krope [T x rope_dim] (device fp32) is rounded
+ * (RNE, as to_half in src/core/io.cpp:152-158) and written to flat slot
+ * slot_mapping[t] of the pool `pages`.  Slots must lie inside the pool
+ * (num_pool_pages pages); out-of-range slots are skipped. */
+int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_size, int dtype,
+                      const float* ckv, const float* krope, const int32_t* slot_mapping,
+                      int num_pool_pages, void* pages);
+
+/* ------------------------------------------------------------------ (c)
+ * Absorbed MLA decode attention over the paged cache: the per-head loop of
+ * CpuDecoder::decode (src/infer/inference.cpp:116-153) and the MPS graph
+ * (mps_backend.mm:556-572), for every session with q_len == 1 in the batch:
+ *     s_i = (q_latent[h] . c_i + q_rope[h] . k_i) * scale,  i in [0, k_len)
+ *     out[h] = sum_i softmax(s)_i c_i           (fp32 accumulation)
+ *     lse[h] = ln(sum_i exp(s_i))
+ * q_latent [rows x H x kv_rank], q_rope [rows x H x rope_dim]: 16-bit of
+ * `dtype` (the MPS graph keeps q_latent in the storage dtype,
+ * mps_backend.mm:561).  out [rows x H x kv_rank] fp32, lse [rows x H] fp32
+ * (may be NULL).  Rows of sessions with q_len != 1 are not written.
+ * Work is split over the metadata's work items (split-K over pages) and
+ * merged with a log-sum-exp combine.  `workspace` (device) must hold
+ * mla_decode_workspace_bytes(max_work, H, kv_rank) bytes. */
+size_t mla_decode_workspace_bytes(int max_work, int n_heads, int kv_rank);
+int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
+                         int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_k, const int32_t* page_table, int max_pages,
+                         int num_pool_pages, const void* pages, const void* q_latent,
+                         const void* q_rope, const int32_t* num_splits, const int32_t* cu_splits,
+                         const int32_t* work_session, const int32_t* work_split,
+                         const int32_t* info, int max_work, float* out, float* lse,
+                         void* workspace, size_t workspace_bytes, int flags);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
