@@ -104,8 +104,7 @@ def main():
     new_kr = torch.randn((n_layers, B, 16), device="cuda", generator=g)
     max_work = args.target_blocks + 2 * B
     out = torch.empty((B, H, 128), dtype=torch.float32, device="cuda")
-    ws = torch.empty(mla.decode_workspace_bytes(max_work, H, 128), dtype=torch.uint8,
-                     device="cuda")
+    ws = mla.decode_workspace(max_work, B, H, 128)
     scale = 1.0 / 8.0
 
     def meta():

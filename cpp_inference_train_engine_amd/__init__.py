@@ -40,7 +40,7 @@ _SIGNATURES = {
     "mla_read_metadata_info": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "mla_append_latent": (C.c_int, [C.c_void_p] + [C.c_int] * 5 + [C.c_void_p] * 3 +
                           [C.c_int, C.c_void_p]),
-    "mla_decode_workspace_bytes": (C.c_size_t, [C.c_int] * 3),
+    "mla_decode_workspace_bytes": (C.c_size_t, [C.c_int] * 4),
     "mla_decode_attention": (C.c_int, [C.c_void_p] + [C.c_int] * 6 + [C.c_float] +
                              [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_void_p] * 8 +
                              [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
@@ -90,7 +90,7 @@ def stream_handle(stream=None) -> int | None:
 
 from .ops import (  # noqa: E402  (re-exported operator interface)
     PagedLatentCache, RaggedBatch, append_latent, build_metadata, decode_attention,
-    decode_workspace_bytes)
+    decode_workspace, decode_workspace_bytes)
 
 __all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
            "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",

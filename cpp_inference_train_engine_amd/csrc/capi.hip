@@ -90,10 +90,15 @@ int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_s
                       "mla_append_latent");
 }
 
-size_t mla_decode_workspace_bytes(int max_work, int n_heads, int kv_rank) {
-    if (max_work <= 0 || n_heads <= 0 || kv_rank <= 0)
+static size_t partial_bytes(int max_work, int n_heads, int kv_rank) {
+    const size_t b = (size_t)max_work * n_heads * ((size_t)kv_rank + 2) * sizeof(float);
+    return (b + 255) & ~(size_t)255;
+}
+
+size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, int kv_rank) {
+    if (max_work <= 0 || max_sessions < 0 || n_heads <= 0 || kv_rank <= 0)
         return 0;
-    return (size_t)max_work * n_heads * ((size_t)kv_rank + 2) * sizeof(float);
+    return partial_bytes(max_work, n_heads, kv_rank) + (size_t)max_sessions * sizeof(int32_t);
 }
 
 int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
@@ -104,7 +109,7 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
                          const int32_t* work_session, const int32_t* work_split,
                          const int32_t* info, int max_work, float* out, float* lse,
                          void* workspace, size_t workspace_bytes, int flags) {
-    if (B < 0 || n_heads < 1 || kv_rank < 1 || kv_rank > 1024 || rope_dim < 0 ||
+    if (B < 0 || n_heads < 1 || kv_rank < 1 || kv_rank > 1024 || rope_dim < 0 || rope_dim > 1024 ||
         page_size < 1 || max_pages < 0 || num_pool_pages < 0 || max_work < 0 ||
         (dtype != MLA_DTYPE_F16 && dtype != MLA_DTYPE_BF16) || !(scale > 0.0f))
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: invalid argument");
@@ -114,7 +119,7 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
         (rope_dim > 0 && !q_rope) || !num_splits || !cu_splits || !work_session ||
         !work_split || !info || !out)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: null buffer");
-    const size_t need = mla_decode_workspace_bytes(max_work, n_heads, kv_rank);
+    const size_t need = mla_decode_workspace_bytes(max_work, B, n_heads, kv_rank);
     if (!workspace || workspace_bytes < need)
         return fail(MLA_ERR_INVALID_ARGUMENT,
                     "mla_decode_attention: workspace needs " + std::to_string(need) + " bytes");
@@ -144,6 +149,8 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
     a.lse = lse;
     a.part_o = const_cast<float*>(ws);
     a.part_ml = const_cast<float*>(ws) + (size_t)max_work * n_heads * kv_rank;
+    a.counters = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                        partial_bytes(max_work, n_heads, kv_rank));
     // The MFMA kernel issues 16-byte loads of q and of cache rows.
     const bool aligned = ((reinterpret_cast<uintptr_t>(pages) | reinterpret_cast<uintptr_t>(q_latent) |
                            reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out) |

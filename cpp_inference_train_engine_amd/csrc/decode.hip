@@ -34,24 +34,40 @@ namespace {
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------- MFMA ----
-template <typename T, int KV, int RP, int PS>
-__global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeArgs a) {
+// Work unit of one wave: 32 tokens (two 16-token MFMA tiles) of one page.  A
+// workgroup of WAVES waves owns one work item (session, split) and deals its
+// units round-robin to the waves; the waves' softmax states are merged in LDS,
+// and the workgroups of one session are merged by the last one to finish
+// (per-session arrival counter, reset by that last workgroup).
+// 128 VGPRs (4 waves/SIMD): two 8-wave workgroups per CU, bounded by LDS too.
+template <typename T, int KV, int RP, int PS, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void decode_mfma_kernel(DecodeArgs a) {
     static_assert(KV % 32 == 0 && RP % 16 == 0 && PS % 32 == 0, "tile shape");
-    constexpr int TILES = PS / 16;  // 16-token tiles per page
-    constexpr int KS = KV / 32;     // latent K-steps of S^T
-    constexpr int RS = RP / 16;     // rope K-steps of S^T
-    constexpr int RT = KV / 16;     // 16-row tiles of O^T
-    constexpr int STRIDE = KV + 4;  // LDS row pitch in 16-bit words (bank spread)
+    constexpr int UNIT = 32;          // tokens per wave unit
+    constexpr int UPP = PS / UNIT;    // units per page
+    constexpr int KS = KV / 32;       // latent K-steps of S^T
+    constexpr int RS = RP / 16;       // rope K-steps of S^T
+    constexpr int RT = KV / 16;       // 16-row tiles of O^T
+    constexpr int STRIDE = KV + 4;    // LDS transpose pitch, 16-bit words (bank spread)
+    constexpr int MSTRIDE = KV + 4;   // LDS merge pitch, floats
+    static_assert(16 * MSTRIDE * 4 <= UNIT * STRIDE * 2, "merge buffer aliases transpose buffer");
     using V8 = typename T::vec8;
     using V4 = typename T::vec4;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[32 * STRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t lds[WAVES][UNIT * STRIDE];
+    __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
+    __shared__ int sm_last;
 
-    const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int W = a.info[0];
     if (W <= 0)
         return;
     const int split = a.info[1];
     const long long rec = (long long)PS * (KV + RP);
+    const bool head_ok = n < a.H;
+    uint16_t* myl = lds[wave];
+    float* mb = reinterpret_cast<float*>(&lds[0][0]);  // [WAVES][16][MSTRIDE] after the loop
+
     for (int w = blockIdx.x; w < W; w += gridDim.x) {
         const int s = a.work_session[w], sp = a.work_split[w];
         const int row = a.cu_q[s];
@@ -61,11 +77,12 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeArgs a) {
         const int need = (kl + PS - 1) / PS;
         const int p_begin = sp * split;
         const int p_end = min(need, p_begin + split);
+        const int u_end = min(p_end * UPP, (kl + UNIT - 1) / UNIT);
+        const int ns = a.num_splits[s];
 
         // Q^T operands (B of S^T): lane (g, n) = head n, latent k 32j+8g.., rope 16k+4g..
         V8 bq[KS];
         V4 bqr[RS];
-        const bool head_ok = n < a.H;
 #pragma unroll
         for (int j = 0; j < KS; ++j) {
             u32x4 v = {0, 0, 0, 0};
@@ -89,18 +106,18 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeArgs a) {
         for (int r = 0; r < RT; ++r)
             acc[r] = floatx4{0, 0, 0, 0};
 
-        for (int p = p_begin; p < p_end; ++p) {
-            const int page = a.page_table[(long long)s * a.max_pages + p];
+        for (int u = p_begin * UPP + wave; u < u_end; u += WAVES) {
+            const int page = a.page_table[(long long)s * a.max_pages + u / UPP];
             const bool page_ok = (unsigned)page < (unsigned)a.num_pool_pages;
             const uint16_t* base = a.pages + (page_ok ? page : 0) * rec;
-            const int tok0 = p * PS;
-            // A operands of S^T straight from HBM: token 16t+n, 16 bytes per K-step.
-            u32x4 lat[TILES][KS];
-            u32x2 rop[TILES][RS];
+            const int tok0 = u * UNIT, slot0 = (u % UPP) * UNIT;
+            // A operands of S^T straight from HBM: token slot0+16t+n, 16 bytes per K-step.
+            u32x4 lat[2][KS];
+            u32x2 rop[2][RS];
 #pragma unroll
-            for (int t = 0; t < TILES; ++t) {
-                const int r = 16 * t + n;
-                const bool ok = page_ok && tok0 + r < kl;
+            for (int t = 0; t < 2; ++t) {
+                const int r = slot0 + 16 * t + n;
+                const bool ok = page_ok && tok0 + 16 * t + n < kl;
 #pragma unroll
                 for (int j = 0; j < KS; ++j)
                     lat[t][j] = ok ? *reinterpret_cast<const u32x4*>(base + r * KV + 32 * j + 8 * g)
@@ -111,10 +128,10 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeArgs a) {
                                                                      16 * k + 4 * g)
                                    : u32x2{0, 0};
             }
-            // Scores S^T[16t + 4g + i][head n].
-            floatx4 sc[TILES];
+            // Scores S^T[tok0 + 16t + 4g + i][head n].
+            floatx4 sc[2];
 #pragma unroll
-            for (int t = 0; t < TILES; ++t) {
+            for (int t = 0; t < 2; ++t) {
                 floatx4 c = {0, 0, 0, 0};
 #pragma unroll
                 for (int j = 0; j < KS; ++j)
@@ -124,9 +141,19 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeArgs a) {
                     c = T::mma16(__builtin_bit_cast(V4, rop[t][k]), bqr[k], c);
                 sc[t] = c;
             }
+            // The latent rows go to LDS for the transposed read of O^T = C^T . P^T.
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int j = 0; j < KS; ++j) {
+                    uint16_t* dst = myl + (16 * t + n) * STRIDE + 32 * j + 8 * g;
+                    const u32x4 v = lat[t][j];
+                    *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
+                    *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
+                }
             float mloc = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < TILES; ++t)
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int tok = tok0 + 16 * t + 4 * g + i;
@@ -139,80 +166,126 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(DecodeArgs a) {
             const float m_new = fmaxf(m_run, mloc);
             const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m_run - m_new);
             float psum = 0.0f;
+            V8 pb;
 #pragma unroll
-            for (int t = 0; t < TILES; ++t)
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float e = m_new == -INFINITY ? 0.0f : exp2_fast(sc[t][i] - m_new);
-                    sc[t][i] = e;
                     psum += e;
+                    pb[4 * t + i] = static_cast<typename T::scalar>(e);
                 }
             l_run = l_run * alpha + psum;
             m_run = m_new;
 #pragma unroll
             for (int r = 0; r < RT; ++r)
                 acc[r] *= alpha;
-            // O^T += C^T . P^T, 32 tokens (tiles 2kb, 2kb+1) per MFMA K-block.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // O^T += C^T . P^T: A = C^T (lane: column 16rt+n, tokens 4g+i and 16+4g+i),
+            // B = P^T (lane: head n, the same 8 tokens) -- consistent K-slot order.
 #pragma unroll
-            for (int kb = 0; kb < TILES / 2; ++kb) {
-#pragma unroll
-                for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                    for (int j = 0; j < KS; ++j) {
-                        uint16_t* dst = lds + (16 * tt + n) * STRIDE + 32 * j + 8 * g;
-                        const u32x4 v = lat[2 * kb + tt][j];
-                        *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
-                        *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
-                    }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                V8 pb;
+            for (int rt = 0; rt < RT; ++rt) {
+                V8 ac;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pb[i] = static_cast<typename T::scalar>(sc[2 * kb][i]);
-                    pb[4 + i] = static_cast<typename T::scalar>(sc[2 * kb + 1][i]);
+                    ac[i] = __builtin_bit_cast(typename T::scalar,
+                                               myl[(4 * g + i) * STRIDE + 16 * rt + n]);
+                    ac[4 + i] = __builtin_bit_cast(typename T::scalar,
+                                                   myl[(16 + 4 * g + i) * STRIDE + 16 * rt + n]);
                 }
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
-                    V8 ac;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        ac[i] = __builtin_bit_cast(typename T::scalar,
-                                                   lds[(4 * g + i) * STRIDE + 16 * rt + n]);
-                        ac[4 + i] = __builtin_bit_cast(typename T::scalar,
-                                                       lds[(16 + 4 * g + i) * STRIDE + 16 * rt + n]);
-                    }
-                    acc[rt] = T::mma32(ac, pb, acc[rt]);
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                acc[rt] = T::mma32(ac, pb, acc[rt]);
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         l_run += __shfl_xor(l_run, 16, 64);
         l_run += __shfl_xor(l_run, 32, 64);
-        if (!head_ok)
-            continue;
-        // Lane (g, n) holds O^T[16rt + 4g + i][head n].
-        if (a.num_splits[s] == 1) {
-            const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-            float* o = a.out + ((long long)row * a.H + n) * KV;
+
+        // ---- merge the WAVES softmax states of this work item in LDS ----
+        if (g == 0) {
+            sm_m[wave][n] = m_run;
+            sm_l[wave][n] = l_run;
+        }
+        __syncthreads();  // every wave is done with its transpose buffer
+        {
+            float mh = -INFINITY;
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-                *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt] * inv;
-            if (a.lse && g == 0)
-                a.lse[(long long)row * a.H + n] = (m_run + __log2f(l_run)) * kLn2;
-        } else {
-            float* o = a.part_o + ((long long)w * a.H + n) * KV;
+            for (int v = 0; v < WAVES; ++v)
+                mh = fmaxf(mh, sm_m[v][n]);
+            const float f = m_run == -INFINITY ? 0.0f : exp2_fast(m_run - mh);
+            if (head_ok)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-                *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt];
-            if (g == 0) {
-                a.part_ml[((long long)w * a.H + n) * 2] = m_run;
-                a.part_ml[((long long)w * a.H + n) * 2 + 1] = l_run;
+                for (int rt = 0; rt < RT; ++rt)
+                    *reinterpret_cast<floatx4*>(mb + (wave * 16 + n) * MSTRIDE + 16 * rt + 4 * g) =
+                        acc[rt] * f;
+        }
+        __syncthreads();
+        for (int e = tid; e < a.H * (KV / 4); e += 64 * WAVES) {
+            const int h = e / (KV / 4), c = (e % (KV / 4)) * 4;
+            float mh = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < WAVES; ++v)
+                mh = fmaxf(mh, sm_m[v][h]);
+            float lh = 0.0f;
+            floatx4 o = {0, 0, 0, 0};
+#pragma unroll
+            for (int v = 0; v < WAVES; ++v) {
+                const float mv = sm_m[v][h];
+                lh += mv == -INFINITY ? 0.0f : sm_l[v][h] * exp2_fast(mv - mh);
+                o += *reinterpret_cast<const floatx4*>(mb + (v * 16 + h) * MSTRIDE + c);
+            }
+            if (ns == 1) {
+                const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+                *reinterpret_cast<floatx4*>(a.out + ((long long)row * a.H + h) * KV + c) = o * inv;
+                if (a.lse && c == 0)
+                    a.lse[(long long)row * a.H + h] = (mh + __log2f(lh)) * kLn2;
+            } else {
+                *reinterpret_cast<floatx4*>(a.part_o + ((long long)w * a.H + h) * KV + c) = o;
+                if (c == 0) {
+                    a.part_ml[((long long)w * a.H + h) * 2] = mh;
+                    a.part_ml[((long long)w * a.H + h) * 2 + 1] = lh;
+                }
             }
         }
+        if (ns > 1) {
+            // ---- the last workgroup of the session merges every split ----
+            __threadfence();
+            __syncthreads();
+            if (tid == 0) {
+                const int old = atomicAdd(a.counters + s, 1);
+                sm_last = old == ns - 1;
+                if (old == ns - 1)
+                    atomicExch(a.counters + s, 0);
+            }
+            __syncthreads();
+            if (sm_last) {
+                __threadfence();
+                const int w0 = a.cu_splits[s];
+                for (int e = tid; e < a.H * (KV / 4); e += 64 * WAVES) {
+                    const int h = e / (KV / 4), c = (e % (KV / 4)) * 4;
+                    float mh = -INFINITY;
+                    for (int i = 0; i < ns; ++i)
+                        mh = fmaxf(mh, a.part_ml[((long long)(w0 + i) * a.H + h) * 2]);
+                    float lh = 0.0f;
+                    floatx4 o = {0, 0, 0, 0};
+                    for (int i = 0; i < ns; ++i) {
+                        const long long idx = (long long)(w0 + i) * a.H + h;
+                        const float mv = a.part_ml[idx * 2];
+                        const float f = mv == -INFINITY ? 0.0f : exp2_fast(mv - mh);
+                        lh += f * a.part_ml[idx * 2 + 1];
+                        o += f * *reinterpret_cast<const floatx4*>(a.part_o + idx * KV + c);
+                    }
+                    const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+                    *reinterpret_cast<floatx4*>(a.out + ((long long)row * a.H + h) * KV + c) = o * inv;
+                    if (a.lse && c == 0)
+                        a.lse[(long long)row * a.H + h] = (mh + __log2f(lh)) * kLn2;
+                }
+            }
+        }
+        __syncthreads();  // LDS and sm_* are reused by the next work item
     }
 }
 
@@ -376,10 +449,13 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     }
 }
 
+constexpr int kMfmaWaves = 8;
+
 template <typename T>
 hipError_t launch_mfma(const DecodeArgs& a, int grid, hipStream_t stream) {
     if (a.kv_rank == 128 && a.rope_dim == 16 && a.page_size == 64)
-        hipLaunchKernelGGL((decode_mfma_kernel<T, 128, 16, 64>), dim3(grid), dim3(64), 0, stream, a);
+        hipLaunchKernelGGL((decode_mfma_kernel<T, 128, 16, 64, kMfmaWaves>), dim3(grid),
+                           dim3(64 * kMfmaWaves), 0, stream, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -397,7 +473,8 @@ hipError_t launch_decode(const DecodeArgs& a, int dtype, bool force_generic, hip
     const int grid = a.max_work < 65535 ? a.max_work : 65535;
     hipError_t err;
     if (!force_generic && decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size)) {
-        err = dtype == 0 ? launch_mfma<F16>(a, grid, stream) : launch_mfma<BF16>(a, grid, stream);
+        // The MFMA kernel merges split partials itself (no merge launch).
+        return dtype == 0 ? launch_mfma<F16>(a, grid, stream) : launch_mfma<BF16>(a, grid, stream);
     } else {
         const size_t shmem = (a.kv_rank + a.rope_dim + kGenChunk + 8) * sizeof(float);
         const dim3 g(grid, a.H);

@@ -87,10 +87,6 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
             const long long kl = ctx + q;
             const long long need = (kl + a.page_size - 1) / a.page_size;
             bad = q < 0 || ctx < 0 || npages < 0 || npages > a.max_pages || need > npages;
-            for (long long j = 0; !bad && j < npages; ++j) {
-                const int32_t pid = a.page_ids[a.cu_pages[b] + j];
-                bad = pid < 0 || pid >= a.num_pool_pages;
-            }
             v[0] = q;
             v[1] = kl;
             v[2] = q > 0 ? need : 0;
@@ -109,6 +105,22 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
                 carry[k] += tot[k];
         __syncthreads();
     }
+    // Phase 1b: padded page table and page-id validation, one entry per thread
+    // (independent loads; a session listing more than max_pages pages is
+    // already invalid and only its first max_pages ids are read).
+    const long long entries = (long long)a.B * a.max_pages;
+    for (long long e = tid; e < entries; e += kMetaThreads) {
+        const int b = (int)(e / a.max_pages), j = (int)(e % a.max_pages);
+        const int npages = a.cu_pages[b + 1] - a.cu_pages[b];
+        int32_t pid = -1;
+        if (j < npages) {
+            pid = a.page_ids[a.cu_pages[b] + j];
+            if (pid < 0 || pid >= a.num_pool_pages)
+                atomicMin(&err, b);
+        }
+        a.page_table[e] = pid;
+    }
+    __syncthreads();
     if (err != INT_MAX) {
         if (tid == 0) {
             a.info[0] = -1;
@@ -167,12 +179,6 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         const int b = upper_index(a.cu_splits, a.B, w);
         a.work_session[w] = b;
         a.work_split[w] = (int32_t)(w - a.cu_splits[b]);
-    }
-    const long long entries = (long long)a.B * a.max_pages;
-    for (long long e = tid; e < entries; e += kMetaThreads) {
-        const int b = (int)(e / a.max_pages), j = (int)(e % a.max_pages);
-        const int npages = a.cu_pages[b + 1] - a.cu_pages[b];
-        a.page_table[e] = j < npages ? a.page_ids[a.cu_pages[b] + j] : -1;
     }
     for (long long i = tid; i < total_q; i += kMetaThreads) {
         const int b = upper_index(a.cu_seqlens_q, a.B, i);

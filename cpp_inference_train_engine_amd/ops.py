@@ -115,8 +115,16 @@ def append_latent(cache: PagedLatentCache, layer: int, ckv, krope, slot_mapping,
                                   ptr(slot_mapping), cache.num_pages, ptr(cache.layer(layer))))
 
 
-def decode_workspace_bytes(max_work: int, n_heads: int, kv_rank: int) -> int:
-    return int(lib().mla_decode_workspace_bytes(max_work, n_heads, kv_rank))
+def decode_workspace_bytes(max_work: int, max_sessions: int, n_heads: int, kv_rank: int) -> int:
+    return int(lib().mla_decode_workspace_bytes(max_work, max_sessions, n_heads, kv_rank))
+
+
+def decode_workspace(max_work: int, max_sessions: int, n_heads: int, kv_rank: int,
+                     device="cuda"):
+    """Zero-filled decode workspace (split partials + per-session merge counters)."""
+    torch = _torch()
+    n = max(decode_workspace_bytes(max_work, max_sessions, n_heads, kv_rank), 4)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
 def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
@@ -130,8 +138,7 @@ def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, 
     if out is None:
         out = torch.zeros((rows, H, kv_rank), dtype=torch.float32, device=q_latent.device)
     if workspace is None:
-        nbytes = decode_workspace_bytes(batch.max_work, H, kv_rank)
-        workspace = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q_latent.device)
+        workspace = decode_workspace(batch.max_work, batch.B, H, kv_rank, q_latent.device)
     check(lib().mla_decode_attention(
         stream_handle(stream), batch.B, H, kv_rank, rope_dim, batch.page_size, dtype,
         float(scale), ptr(batch.cu_seqlens_q), ptr(batch.cu_seqlens_k), ptr(batch.page_table),
@@ -143,4 +150,4 @@ def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, 
 
 
 __all__ = ["RaggedBatch", "build_metadata", "PagedLatentCache", "append_latent",
-           "decode_workspace_bytes", "decode_attention", "DTYPE_F16", "DTYPE_BF16"]
+           "decode_workspace_bytes", "decode_workspace", "decode_attention", "DTYPE_F16", "DTYPE_BF16"]

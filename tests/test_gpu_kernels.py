@@ -252,3 +252,27 @@ def test_decode_skips_prefill_rows_and_tolerates_garbage_slots(gpu, orc):
     got, _, _ = _run_decode(gpu, batch, split=1, want_lse=False)
     assert np.all(got[1:4] == 0)
     assert np.abs(got[[0, 4, 5]]).sum() > 0
+
+
+def test_decode_workspace_reuse_across_calls(gpu, orc):
+    """The fused split merge leaves its per-session counters at zero: one zeroed workspace
+    serves consecutive calls with different batches, layers and split sizes."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    ws = gpu.decode_workspace(4096, 64, 8, 128)
+    for seed, split, n in [(11, 1, 64), (12, 3, 20), (13, 0, 64), (11, 2, 64)]:
+        batch = ragged_decode_batch(B=n, max_len=3000, seed=seed, n_layers=2)
+        for layer in (0, 1):
+            rb = gpu.build_metadata(_dev(batch.ctx_len), _dev(batch.q_len), _dev(batch.cu_pages),
+                                    _dev(batch.page_ids), 64, batch.max_pages, batch.num_pages,
+                                    split_pages=split, target_blocks=300, max_work=4096)
+            pages = _dev(batch.pages[layer].view(np.int16)).view(torch.float16)
+            ql = _dev(batch.q_latent.view(np.int16)).view(torch.float16)
+            qr = _dev(batch.q_rope.view(np.int16)).view(torch.float16)
+            out = gpu.decode_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16,
+                                       workspace=ws)
+            torch.cuda.synchronize()
+            want, _ = _oracle_decode(orc, batch, layer=layer)
+            _check(out.cpu().numpy(), want, f"seed={seed} split={split} layer={layer}")
+    counters = ws[-64 * 4:].view(torch.int32).cpu().numpy()
+    assert np.all(counters == 0)
