@@ -33,6 +33,15 @@ namespace {
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Device-coherent (agent-scope) accesses: compiled to sc1 loads/stores that do not
+// hit stale lines in another XCD's L2.
+__device__ inline void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float load_coherent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------- MFMA ----
 // Work unit of one wave: 32 tokens (two 16-token MFMA tiles) of one page.  A
 // workgroup of WAVES waves owns one work item (session, split) and deals its
@@ -40,20 +49,27 @@ __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 // and the workgroups of one session are merged by the last one to finish
 // (per-session arrival counter, reset by that last workgroup).
 // 128 VGPRs (4 waves/SIMD): two 8-wave workgroups per CU, bounded by LDS too.
+#ifndef MLA_DECODE_WAVES_PER_EU
+#define MLA_DECODE_WAVES_PER_EU 4
+#endif
 template <typename T, int KV, int RP, int PS, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(4, 8)))
-void decode_mfma_kernel(DecodeArgs a) {
-    static_assert(KV % 32 == 0 && RP % 16 == 0 && PS % 32 == 0, "tile shape");
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfma_kernel(DecodeArgs a) {
+    static_assert(KV % 32 == 0 && RP % 8 == 0 && PS % 32 == 0, "tile shape");
     constexpr int UNIT = 32;          // tokens per wave unit
     constexpr int UPP = PS / UNIT;    // units per page
     constexpr int KS = KV / 32;       // latent K-steps of S^T
-    constexpr int RS = RP / 16;       // rope K-steps of S^T
+    // Rope K-steps of S^T, 32 wide: lane group g covers rope dims 32k+8g..+7 and
+    // holds zeros past RP (both operands), so every MFMA is 16x16x32.  This keeps
+    // the score chain on one MFMA shape; the legacy 16x16x16 form was given a
+    // destination partially overlapping its accumulator input by the register
+    // allocator, which corrupts results.
+    constexpr int RS = (RP + 31) / 32;
     constexpr int RT = KV / 16;       // 16-row tiles of O^T
     constexpr int STRIDE = KV + 4;    // LDS transpose pitch, 16-bit words (bank spread)
     constexpr int MSTRIDE = KV + 4;   // LDS merge pitch, floats
     static_assert(16 * MSTRIDE * 4 <= UNIT * STRIDE * 2, "merge buffer aliases transpose buffer");
     using V8 = typename T::vec8;
-    using V4 = typename T::vec4;
     __shared__ __attribute__((aligned(16))) uint16_t lds[WAVES][UNIT * STRIDE];
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
     __shared__ int sm_last;
@@ -82,7 +98,7 @@ void decode_mfma_kernel(DecodeArgs a) {
 
         // Q^T operands (B of S^T): lane (g, n) = head n, latent k 32j+8g.., rope 16k+4g..
         V8 bq[KS];
-        V4 bqr[RS];
+        V8 bqr[RS];
 #pragma unroll
         for (int j = 0; j < KS; ++j) {
             u32x4 v = {0, 0, 0, 0};
@@ -93,11 +109,11 @@ void decode_mfma_kernel(DecodeArgs a) {
         }
 #pragma unroll
         for (int k = 0; k < RS; ++k) {
-            u32x2 v = {0, 0};
-            if (head_ok)
-                v = *reinterpret_cast<const u32x2*>(a.q_rope + ((long long)row * a.H + n) * RP +
-                                                    16 * k + 4 * g);
-            bqr[k] = __builtin_bit_cast(V4, v);
+            u32x4 v = {0, 0, 0, 0};
+            if (head_ok && 32 * k + 8 * g < RP)
+                v = *reinterpret_cast<const u32x4*>(a.q_rope + ((long long)row * a.H + n) * RP +
+                                                    32 * k + 8 * g);
+            bqr[k] = __builtin_bit_cast(V8, v);
         }
 
         float m_run = -INFINITY, l_run = 0.0f;
@@ -113,7 +129,7 @@ void decode_mfma_kernel(DecodeArgs a) {
             const int tok0 = u * UNIT, slot0 = (u % UPP) * UNIT;
             // A operands of S^T straight from HBM: token slot0+16t+n, 16 bytes per K-step.
             u32x4 lat[2][KS];
-            u32x2 rop[2][RS];
+            u32x4 rop[2][RS];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int r = slot0 + 16 * t + n;
@@ -124,9 +140,10 @@ void decode_mfma_kernel(DecodeArgs a) {
                                    : u32x4{0, 0, 0, 0};
 #pragma unroll
                 for (int k = 0; k < RS; ++k)
-                    rop[t][k] = ok ? *reinterpret_cast<const u32x2*>(base + PS * KV + r * RP +
-                                                                     16 * k + 4 * g)
-                                   : u32x2{0, 0};
+                    rop[t][k] = ok && 32 * k + 8 * g < RP
+                                    ? *reinterpret_cast<const u32x4*>(base + PS * KV + r * RP +
+                                                                      32 * k + 8 * g)
+                                    : u32x4{0, 0, 0, 0};
             }
             // Scores S^T[tok0 + 16t + 4g + i][head n].
             floatx4 sc[2];
@@ -138,7 +155,7 @@ void decode_mfma_kernel(DecodeArgs a) {
                     c = T::mma32(__builtin_bit_cast(V8, lat[t][j]), bq[j], c);
 #pragma unroll
                 for (int k = 0; k < RS; ++k)
-                    c = T::mma16(__builtin_bit_cast(V4, rop[t][k]), bqr[k], c);
+                    c = T::mma32(__builtin_bit_cast(V8, rop[t][k]), bqr[k], c);
                 sc[t] = c;
             }
             // The latent rows go to LDS for the transposed read of O^T = C^T . P^T.
@@ -205,6 +222,12 @@ void decode_mfma_kernel(DecodeArgs a) {
         l_run += __shfl_xor(l_run, 32, 64);
 
         // ---- merge the WAVES softmax states of this work item in LDS ----
+#ifdef MLA_DECODE_DEBUG_STATES
+        if (g == 0) {
+            a.part_ml[((long long)(w * WAVES + wave) * 16 + n) * 2] = m_run;
+            a.part_ml[((long long)(w * WAVES + wave) * 16 + n) * 2 + 1] = l_run;
+        }
+#endif
         if (g == 0) {
             sm_m[wave][n] = m_run;
             sm_l[wave][n] = l_run;
@@ -243,40 +266,48 @@ void decode_mfma_kernel(DecodeArgs a) {
                 if (a.lse && c == 0)
                     a.lse[(long long)row * a.H + h] = (mh + __log2f(lh)) * kLn2;
             } else {
-                *reinterpret_cast<floatx4*>(a.part_o + ((long long)w * a.H + h) * KV + c) = o;
+                // Partials cross workgroups (and XCDs, whose L2s are not coherent with
+                // each other): write them with device-coherent stores.
+                float* po = a.part_o + ((long long)w * a.H + h) * KV + c;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    store_coherent(po + i, o[i]);
                 if (c == 0) {
-                    a.part_ml[((long long)w * a.H + h) * 2] = mh;
-                    a.part_ml[((long long)w * a.H + h) * 2 + 1] = lh;
+                    store_coherent(a.part_ml + ((long long)w * a.H + h) * 2, mh);
+                    store_coherent(a.part_ml + ((long long)w * a.H + h) * 2 + 1, lh);
                 }
             }
         }
         if (ns > 1) {
             // ---- the last workgroup of the session merges every split ----
-            __threadfence();
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete
             __syncthreads();
             if (tid == 0) {
-                const int old = atomicAdd(a.counters + s, 1);
+                const int old = __hip_atomic_fetch_add(a.counters + s, 1, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
                 sm_last = old == ns - 1;
                 if (old == ns - 1)
-                    atomicExch(a.counters + s, 0);
+                    __hip_atomic_store(a.counters + s, 0, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
             }
             __syncthreads();
             if (sm_last) {
-                __threadfence();
                 const int w0 = a.cu_splits[s];
                 for (int e = tid; e < a.H * (KV / 4); e += 64 * WAVES) {
                     const int h = e / (KV / 4), c = (e % (KV / 4)) * 4;
                     float mh = -INFINITY;
                     for (int i = 0; i < ns; ++i)
-                        mh = fmaxf(mh, a.part_ml[((long long)(w0 + i) * a.H + h) * 2]);
+                        mh = fmaxf(mh, load_coherent(a.part_ml + ((long long)(w0 + i) * a.H + h) * 2));
                     float lh = 0.0f;
                     floatx4 o = {0, 0, 0, 0};
                     for (int i = 0; i < ns; ++i) {
                         const long long idx = (long long)(w0 + i) * a.H + h;
-                        const float mv = a.part_ml[idx * 2];
+                        const float mv = load_coherent(a.part_ml + idx * 2);
                         const float f = mv == -INFINITY ? 0.0f : exp2_fast(mv - mh);
-                        lh += f * a.part_ml[idx * 2 + 1];
-                        o += f * *reinterpret_cast<const floatx4*>(a.part_o + idx * KV + c);
+                        lh += f * load_coherent(a.part_ml + idx * 2 + 1);
+                        const float* po = a.part_o + idx * KV + c;
+                        o += f * floatx4{load_coherent(po), load_coherent(po + 1),
+                                         load_coherent(po + 2), load_coherent(po + 3)};
                     }
                     const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
                     *reinterpret_cast<floatx4*>(a.out + ((long long)row * a.H + h) * KV + c) = o * inv;
@@ -449,7 +480,10 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     }
 }
 
-constexpr int kMfmaWaves = 8;
+#ifndef MLA_DECODE_WAVES
+#define MLA_DECODE_WAVES 8
+#endif
+constexpr int kMfmaWaves = MLA_DECODE_WAVES;
 
 template <typename T>
 hipError_t launch_mfma(const DecodeArgs& a, int grid, hipStream_t stream) {
