@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sessions", type=int, default=64)
     ap.add_argument("--target-blocks", type=int, default=1024)
-    ap.add_argument("--split-pages", type=int, default=0)
+    ap.add_argument("--split-pages", type=int, default=4)
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)

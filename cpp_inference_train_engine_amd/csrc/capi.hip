@@ -98,7 +98,7 @@ static size_t partial_bytes(int max_work, int n_heads, int kv_rank) {
 size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, int kv_rank) {
     if (max_work <= 0 || max_sessions < 0 || n_heads <= 0 || kv_rank <= 0)
         return 0;
-    return partial_bytes(max_work, n_heads, kv_rank) + (size_t)max_sessions * sizeof(int32_t);
+    return partial_bytes(max_work, n_heads, kv_rank);
 }
 
 int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
@@ -149,8 +149,6 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
     a.lse = lse;
     a.part_o = const_cast<float*>(ws);
     a.part_ml = const_cast<float*>(ws) + (size_t)max_work * n_heads * kv_rank;
-    a.counters = reinterpret_cast<int*>(static_cast<char*>(workspace) +
-                                        partial_bytes(max_work, n_heads, kv_rank));
     // The MFMA kernel issues 16-byte loads of q and of cache rows.
     const bool aligned = ((reinterpret_cast<uintptr_t>(pages) | reinterpret_cast<uintptr_t>(q_latent) |
                            reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out) |

@@ -33,46 +33,151 @@ namespace {
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Device-coherent (agent-scope) accesses: compiled to sc1 loads/stores that do not
-// hit stale lines in another XCD's L2.
-__device__ inline void store_coherent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline float load_coherent(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// ---------------------------------------------------------------- MFMA ----
+// A 32-token unit = two 16-token MFMA tiles.  Lane (g, n) holds, as the A
+// operands of S^T, token 16t+n of the unit: 16 latent bytes per 32-wide K-step
+// and the rope key padded to 32-wide K-steps (lane groups past rope_dim hold
+// zeros in both operands).  Every MFMA of the kernel is 16x16x32: the legacy
+// 16x16x16 form got a destination partially overlapping its accumulator input
+// from the register allocator, which corrupts results.
+template <int KV, int RP>
+struct UnitRegs {
+    static constexpr int KS = KV / 32, RS = (RP + 31) / 32;
+    u32x4 lat[2][KS];
+    u32x4 rop[2][RS];
+};
+
+// Loads rows slot0.. of page record `base`; only the first `valid` rows are read.
+template <int KV, int RP, int PS>
+__device__ __forceinline__ void load_unit(UnitRegs<KV, RP>& u, const uint16_t* base, int slot0,
+                                          int valid, int g, int n) {
+    constexpr int KS = UnitRegs<KV, RP>::KS, RS = UnitRegs<KV, RP>::RS;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int r = slot0 + 16 * t + n;
+        const bool ok = 16 * t + n < valid;
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+            u.lat[t][j] = ok ? *reinterpret_cast<const u32x4*>(base + r * KV + 32 * j + 8 * g)
+                             : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < RS; ++k)
+            u.rop[t][k] = ok && 32 * k + 8 * g < RP
+                              ? *reinterpret_cast<const u32x4*>(base + PS * KV + r * RP + 32 * k +
+                                                                8 * g)
+                              : u32x4{0, 0, 0, 0};
+    }
 }
 
-// ---------------------------------------------------------------- MFMA ----
-// Work unit of one wave: 32 tokens (two 16-token MFMA tiles) of one page.  A
-// workgroup of WAVES waves owns one work item (session, split) and deals its
-// units round-robin to the waves; the waves' softmax states are merged in LDS,
-// and the workgroups of one session are merged by the last one to finish
-// (per-session arrival counter, reset by that last workgroup).
-// 128 VGPRs (4 waves/SIMD): two 8-wave workgroups per CU, bounded by LDS too.
+// Scores of one unit, online-softmax update, O^T += C^T . P^T.  `valid` tokens of
+// the unit count; the rest are masked.  myl is this wave's LDS transpose buffer.
+template <typename T, int KV, int RP>
+__device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int valid,
+                                             const typename T::vec8* bq,
+                                             const typename T::vec8* bqr, float scale_log2,
+                                             float& m_run, float& l_run, floatx4* acc,
+                                             uint16_t* myl, int g, int n) {
+    constexpr int KS = UnitRegs<KV, RP>::KS, RS = UnitRegs<KV, RP>::RS;
+    constexpr int RT = KV / 16;
+    constexpr int STRIDE = KV + 4;
+    using V8 = typename T::vec8;
+    // S^T[16t + 4g + i][head n]
+    floatx4 sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        floatx4 c = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+            c = T::mma32(__builtin_bit_cast(V8, u.lat[t][j]), bq[j], c);
+#pragma unroll
+        for (int k = 0; k < RS; ++k)
+            c = T::mma32(__builtin_bit_cast(V8, u.rop[t][k]), bqr[k], c);
+        sc[t] = c;
+    }
+    // Latent rows to LDS for the transposed read of C^T.
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+            uint16_t* dst = myl + (16 * t + n) * STRIDE + 32 * j + 8 * g;
+            const u32x4 v = u.lat[t][j];
+            *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
+            *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
+        }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = 16 * t + 4 * g + i < valid ? sc[t][i] * scale_log2 : -INFINITY;
+            sc[t][i] = x;
+            mloc = fmaxf(mloc, x);
+        }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m_run - m_new);
+    float psum = 0.0f;
+    V8 pb;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e = m_new == -INFINITY ? 0.0f : exp2_fast(sc[t][i] - m_new);
+            psum += e;
+            pb[4 * t + i] = static_cast<typename T::scalar>(e);
+        }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+        acc[r] *= alpha;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // A = C^T (lane: column 16rt+n, tokens 4g+i and 16+4g+i), B = P^T (lane: head n,
+    // the same 8 tokens): the K-slot order agrees between the operands.
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        V8 ac;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ac[i] = __builtin_bit_cast(typename T::scalar, myl[(4 * g + i) * STRIDE + 16 * rt + n]);
+            ac[4 + i] =
+                __builtin_bit_cast(typename T::scalar, myl[(16 + 4 * g + i) * STRIDE + 16 * rt + n]);
+        }
+        acc[rt] = T::mma32(ac, pb, acc[rt]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One workgroup of WAVES waves per work item (session, split); wave v takes pages
+// p_begin+v, p_begin+v+WAVES, ... and issues both 32-token halves of a page before
+// computing.  The waves' softmax states merge in LDS; a session split over several
+// workgroups leaves one partial per workgroup for merge_kernel (the next launch on
+// the stream, so the partials are coherent without device-scope fences).
+// Up to 256 VGPRs (2 waves/SIMD): two 4-wave workgroups per CU; each wave keeps
+// one whole page (18 KB) in flight.
 #ifndef MLA_DECODE_WAVES_PER_EU
-#define MLA_DECODE_WAVES_PER_EU 4
+#define MLA_DECODE_WAVES_PER_EU 2
 #endif
+
 template <typename T, int KV, int RP, int PS, int WAVES>
 __global__ __launch_bounds__(64 * WAVES)
 __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfma_kernel(DecodeArgs a) {
     static_assert(KV % 32 == 0 && RP % 8 == 0 && PS % 32 == 0, "tile shape");
-    constexpr int UNIT = 32;          // tokens per wave unit
-    constexpr int UPP = PS / UNIT;    // units per page
-    constexpr int KS = KV / 32;       // latent K-steps of S^T
-    // Rope K-steps of S^T, 32 wide: lane group g covers rope dims 32k+8g..+7 and
-    // holds zeros past RP (both operands), so every MFMA is 16x16x32.  This keeps
-    // the score chain on one MFMA shape; the legacy 16x16x16 form was given a
-    // destination partially overlapping its accumulator input by the register
-    // allocator, which corrupts results.
-    constexpr int RS = (RP + 31) / 32;
+    constexpr int UPP = PS / 32;      // 32-token units per page
+    constexpr int KS = KV / 32, RS = (RP + 31) / 32;
     constexpr int RT = KV / 16;       // 16-row tiles of O^T
     constexpr int STRIDE = KV + 4;    // LDS transpose pitch, 16-bit words (bank spread)
     constexpr int MSTRIDE = KV + 4;   // LDS merge pitch, floats
-    static_assert(16 * MSTRIDE * 4 <= UNIT * STRIDE * 2, "merge buffer aliases transpose buffer");
+    constexpr int THREADS = 64 * WAVES;
+    static_assert(16 * MSTRIDE * 4 <= 32 * STRIDE * 2, "merge buffer aliases transpose buffer");
     using V8 = typename T::vec8;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[WAVES][UNIT * STRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t lds[WAVES][32 * STRIDE];
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
-    __shared__ int sm_last;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int W = a.info[0];
@@ -93,12 +198,10 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
         const int need = (kl + PS - 1) / PS;
         const int p_begin = sp * split;
         const int p_end = min(need, p_begin + split);
-        const int u_end = min(p_end * UPP, (kl + UNIT - 1) / UNIT);
         const int ns = a.num_splits[s];
 
-        // Q^T operands (B of S^T): lane (g, n) = head n, latent k 32j+8g.., rope 16k+4g..
-        V8 bq[KS];
-        V8 bqr[RS];
+        // Q^T operands (B of S^T): lane (g, n) = head n.
+        V8 bq[KS], bqr[RS];
 #pragma unroll
         for (int j = 0; j < KS; ++j) {
             u32x4 v = {0, 0, 0, 0};
@@ -122,112 +225,26 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
         for (int r = 0; r < RT; ++r)
             acc[r] = floatx4{0, 0, 0, 0};
 
-        for (int u = p_begin * UPP + wave; u < u_end; u += WAVES) {
-            const int page = a.page_table[(long long)s * a.max_pages + u / UPP];
-            const bool page_ok = (unsigned)page < (unsigned)a.num_pool_pages;
-            const uint16_t* base = a.pages + (page_ok ? page : 0) * rec;
-            const int tok0 = u * UNIT, slot0 = (u % UPP) * UNIT;
-            // A operands of S^T straight from HBM: token slot0+16t+n, 16 bytes per K-step.
-            u32x4 lat[2][KS];
-            u32x4 rop[2][RS];
+        for (int p = p_begin + wave; p < p_end; p += WAVES) {
+            const int page = a.page_table[(long long)s * a.max_pages + p];
+            if ((unsigned)page >= (unsigned)a.num_pool_pages)
+                continue;
+            const uint16_t* base = a.pages + page * rec;
+            const int valid = min(PS, kl - p * PS);
+            UnitRegs<KV, RP> u[UPP];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int r = slot0 + 16 * t + n;
-                const bool ok = page_ok && tok0 + 16 * t + n < kl;
+            for (int q = 0; q < UPP; ++q)
+                load_unit<KV, RP, PS>(u[q], base, 32 * q, valid - 32 * q, g, n);
 #pragma unroll
-                for (int j = 0; j < KS; ++j)
-                    lat[t][j] = ok ? *reinterpret_cast<const u32x4*>(base + r * KV + 32 * j + 8 * g)
-                                   : u32x4{0, 0, 0, 0};
-#pragma unroll
-                for (int k = 0; k < RS; ++k)
-                    rop[t][k] = ok && 32 * k + 8 * g < RP
-                                    ? *reinterpret_cast<const u32x4*>(base + PS * KV + r * RP +
-                                                                      32 * k + 8 * g)
-                                    : u32x4{0, 0, 0, 0};
-            }
-            // Scores S^T[tok0 + 16t + 4g + i][head n].
-            floatx4 sc[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                floatx4 c = {0, 0, 0, 0};
-#pragma unroll
-                for (int j = 0; j < KS; ++j)
-                    c = T::mma32(__builtin_bit_cast(V8, lat[t][j]), bq[j], c);
-#pragma unroll
-                for (int k = 0; k < RS; ++k)
-                    c = T::mma32(__builtin_bit_cast(V8, rop[t][k]), bqr[k], c);
-                sc[t] = c;
-            }
-            // The latent rows go to LDS for the transposed read of O^T = C^T . P^T.
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int j = 0; j < KS; ++j) {
-                    uint16_t* dst = myl + (16 * t + n) * STRIDE + 32 * j + 8 * g;
-                    const u32x4 v = lat[t][j];
-                    *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
-                    *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
-                }
-            float mloc = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tok = tok0 + 16 * t + 4 * g + i;
-                    const float x = (page_ok && tok < kl) ? sc[t][i] * a.scale_log2 : -INFINITY;
-                    sc[t][i] = x;
-                    mloc = fmaxf(mloc, x);
-                }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-            const float m_new = fmaxf(m_run, mloc);
-            const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m_run - m_new);
-            float psum = 0.0f;
-            V8 pb;
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float e = m_new == -INFINITY ? 0.0f : exp2_fast(sc[t][i] - m_new);
-                    psum += e;
-                    pb[4 * t + i] = static_cast<typename T::scalar>(e);
-                }
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
-#pragma unroll
-            for (int r = 0; r < RT; ++r)
-                acc[r] *= alpha;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            // O^T += C^T . P^T: A = C^T (lane: column 16rt+n, tokens 4g+i and 16+4g+i),
-            // B = P^T (lane: head n, the same 8 tokens) -- consistent K-slot order.
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                V8 ac;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    ac[i] = __builtin_bit_cast(typename T::scalar,
-                                               myl[(4 * g + i) * STRIDE + 16 * rt + n]);
-                    ac[4 + i] = __builtin_bit_cast(typename T::scalar,
-                                                   myl[(16 + 4 * g + i) * STRIDE + 16 * rt + n]);
-                }
-                acc[rt] = T::mma32(ac, pb, acc[rt]);
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int q = 0; q < UPP; ++q)
+                if (valid > 32 * q)
+                    process_unit<T, KV, RP>(u[q], valid - 32 * q, bq, bqr, a.scale_log2, m_run,
+                                            l_run, acc, myl, g, n);
         }
         l_run += __shfl_xor(l_run, 16, 64);
         l_run += __shfl_xor(l_run, 32, 64);
 
         // ---- merge the WAVES softmax states of this work item in LDS ----
-#ifdef MLA_DECODE_DEBUG_STATES
-        if (g == 0) {
-            a.part_ml[((long long)(w * WAVES + wave) * 16 + n) * 2] = m_run;
-            a.part_ml[((long long)(w * WAVES + wave) * 16 + n) * 2 + 1] = l_run;
-        }
-#endif
         if (g == 0) {
             sm_m[wave][n] = m_run;
             sm_l[wave][n] = l_run;
@@ -246,7 +263,7 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
                         acc[rt] * f;
         }
         __syncthreads();
-        for (int e = tid; e < a.H * (KV / 4); e += 64 * WAVES) {
+        for (int e = tid; e < a.H * (KV / 4); e += THREADS) {
             const int h = e / (KV / 4), c = (e % (KV / 4)) * 4;
             float mh = -INFINITY;
 #pragma unroll
@@ -266,53 +283,10 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
                 if (a.lse && c == 0)
                     a.lse[(long long)row * a.H + h] = (mh + __log2f(lh)) * kLn2;
             } else {
-                // Partials cross workgroups (and XCDs, whose L2s are not coherent with
-                // each other): write them with device-coherent stores.
-                float* po = a.part_o + ((long long)w * a.H + h) * KV + c;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    store_coherent(po + i, o[i]);
+                *reinterpret_cast<floatx4*>(a.part_o + ((long long)w * a.H + h) * KV + c) = o;
                 if (c == 0) {
-                    store_coherent(a.part_ml + ((long long)w * a.H + h) * 2, mh);
-                    store_coherent(a.part_ml + ((long long)w * a.H + h) * 2 + 1, lh);
-                }
-            }
-        }
-        if (ns > 1) {
-            // ---- the last workgroup of the session merges every split ----
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are complete
-            __syncthreads();
-            if (tid == 0) {
-                const int old = __hip_atomic_fetch_add(a.counters + s, 1, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT);
-                sm_last = old == ns - 1;
-                if (old == ns - 1)
-                    __hip_atomic_store(a.counters + s, 0, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __syncthreads();
-            if (sm_last) {
-                const int w0 = a.cu_splits[s];
-                for (int e = tid; e < a.H * (KV / 4); e += 64 * WAVES) {
-                    const int h = e / (KV / 4), c = (e % (KV / 4)) * 4;
-                    float mh = -INFINITY;
-                    for (int i = 0; i < ns; ++i)
-                        mh = fmaxf(mh, load_coherent(a.part_ml + ((long long)(w0 + i) * a.H + h) * 2));
-                    float lh = 0.0f;
-                    floatx4 o = {0, 0, 0, 0};
-                    for (int i = 0; i < ns; ++i) {
-                        const long long idx = (long long)(w0 + i) * a.H + h;
-                        const float mv = load_coherent(a.part_ml + idx * 2);
-                        const float f = mv == -INFINITY ? 0.0f : exp2_fast(mv - mh);
-                        lh += f * load_coherent(a.part_ml + idx * 2 + 1);
-                        const float* po = a.part_o + idx * KV + c;
-                        o += f * floatx4{load_coherent(po), load_coherent(po + 1),
-                                         load_coherent(po + 2), load_coherent(po + 3)};
-                    }
-                    const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
-                    *reinterpret_cast<floatx4*>(a.out + ((long long)row * a.H + h) * KV + c) = o * inv;
-                    if (a.lse && c == 0)
-                        a.lse[(long long)row * a.H + h] = (mh + __log2f(lh)) * kLn2;
+                    a.part_ml[((long long)w * a.H + h) * 2] = mh;
+                    a.part_ml[((long long)w * a.H + h) * 2 + 1] = lh;
                 }
             }
         }
@@ -450,38 +424,94 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
 }
 
 // --------------------------------------------------------------- merge ----
-// Log-sum-exp combine of a session's split partials (log2 domain).
-__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+// Log-sum-exp combine of a session's split partials (log2 domain).  One block per
+// (session, head); every split's (max, sum) is fetched in parallel into LDS, then
+// each thread sums its columns over the splits with kMergeUnroll loads in flight.
+constexpr int kMergeThreads = 128;
+constexpr int kMergeUnroll = 8;
+
+__global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
+    __shared__ float f_s[kMergeThreads];
+    __shared__ float red[kMergeThreads / 64 * 2];
+    __shared__ float m_all, l_all;
     const int W = a.info[0];
     if (W <= 0)
         return;
-    for (int s = blockIdx.x; s < a.B; s += gridDim.x) {
+    const int tid = threadIdx.x, KV = a.kv_rank;
+    for (int sh = blockIdx.x; sh < a.B * a.H; sh += gridDim.x) {
+        const int s = sh / a.H, h = sh % a.H;
         const int row = a.cu_q[s];
         const int ns = a.num_splits[s];
         if (a.cu_q[s + 1] - row != 1 || ns <= 1)
             continue;
         const int w0 = a.cu_splits[s];
-        for (int e = threadIdx.x; e < a.H * a.kv_rank; e += 256) {
-            const int h = e / a.kv_rank, r = e % a.kv_rank;
-            float m = -INFINITY;
-            for (int i = 0; i < ns; ++i)
-                m = fmaxf(m, a.part_ml[((long long)(w0 + i) * a.H + h) * 2]);
-            float l = 0.0f, o = 0.0f;
-            for (int i = 0; i < ns; ++i) {
-                const long long idx = (long long)(w0 + i) * a.H + h;
-                const float f = m == -INFINITY ? 0.0f : exp2_fast(a.part_ml[idx * 2] - m);
-                l += f * a.part_ml[idx * 2 + 1];
-                o += f * a.part_o[idx * a.kv_rank + r];
+        float* o_row = a.out + ((long long)row * a.H + h) * KV;
+        // Global max and denominator over the splits.
+        float mloc = -INFINITY;
+        for (int i = tid; i < ns; i += kMergeThreads)
+            mloc = fmaxf(mloc, a.part_ml[((long long)(w0 + i) * a.H + h) * 2]);
+        mloc = wave_max(mloc);
+        if ((tid & 63) == 0)
+            red[tid >> 6] = mloc;
+        __syncthreads();
+        if (tid == 0) {
+            float m = red[0];
+            for (int v = 1; v < kMergeThreads / 64; ++v)
+                m = fmaxf(m, red[v]);
+            m_all = m;
+        }
+        __syncthreads();
+        const float M = m_all;
+        float lloc = 0.0f;
+        for (int i = tid; i < ns; i += kMergeThreads) {
+            const long long idx = (long long)(w0 + i) * a.H + h;
+            const float mv = a.part_ml[idx * 2];
+            lloc += mv == -INFINITY ? 0.0f : a.part_ml[idx * 2 + 1] * exp2_fast(mv - M);
+        }
+        lloc = wave_sum(lloc);
+        if ((tid & 63) == 0)
+            red[kMergeThreads / 64 + (tid >> 6)] = lloc;
+        __syncthreads();
+        if (tid == 0) {
+            float l = 0.0f;
+            for (int v = 0; v < kMergeThreads / 64; ++v)
+                l += red[kMergeThreads / 64 + v];
+            l_all = l;
+        }
+        __syncthreads();
+        const float inv = l_all > 0.0f ? 1.0f / l_all : 0.0f;
+        if (a.lse && tid == 0)
+            a.lse[(long long)row * a.H + h] = (M + __log2f(l_all)) * kLn2;
+        for (int i0 = 0; i0 < ns; i0 += kMergeThreads) {
+            const int cnt = min(kMergeThreads, ns - i0);
+            if (tid < cnt) {
+                const float mv = a.part_ml[((long long)(w0 + i0 + tid) * a.H + h) * 2];
+                f_s[tid] = mv == -INFINITY ? 0.0f : exp2_fast(mv - M) * inv;
             }
-            a.out[((long long)row * a.H + h) * a.kv_rank + r] = l > 0.0f ? o / l : 0.0f;
-            if (a.lse && r == 0)
-                a.lse[(long long)row * a.H + h] = (m + __log2f(l)) * kLn2;
+            __syncthreads();
+            for (int r = tid; r < KV; r += kMergeThreads) {
+                float o = i0 == 0 ? 0.0f : o_row[r];
+                for (int j0 = 0; j0 < cnt; j0 += kMergeUnroll) {
+                    float v[kMergeUnroll];
+#pragma unroll
+                    for (int j = 0; j < kMergeUnroll; ++j)
+                        v[j] = j0 + j < cnt
+                                   ? a.part_o[((long long)(w0 + i0 + j0 + j) * a.H + h) * KV + r]
+                                   : 0.0f;
+#pragma unroll
+                    for (int j = 0; j < kMergeUnroll; ++j)
+                        if (j0 + j < cnt)
+                            o += f_s[j0 + j] * v[j];
+                }
+                o_row[r] = o;
+            }
+            __syncthreads();
         }
     }
 }
 
 #ifndef MLA_DECODE_WAVES
-#define MLA_DECODE_WAVES 8
+#define MLA_DECODE_WAVES 4
 #endif
 constexpr int kMfmaWaves = MLA_DECODE_WAVES;
 
@@ -507,8 +537,7 @@ hipError_t launch_decode(const DecodeArgs& a, int dtype, bool force_generic, hip
     const int grid = a.max_work < 65535 ? a.max_work : 65535;
     hipError_t err;
     if (!force_generic && decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size)) {
-        // The MFMA kernel merges split partials itself (no merge launch).
-        return dtype == 0 ? launch_mfma<F16>(a, grid, stream) : launch_mfma<BF16>(a, grid, stream);
+        err = dtype == 0 ? launch_mfma<F16>(a, grid, stream) : launch_mfma<BF16>(a, grid, stream);
     } else {
         const size_t shmem = (a.kv_rank + a.rope_dim + kGenChunk + 8) * sizeof(float);
         const dim3 g(grid, a.H);
@@ -520,8 +549,9 @@ hipError_t launch_decode(const DecodeArgs& a, int dtype, bool force_generic, hip
     }
     if (err != hipSuccess)
         return err;
-    const int mgrid = a.B < 4096 ? a.B : 4096;
-    hipLaunchKernelGGL(merge_kernel, dim3(mgrid), dim3(256), 0, stream, a);
+    const long long pairs = (long long)a.B * a.H;
+    const int mgrid = pairs < 65535 ? (int)pairs : 65535;
+    hipLaunchKernelGGL(merge_kernel, dim3(mgrid), dim3(kMergeThreads), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -26,8 +26,7 @@ struct AppendArgs {
 
 // Absorbed decode attention.  Partials live in the workspace:
 //   part_o [max_work][H][kv_rank] fp32 (unnormalised), part_ml [max_work][H][2]
-//   (running max in log2 units, running denominator), counters [B] int32
-//   (per-session arrival counters of the fused split merge; zero between calls).
+//   (running max in log2 units, running denominator).
 struct DecodeArgs {
     int B, H, kv_rank, rope_dim, page_size, max_pages, num_pool_pages, max_work;
     float scale_log2;  // softmax scale * log2(e)
@@ -35,7 +34,6 @@ struct DecodeArgs {
         *work_split, *info;
     const uint16_t *pages, *q_latent, *q_rope;
     float *out, *lse, *part_o, *part_ml;
-    int* counters;
 };
 
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);

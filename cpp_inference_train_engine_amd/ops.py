@@ -121,7 +121,7 @@ def decode_workspace_bytes(max_work: int, max_sessions: int, n_heads: int, kv_ra
 
 def decode_workspace(max_work: int, max_sessions: int, n_heads: int, kv_rank: int,
                      device="cuda"):
-    """Zero-filled decode workspace (split partials + per-session merge counters)."""
+    """Decode workspace (split partials)."""
     torch = _torch()
     n = max(decode_workspace_bytes(max_work, max_sessions, n_heads, kv_rank), 4)
     return torch.zeros(n, dtype=torch.uint8, device=device)

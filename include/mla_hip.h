@@ -120,12 +120,12 @@ int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_s
  * `dtype` (the MPS graph keeps q_latent in the storage dtype,
  * mps_backend.mm:561).  out [rows x H x kv_rank] fp32, lse [rows x H] fp32
  * (may be NULL).  Rows of sessions with q_len != 1 are not written.
- * Work is split over the metadata's work items (split-K over pages) and
- * merged with a log-sum-exp combine inside the same launch.  `workspace`
- * (device) must hold mla_decode_workspace_bytes(max_work, B, H, kv_rank)
- * bytes and be ZERO-FILLED before its first use: it carries per-session
- * arrival counters that every completed call leaves at zero again.  Calls
- * that share a workspace must be ordered on one stream. */
+ * Work is split over the metadata's work items (split-K over pages); the
+ * split partials of a session are merged with a log-sum-exp combine by a
+ * second launch on the same stream.  `workspace` (device) must hold
+ * mla_decode_workspace_bytes(max_work, B, H, kv_rank) bytes (partials; no
+ * initialisation needed).  Calls that share a workspace must be ordered on
+ * one stream. */
 size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, int kv_rank);
 int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
                          int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,

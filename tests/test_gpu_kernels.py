@@ -255,8 +255,8 @@ def test_decode_skips_prefill_rows_and_tolerates_garbage_slots(gpu, orc):
 
 
 def test_decode_workspace_reuse_across_calls(gpu, orc):
-    """The fused split merge leaves its per-session counters at zero: one zeroed workspace
-    serves consecutive calls with different batches, layers and split sizes."""
+    """One workspace serves consecutive calls with different batches, layers and split
+    sizes (stale partials of an earlier call never leak into a later one)."""
     import torch
     from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
     ws = gpu.decode_workspace(4096, 64, 8, 128)
@@ -274,5 +274,3 @@ def test_decode_workspace_reuse_across_calls(gpu, orc):
             torch.cuda.synchronize()
             want, _ = _oracle_decode(orc, batch, layer=layer)
             _check(out.cpu().numpy(), want, f"seed={seed} split={split} layer={layer}")
-    counters = ws[-64 * 4:].view(torch.int32).cpu().numpy()
-    assert np.all(counters == 0)

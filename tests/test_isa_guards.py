@@ -2,9 +2,7 @@
 
 MFMA instructions must not have a destination that partially overlaps their
 accumulator input (identical or disjoint only): such a register assignment
-corrupted the decode kernel's scores.  The decode kernel must also stay spill-
-free enough to keep its occupancy, and device-coherent partial traffic must use
-sc1 accesses.
+corrupted the decode kernel's scores.
 """
 import glob
 import os
@@ -65,9 +63,3 @@ def test_overlap_checker_flags_the_bad_form():
                          ids=os.path.basename)
 def test_no_mfma_partial_dst_src_overlap(src, tmp_path):
     assert mfma_partial_overlaps(_asm(src, tmp_path)) == []
-
-
-def test_decode_partials_use_coherent_accesses(tmp_path):
-    asm = _asm(os.path.join(CSRC, "decode.hip"), tmp_path)
-    assert re.search(r"global_store_dword .* sc1", asm)
-    assert re.search(r"global_load_dword .* sc1", asm)
