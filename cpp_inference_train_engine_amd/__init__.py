@@ -18,6 +18,7 @@ MLA_OK = 0
 ERROR_NAMES = {1: "invalid_argument", 2: "io_error", 3: "unsupported", 4: "out_of_memory",
                5: "gpu_error", 6: "numerical_error"}
 DTYPE_F16, DTYPE_BF16 = 0, 1
+WORK_DESC_INTS, WORK_PAGES, MAX_WORK = 8, 8, 65535
 DECODE_FORCE_GENERIC = 1
 
 
@@ -36,13 +37,13 @@ _SIGNATURES = {
     "mla_last_error": (C.c_char_p, []),
     "mla_abi_version": (C.c_int, []),
     "mla_build_metadata": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 4 +
-                           [C.c_int] * 7 + [C.c_void_p] * 9),
+                           [C.c_int] * 7 + [C.c_void_p] * 11),
     "mla_read_metadata_info": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "mla_append_latent": (C.c_int, [C.c_void_p] + [C.c_int] * 5 + [C.c_void_p] * 3 +
                           [C.c_int, C.c_void_p]),
     "mla_decode_workspace_bytes": (C.c_size_t, [C.c_int] * 4),
     "mla_decode_attention": (C.c_int, [C.c_void_p] + [C.c_int] * 6 + [C.c_float] +
-                             [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_void_p] * 8 +
+                             [C.c_void_p] * 2 + [C.c_int] * 2 + [C.c_void_p] * 8 +
                              [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
                               C.c_int]),
 }

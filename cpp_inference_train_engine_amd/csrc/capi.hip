@@ -39,20 +39,22 @@ int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_
                        int max_work, int max_rows, int32_t* cu_seqlens_q,
                        int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
                        int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
-                       int32_t* work_split, int32_t* info) {
+                       int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
+                       int32_t* info) {
     if (B < 0 || page_size < 1 || max_pages < 0 || num_pool_pages < 0 || split_pages < 0 ||
-        target_blocks < 1 || max_work < 0 || max_rows < 0)
+        target_blocks < 1 || max_work < 0 || max_work > kMaxWork || max_rows < 0)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: invalid scalar argument");
     if (!info || !cu_seqlens_q || !cu_seqlens_k || !cu_splits || !cu_pages ||
         (B > 0 && (!ctx_len || !q_len || !num_splits || (max_pages > 0 && !page_table))) ||
-        (max_work > 0 && (!work_session || !work_split)) || (max_rows > 0 && !slot_mapping))
+        (max_work > 0 && (!work_session || !work_split || !work_desc || !work_pages)) ||
+        (max_rows > 0 && !slot_mapping))
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: null buffer");
     if ((long long)B * max_pages > (1LL << 40))
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: page table too large");
     MetadataArgs a{B, ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num_pool_pages,
                    split_pages, target_blocks, max_work, max_rows, cu_seqlens_q, cu_seqlens_k,
                    page_table, slot_mapping, num_splits, cu_splits, work_session, work_split,
-                   info};
+                   work_desc, work_pages, info};
     return gpu_status(launch_build_metadata(a, static_cast<hipStream_t>(stream)),
                       "mla_build_metadata");
 }
@@ -103,21 +105,21 @@ size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, i
 
 int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
                          int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
-                         const int32_t* cu_seqlens_k, const int32_t* page_table, int max_pages,
-                         int num_pool_pages, const void* pages, const void* q_latent,
-                         const void* q_rope, const int32_t* num_splits, const int32_t* cu_splits,
-                         const int32_t* work_session, const int32_t* work_split,
-                         const int32_t* info, int max_work, float* out, float* lse,
-                         void* workspace, size_t workspace_bytes, int flags) {
+                         const int32_t* page_table, int max_pages, int num_pool_pages,
+                         const void* pages, const void* q_latent, const void* q_rope,
+                         const int32_t* num_splits, const int32_t* cu_splits,
+                         const int32_t* work_desc, const int32_t* work_pages, const int32_t* info,
+                         int max_work, float* out, float* lse, void* workspace,
+                         size_t workspace_bytes, int flags) {
     if (B < 0 || n_heads < 1 || kv_rank < 1 || kv_rank > 1024 || rope_dim < 0 || rope_dim > 1024 ||
         page_size < 1 || max_pages < 0 || num_pool_pages < 0 || max_work < 0 ||
+        max_work > kMaxWork ||
         (dtype != MLA_DTYPE_F16 && dtype != MLA_DTYPE_BF16) || !(scale > 0.0f))
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: invalid argument");
     if (B == 0 || max_work == 0)
         return MLA_OK;
-    if (!cu_seqlens_q || !cu_seqlens_k || !page_table || !pages || !q_latent ||
-        (rope_dim > 0 && !q_rope) || !num_splits || !cu_splits || !work_session ||
-        !work_split || !info || !out)
+    if (!cu_seqlens_q || !page_table || !pages || !q_latent || (rope_dim > 0 && !q_rope) ||
+        !num_splits || !cu_splits || !work_desc || !work_pages || !info || !out)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: null buffer");
     const size_t need = mla_decode_workspace_bytes(max_work, B, n_heads, kv_rank);
     if (!workspace || workspace_bytes < need)
@@ -135,12 +137,11 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
     a.max_work = max_work;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.cu_q = cu_seqlens_q;
-    a.cu_k = cu_seqlens_k;
     a.page_table = page_table;
     a.num_splits = num_splits;
     a.cu_splits = cu_splits;
-    a.work_session = work_session;
-    a.work_split = work_split;
+    a.work_desc = work_desc;
+    a.work_pages = work_pages;
     a.info = info;
     a.pages = static_cast<const uint16_t*>(pages);
     a.q_latent = static_cast<const uint16_t*>(q_latent);

@@ -180,25 +180,21 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
-    const int W = a.info[0];
-    if (W <= 0)
-        return;
-    const int split = a.info[1];
     const long long rec = (long long)PS * (KV + RP);
     const bool head_ok = n < a.H;
     uint16_t* myl = lds[wave];
     float* mb = reinterpret_cast<float*>(&lds[0][0]);  // [WAVES][16][MSTRIDE] after the loop
 
-    for (int w = blockIdx.x; w < W; w += gridDim.x) {
-        const int s = a.work_session[w], sp = a.work_split[w];
-        const int row = a.cu_q[s];
-        if (a.cu_q[s + 1] - row != 1)
-            continue;
-        const int kl = a.cu_k[s + 1] - a.cu_k[s];
-        const int need = (kl + PS - 1) / PS;
-        const int p_begin = sp * split;
-        const int p_end = min(need, p_begin + split);
-        const int ns = a.num_splits[s];
+    for (int w = blockIdx.x; w < a.max_work; w += gridDim.x) {
+        // One descriptor load (plus this wave's first page id) starts the item.
+        const int32_t* d = a.work_desc + (long long)w * kWorkDescInts;
+        const int page0 = wave < kWorkPages ? a.work_pages[(long long)w * kWorkPages + wave] : -1;
+        const int s = d[0];
+        if (s < 0)
+            break;  // items past the last one are all marked empty
+        if (d[7] != 1)
+            continue;  // not a decode row
+        const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
 
         // Q^T operands (B of S^T): lane (g, n) = head n.
         V8 bq[KS], bqr[RS];
@@ -226,7 +222,8 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
             acc[r] = floatx4{0, 0, 0, 0};
 
         for (int p = p_begin + wave; p < p_end; p += WAVES) {
-            const int page = a.page_table[(long long)s * a.max_pages + p];
+            const int page = p == p_begin + wave ? page0
+                                                  : a.page_table[(long long)s * a.max_pages + p];
             if ((unsigned)page >= (unsigned)a.num_pool_pages)
                 continue;
             const uint16_t* base = a.pages + page * rec;
@@ -331,20 +328,16 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
     float* sc = smem + a.kv_rank + a.rope_dim;  // kGenChunk
     float* red = sc + kGenChunk;              // 4
     const int tid = threadIdx.x, h = blockIdx.y;
-    const int W = a.info[0];
-    if (W <= 0)
-        return;
-    const int split = a.info[1];
     const int KV = a.kv_rank, RP = a.rope_dim, PS = a.page_size;
     const long long rec = (long long)PS * (KV + RP);
-    for (int w = blockIdx.x; w < W; w += gridDim.x) {
-        const int s = a.work_session[w], sp = a.work_split[w];
-        const int row = a.cu_q[s];
-        if (a.cu_q[s + 1] - row != 1)
+    for (int w = blockIdx.x; w < a.max_work; w += gridDim.x) {
+        const int32_t* d = a.work_desc + (long long)w * kWorkDescInts;
+        const int s = d[0];
+        if (s < 0)
+            break;
+        if (d[7] != 1)
             continue;
-        const int kl = a.cu_k[s + 1] - a.cu_k[s];
-        const int need = (kl + PS - 1) / PS;
-        const int p_begin = sp * split, p_end = min(need, p_begin + split);
+        const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
         const int t_begin = p_begin * PS, t_end = min(kl, p_end * PS);
         for (int i = tid; i < KV + RP; i += kGenThreads)
             qs[i] = i < KV ? T::to_float(a.q_latent[((long long)row * a.H + h) * KV + i])
@@ -399,7 +392,7 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
             }
             __syncthreads();
         }
-        if (a.num_splits[s] == 1) {
+        if (ns == 1) {
             const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
             for (int k = 0; k < kGenMaxAcc; ++k) {
                 const int r = tid + k * kGenThreads;
@@ -434,17 +427,16 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
     __shared__ float f_s[kMergeThreads];
     __shared__ float red[kMergeThreads / 64 * 2];
     __shared__ float m_all, l_all;
-    const int W = a.info[0];
-    if (W <= 0)
-        return;
+    if (a.info[0] <= 0)
+        return;  // empty or invalid batch: the metadata arrays are not meaningful
     const int tid = threadIdx.x, KV = a.kv_rank;
     for (int sh = blockIdx.x; sh < a.B * a.H; sh += gridDim.x) {
         const int s = sh / a.H, h = sh % a.H;
         const int row = a.cu_q[s];
         const int ns = a.num_splits[s];
-        if (a.cu_q[s + 1] - row != 1 || ns <= 1)
-            continue;
         const int w0 = a.cu_splits[s];
+        if (a.cu_q[s + 1] - row != 1 || ns <= 1 || w0 < 0 || w0 + ns > a.max_work)
+            continue;
         float* o_row = a.out + ((long long)row * a.H + h) * KV;
         // Global max and denominator over the splits.
         float mloc = -INFINITY;
@@ -534,7 +526,7 @@ bool decode_mfma_supported(int H, int kv_rank, int rope_dim, int page_size) {
 hipError_t launch_decode(const DecodeArgs& a, int dtype, bool force_generic, hipStream_t stream) {
     if (a.max_work <= 0 || a.B <= 0)
         return hipSuccess;
-    const int grid = a.max_work < 65535 ? a.max_work : 65535;
+    const int grid = a.max_work;  // <= kMaxWork
     hipError_t err;
     if (!force_generic && decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size)) {
         err = dtype == 0 ? launch_mfma<F16>(a, grid, stream) : launch_mfma<BF16>(a, grid, stream);

@@ -63,18 +63,45 @@ __device__ int upper_index(const int32_t* a, int n, long long x) {
     return lo;
 }
 
+// Prefix arrays are mirrored in LDS for batches up to kMetaLdsCap sessions so the
+// per-entry lookups and binary searches below never wait on global memory.
+constexpr int kMetaLdsCap = 4096;
+
+__device__ void write_error(const MetadataArgs& a, int session) {
+    for (int w = threadIdx.x; w < a.max_work; w += kMetaThreads)
+        a.work_desc[(long long)w * kWorkDescInts] = -1;
+    if (threadIdx.x == 0) {
+        a.info[0] = -1;
+        a.info[1] = session;
+        a.info[2] = 0;
+        a.info[3] = 0;
+    }
+}
+
 __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataArgs a) {
     __shared__ long long lds[3 * kMetaWaves];
     __shared__ long long carry[3];
     __shared__ int err;
+    __shared__ int32_t s_cup[kMetaLdsCap + 1], s_cuq[kMetaLdsCap + 1], s_cus[kMetaLdsCap + 1];
     const int tid = threadIdx.x;
+    const bool in_lds = a.B <= kMetaLdsCap;
+    const int32_t* cup = in_lds ? s_cup : a.cu_pages;
+    const int32_t* cuq = in_lds ? s_cuq : a.cu_seqlens_q;
+    const int32_t* cus = in_lds ? s_cus : a.cu_splits;
     if (tid == 0) {
         carry[0] = carry[1] = carry[2] = 0;
         err = INT_MAX;
         a.cu_seqlens_q[0] = 0;
         a.cu_seqlens_k[0] = 0;
         a.cu_splits[0] = 0;
+        if (in_lds) {
+            s_cuq[0] = 0;
+            s_cus[0] = 0;
+        }
     }
+    if (in_lds)
+        for (int b = tid; b <= a.B; b += kMetaThreads)
+            s_cup[b] = a.cu_pages[b];
     __syncthreads();
     // Phase 1: cu_seqlens_q/k, validation, total pages of sessions with queries.
     for (int base = 0; base < a.B; base += kMetaThreads) {
@@ -83,7 +110,7 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         int bad = 0;
         if (b < a.B) {
             const long long q = a.q_len[b], ctx = a.ctx_len[b];
-            const long long npages = (long long)a.cu_pages[b + 1] - a.cu_pages[b];
+            const long long npages = (long long)cup[b + 1] - cup[b];
             const long long kl = ctx + q;
             const long long need = (kl + a.page_size - 1) / a.page_size;
             bad = q < 0 || ctx < 0 || npages < 0 || npages > a.max_pages || need > npages;
@@ -98,6 +125,8 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
                 atomicMin(&err, b);
             a.cu_seqlens_q[b + 1] = (int32_t)iq;
             a.cu_seqlens_k[b + 1] = (int32_t)ik;
+            if (in_lds)
+                s_cuq[b + 1] = (int32_t)iq;
         }
         __syncthreads();
         if (tid == 0)
@@ -106,15 +135,15 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         __syncthreads();
     }
     // Phase 1b: padded page table and page-id validation, one entry per thread
-    // (independent loads; a session listing more than max_pages pages is
-    // already invalid and only its first max_pages ids are read).
+    // (a session listing more than max_pages pages is already invalid and only its
+    // first max_pages ids are read).
     const long long entries = (long long)a.B * a.max_pages;
     for (long long e = tid; e < entries; e += kMetaThreads) {
         const int b = (int)(e / a.max_pages), j = (int)(e % a.max_pages);
-        const int npages = a.cu_pages[b + 1] - a.cu_pages[b];
+        const int npages = cup[b + 1] - cup[b];
         int32_t pid = -1;
         if (j < npages) {
-            pid = a.page_ids[a.cu_pages[b] + j];
+            pid = a.page_ids[cup[b] + j];
             if (pid < 0 || pid >= a.num_pool_pages)
                 atomicMin(&err, b);
         }
@@ -122,12 +151,7 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
     }
     __syncthreads();
     if (err != INT_MAX) {
-        if (tid == 0) {
-            a.info[0] = -1;
-            a.info[1] = err;
-            a.info[2] = 0;
-            a.info[3] = 0;
-        }
+        write_error(a, err);
         return;
     }
     const long long total_q = carry[0], total_k = carry[1], total_pages = carry[2];
@@ -158,6 +182,8 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
                 atomicMin(&err, b);
             a.num_splits[b] = (int32_t)ns;
             a.cu_splits[b + 1] = (int32_t)w;
+            if (in_lds)
+                s_cus[b + 1] = (int32_t)w;
         }
         __syncthreads();
         if (tid == 0)
@@ -165,25 +191,41 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         __syncthreads();
     }
     if (err != INT_MAX) {
-        if (tid == 0) {
-            a.info[0] = -1;
-            a.info[1] = err;
-            a.info[2] = 0;
-            a.info[3] = 0;
-        }
+        write_error(a, err);
         return;
     }
     const long long W = carry[0];
-    // Phase 3: block-to-session map, padded page table, slot mapping.
-    for (long long w = tid; w < W; w += kMetaThreads) {
-        const int b = upper_index(a.cu_splits, a.B, w);
+    // Phase 3: block-to-session map, work descriptors, slot mapping.
+    for (long long w = tid; w < a.max_work; w += kMetaThreads) {
+        int32_t* d = a.work_desc + w * kWorkDescInts;
+        int32_t* pg = a.work_pages + w * kWorkPages;
+        if (w >= W) {
+            d[0] = -1;
+            continue;
+        }
+        const int b = upper_index(cus, a.B, w);
+        const int sp = (int)(w - cus[b]);
+        const int kl = a.ctx_len[b] + a.q_len[b];
+        const int need = (kl + a.page_size - 1) / a.page_size;
+        const int p0 = (int)(sp * split);
+        const int p1 = (int)(p0 + split < need ? p0 + split : need);
         a.work_session[w] = b;
-        a.work_split[w] = (int32_t)(w - a.cu_splits[b]);
+        a.work_split[w] = sp;
+        d[0] = b;
+        d[1] = cuq[b];
+        d[2] = kl;
+        d[3] = p0;
+        d[4] = p1;
+        d[5] = cus[b + 1] - cus[b];
+        d[6] = cus[b];
+        d[7] = a.q_len[b];
+        for (int j = 0; j < kWorkPages; ++j)
+            pg[j] = p0 + j < p1 ? a.page_ids[cup[b] + p0 + j] : -1;
     }
     for (long long i = tid; i < total_q; i += kMetaThreads) {
-        const int b = upper_index(a.cu_seqlens_q, a.B, i);
-        const long long pos = (long long)a.ctx_len[b] + (i - a.cu_seqlens_q[b]);
-        const int32_t page = a.page_ids[a.cu_pages[b] + pos / a.page_size];
+        const int b = upper_index(cuq, a.B, i);
+        const long long pos = (long long)a.ctx_len[b] + (i - cuq[b]);
+        const int32_t page = a.page_ids[cup[b] + pos / a.page_size];
         a.slot_mapping[i] = (int32_t)(page * (long long)a.page_size + pos % a.page_size);
     }
     if (tid == 0) {

@@ -9,12 +9,20 @@
 
 namespace mla {
 
+// Work descriptor of one split-K work item (kWorkDescInts int32):
+//   {session, first query row, k_len, page_begin, page_end, num_splits of the
+//    session, first work item of the session, q_len}; session -1 = no work.
+// work_pages holds the ids of the item's first kWorkPages pages (-1 past the end).
+constexpr int kWorkDescInts = 8;  // MLA_WORK_DESC_INTS
+constexpr int kWorkPages = 8;     // MLA_WORK_PAGES
+constexpr int kMaxWork = 65535;   // MLA_MAX_WORK
+
 struct MetadataArgs {
     int B;
     const int32_t *ctx_len, *q_len, *cu_pages, *page_ids;
     int page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows;
     int32_t *cu_seqlens_q, *cu_seqlens_k, *page_table, *slot_mapping, *num_splits, *cu_splits,
-        *work_session, *work_split, *info;
+        *work_session, *work_split, *work_desc, *work_pages, *info;
 };
 
 struct AppendArgs {
@@ -30,8 +38,7 @@ struct AppendArgs {
 struct DecodeArgs {
     int B, H, kv_rank, rope_dim, page_size, max_pages, num_pool_pages, max_work;
     float scale_log2;  // softmax scale * log2(e)
-    const int32_t *cu_q, *cu_k, *page_table, *num_splits, *cu_splits, *work_session,
-        *work_split, *info;
+    const int32_t *cu_q, *page_table, *num_splits, *cu_splits, *work_desc, *work_pages, *info;
     const uint16_t *pages, *q_latent, *q_rope;
     float *out, *lse, *part_o, *part_ml;
 };

@@ -11,7 +11,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
-from . import DTYPE_BF16, DTYPE_F16, check, lib, ptr, stream_handle
+from . import (DTYPE_BF16, DTYPE_F16, MAX_WORK, WORK_DESC_INTS, WORK_PAGES, check, lib, ptr,
+               stream_handle)
 
 
 def _torch():
@@ -37,6 +38,8 @@ class RaggedBatch:
     cu_splits: object
     work_session: object
     work_split: object
+    work_desc: object
+    work_pages: object
     info: object
     host_info: list = field(default_factory=list)
 
@@ -61,7 +64,7 @@ def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size: int, max_pages
     if max_rows is None:
         max_rows = max(1, 4 * B)
     if max_work is None:
-        max_work = max(1, target_blocks + 2 * B)
+        max_work = max(1, min(MAX_WORK, target_blocks + 2 * B))
     i32 = dict(dtype=torch.int32, device=dev)
     rb = RaggedBatch(
         B=B, page_size=page_size, max_pages=max_pages, num_pool_pages=num_pool_pages,
@@ -70,13 +73,15 @@ def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size: int, max_pages
         page_table=torch.empty(max(1, B * max_pages), **i32),
         slot_mapping=torch.empty(max_rows, **i32), num_splits=torch.empty(max(B, 1), **i32),
         cu_splits=torch.empty(B + 1, **i32), work_session=torch.empty(max_work, **i32),
-        work_split=torch.empty(max_work, **i32), info=torch.empty(4, **i32))
+        work_split=torch.empty(max_work, **i32),
+        work_desc=torch.empty(max_work * WORK_DESC_INTS, **i32),
+        work_pages=torch.empty(max_work * WORK_PAGES, **i32), info=torch.empty(4, **i32))
     check(lib().mla_build_metadata(
         stream_handle(stream), B, ptr(ctx_len), ptr(q_len), ptr(cu_pages), ptr(page_ids),
         page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows,
         ptr(rb.cu_seqlens_q), ptr(rb.cu_seqlens_k), ptr(rb.page_table), ptr(rb.slot_mapping),
         ptr(rb.num_splits), ptr(rb.cu_splits), ptr(rb.work_session), ptr(rb.work_split),
-        ptr(rb.info)))
+        ptr(rb.work_desc), ptr(rb.work_pages), ptr(rb.info)))
     return rb
 
 
@@ -141,11 +146,10 @@ def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, 
         workspace = decode_workspace(batch.max_work, batch.B, H, kv_rank, q_latent.device)
     check(lib().mla_decode_attention(
         stream_handle(stream), batch.B, H, kv_rank, rope_dim, batch.page_size, dtype,
-        float(scale), ptr(batch.cu_seqlens_q), ptr(batch.cu_seqlens_k), ptr(batch.page_table),
-        batch.max_pages, batch.num_pool_pages, ptr(pages), ptr(q_latent), ptr(q_rope),
-        ptr(batch.num_splits), ptr(batch.cu_splits), ptr(batch.work_session),
-        ptr(batch.work_split), ptr(batch.info), batch.max_work, ptr(out), ptr(lse),
-        ptr(workspace), int(workspace.numel()), flags))
+        float(scale), ptr(batch.cu_seqlens_q), ptr(batch.page_table), batch.max_pages,
+        batch.num_pool_pages, ptr(pages), ptr(q_latent), ptr(q_rope), ptr(batch.num_splits),
+        ptr(batch.cu_splits), ptr(batch.work_desc), ptr(batch.work_pages), ptr(batch.info),
+        batch.max_work, ptr(out), ptr(lse), ptr(workspace), int(workspace.numel()), flags))
     return out
 
 

@@ -71,12 +71,18 @@ int mla_abi_version(void);
  * physical page lists.  Scalars: page_size, max_pages (columns of the padded
  * table), num_pool_pages (valid page ids are [0, num_pool_pages)),
  * split_pages (>0 fixed pages per work item; 0 = auto, ceil(total pages of
- * sessions with q_len>0 / target_blocks)), max_work / max_rows capacities.
+ * sessions with q_len>0 / target_blocks)), max_work (<= MLA_MAX_WORK) and
+ * max_rows capacities.
  * Outputs (device): cu_seqlens_q[B+1], cu_seqlens_k[B+1],
  * page_table[B * max_pages] (-1 padded), slot_mapping[max_rows] (flat slot
  * page*page_size+offset of every appended token), num_splits[B],
  * cu_splits[B+1], work_session[max_work], work_split[max_work] (the
- * block-to-session map) and info[4]:
+ * block-to-session map), work_desc[max_work * MLA_WORK_DESC_INTS] (per work
+ * item: session, first query row, k_len, page_begin, page_end, num_splits of
+ * the session, first work item of the session, q_len; session -1 marks every
+ * item past the last one, and all items of a failed build),
+ * work_pages[max_work * MLA_WORK_PAGES] (ids of each item's first pages, -1
+ * past its end) and info[4]:
  *     ok:    {W (work items), split_pages used, total_q, total_k}
  *     error: {-1, first offending session, 0, 0}
  * A session is invalid when q_len<0, ctx_len<0, it lists more than
@@ -85,13 +91,17 @@ int mla_abi_version(void);
  * exceeded.  Errors are reported through info (read it with
  * mla_read_metadata_info); every consumer kernel treats info[0] < 0 as an
  * empty batch. */
+#define MLA_WORK_DESC_INTS 8
+#define MLA_WORK_PAGES 8
+#define MLA_MAX_WORK 65535
 int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
                        int max_pages, int num_pool_pages, int split_pages, int target_blocks,
                        int max_work, int max_rows, int32_t* cu_seqlens_q,
                        int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
                        int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
-                       int32_t* work_split, int32_t* info);
+                       int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
+                       int32_t* info);
 
 /* Synchronises `stream`, copies info[4] to host_info and returns
  * MLA_ERR_INVALID_ARGUMENT (naming the session) if the build failed. */
@@ -127,14 +137,17 @@ int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_s
  * initialisation needed).  Calls that share a workspace must be ordered on
  * one stream. */
 size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, int kv_rank);
+/* The metadata arguments (cu_seqlens_q, page_table, num_splits, cu_splits,
+ * work_desc, work_pages, info, max_work) are the outputs of one
+ * mla_build_metadata call for this batch. */
 int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
                          int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
-                         const int32_t* cu_seqlens_k, const int32_t* page_table, int max_pages,
-                         int num_pool_pages, const void* pages, const void* q_latent,
-                         const void* q_rope, const int32_t* num_splits, const int32_t* cu_splits,
-                         const int32_t* work_session, const int32_t* work_split,
-                         const int32_t* info, int max_work, float* out, float* lse,
-                         void* workspace, size_t workspace_bytes, int flags);
+                         const int32_t* page_table, int max_pages, int num_pool_pages,
+                         const void* pages, const void* q_latent, const void* q_rope,
+                         const int32_t* num_splits, const int32_t* cu_splits,
+                         const int32_t* work_desc, const int32_t* work_pages, const int32_t* info,
+                         int max_work, float* out, float* lse, void* workspace,
+                         size_t workspace_bytes, int flags);
 
 #ifdef __cplusplus
 }

@@ -81,8 +81,8 @@ def _declare(L):
         "orc_output_projection": (None, [vp, vp, vp]),
         "orc_decode": (i, [vp, vp, vp, vp, vp, i, C.c_uint16, i, i, vp]),
         "orc_attention_paged": (i, [i, i, i, i, i, i, vp, vp, vp, i, vp, vp, vp, f, vp, vp]),
-        "orc_build_metadata": (i, [i, vp, vp, vp, vp, i, i, i, i, i, i,
-                                   vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+        "orc_build_metadata": (i, [i, vp, vp, vp, vp, i, i, i, i, i, i, i,
+                                   vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
         "orc_append_paged": (None, [i, i, i, i, i, vp, vp, vp, vp]),
         "orc_greedy": (i, [vp, i, vp, i, f, vp, i]),
     }
@@ -247,7 +247,7 @@ def attention_paged(H, kv_rank, rope_dim, page_size, dtype, cu_q, k_len, page_ta
 
 
 def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num_pool_pages,
-                   split_pages=0, target_blocks=512, max_work=1 << 20):
+                   split_pages=0, target_blocks=512, max_work=65535, max_rows=1 << 30):
     ctx_len = np.ascontiguousarray(ctx_len, np.int32)
     q_len = np.ascontiguousarray(q_len, np.int32)
     cu_pages = np.ascontiguousarray(cu_pages, np.int32)
@@ -259,15 +259,17 @@ def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num
         page_table=np.zeros((B, max_pages), np.int32), slot_mapping=np.zeros(total_q, np.int32),
         num_splits=np.zeros(B, np.int32), cu_splits=np.zeros(B + 1, np.int32),
         work_session=np.zeros(max_work, np.int32), work_split=np.zeros(max_work, np.int32),
+        work_desc=np.zeros((max_work, 8), np.int32), work_pages=np.zeros((max_work, 8), np.int32),
         info=np.zeros(4, np.int32))
     st = lib().orc_build_metadata(
         B, _p(ctx_len), _p(q_len), _p(cu_pages), _p(page_ids if page_ids.size else
                                                     np.zeros(1, np.int32)),
-        page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work,
+        page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows,
         *(_p(out[k]) for k in ("cu_seqlens_q", "cu_seqlens_k", "page_table", "slot_mapping",
-                               "num_splits", "cu_splits", "work_session", "work_split", "info")))
+                               "num_splits", "cu_splits", "work_session", "work_split",
+                               "work_desc", "work_pages", "info")))
     if st:
-        raise ValueError(f"invalid metadata input (session {int(out['info'][0])})")
+        raise ValueError(f"invalid metadata input (session {int(out['info'][1])})")
     W = int(out["info"][0])
     out["work_session"] = out["work_session"][:W]
     out["work_split"] = out["work_split"][:W]

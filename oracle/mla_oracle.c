@@ -657,17 +657,24 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
 /* ------------------------------------------------------------------------ */
 /* Ragged batch metadata (new)                                               */
 /* ------------------------------------------------------------------------ */
+static int metadata_error(int max_work, int32_t* work_desc, int32_t* info, int session) {
+    for (int w = 0; w < max_work; ++w)
+        work_desc[(size_t)w * 8] = -1;
+    info[0] = -1;
+    info[1] = session;
+    info[2] = info[3] = 0;
+    return 1;
+}
+
 int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
                        int max_pages, int num_pool_pages, int split_pages, int target_blocks,
-                       int max_work, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                       int max_work, int max_rows, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
                        int32_t* page_table, int32_t* slot_mapping, int32_t* num_splits,
                        int32_t* cu_splits, int32_t* work_session, int32_t* work_split,
-                       int32_t* info) {
-    if (B < 0 || page_size < 1 || max_pages < 0 || split_pages < 0 || target_blocks < 1) {
-        info[0] = -1;
-        return 1;
-    }
+                       int32_t* work_desc, int32_t* work_pages, int32_t* info) {
+    if (B < 0 || page_size < 1 || max_pages < 0 || split_pages < 0 || target_blocks < 1)
+        return metadata_error(max_work, work_desc, info, -1);
     long long total_q = 0, total_k = 0, total_pages = 0;
     cu_seqlens_q[0] = 0;
     cu_seqlens_k[0] = 0;
@@ -683,10 +690,8 @@ int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
         }
         total_q += q;
         total_k += kl;
-        if (bad || total_q > INT_MAX || total_k > INT_MAX) {
-            info[0] = b;
-            return 1;
-        }
+        if (bad || total_q > INT_MAX || total_k > INT_MAX || total_q > max_rows)
+            return metadata_error(max_work, work_desc, info, b);
         cu_seqlens_q[b + 1] = (int32_t)total_q;
         cu_seqlens_k[b + 1] = (int32_t)total_k;
         if (q > 0)
@@ -708,16 +713,29 @@ int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
         const long long ns = q_len[b] > 0 ? (need + split - 1) / split : 0;
         num_splits[b] = (int32_t)ns;
         w += ns;
-        if (w > max_work) {
-            info[0] = b;
-            return 1;
-        }
+        if (w > max_work)
+            return metadata_error(max_work, work_desc, info, b);
         cu_splits[b + 1] = (int32_t)w;
     }
     for (int b = 0; b < B; ++b) {
+        const int kl = ctx_len[b] + q_len[b];
+        const int need = (kl + page_size - 1) / page_size;
         for (int s = 0; s < num_splits[b]; ++s) {
-            work_session[cu_splits[b] + s] = b;
-            work_split[cu_splits[b] + s] = s;
+            const int w = cu_splits[b] + s;
+            const int p0 = (int)(s * split), p1 = p0 + split < need ? (int)(p0 + split) : need;
+            int32_t* d = work_desc + (size_t)w * 8;
+            work_session[w] = b;
+            work_split[w] = s;
+            d[0] = b;
+            d[1] = cu_seqlens_q[b];
+            d[2] = kl;
+            d[3] = p0;
+            d[4] = p1;
+            d[5] = num_splits[b];
+            d[6] = cu_splits[b];
+            d[7] = q_len[b];
+            for (int j = 0; j < 8; ++j)
+                work_pages[(size_t)w * 8 + j] = p0 + j < p1 ? page_ids[cu_pages[b] + p0 + j] : -1;
         }
         for (int i = 0; i < q_len[b]; ++i) {
             const int pos = ctx_len[b] + i;
@@ -725,6 +743,8 @@ int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
                 page_table[(size_t)b * max_pages + pos / page_size] * page_size + pos % page_size;
         }
     }
+    for (long long x = w; x < max_work; ++x)
+        work_desc[(size_t)x * 8] = -1;
     info[0] = (int32_t)w;
     info[1] = (int32_t)split;
     info[2] = (int32_t)total_q;

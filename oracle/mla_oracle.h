@@ -103,16 +103,20 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
  * with target_blocks).
  * Outputs (caller-sized): cu_seqlens_q[B+1], cu_seqlens_k[B+1],
  * page_table[B x max_pages] (-1 padded), slot_mapping[total_q],
- * num_splits[B], cu_splits[B+1], work_session[W], work_split[W], info[4] =
- * {W, split_pages, total_q, total_k}.  Returns 0 or 1 (invalid argument) and
- * writes the first offending session to info[0] on error. */
+ * num_splits[B], cu_splits[B+1], work_session[W], work_split[W],
+ * work_desc[max_work x 8] = {session, first query row, k_len, page_begin,
+ * page_end, num_splits, first item of the session, q_len} (session -1 for every
+ * item >= W and for every item of a failed build), work_pages[max_work x 8] =
+ * first 8 page ids of each item (-1 past its end), info[4] =
+ * {W, split_pages, total_q, total_k} or {-1, first offending session, 0, 0}.
+ * Returns 0, or 1 (invalid argument). */
 int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
                        int max_pages, int num_pool_pages, int split_pages, int target_blocks,
-                       int max_work, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                       int max_work, int max_rows, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
                        int32_t* page_table, int32_t* slot_mapping, int32_t* num_splits,
                        int32_t* cu_splits, int32_t* work_session, int32_t* work_split,
-                       int32_t* info);
+                       int32_t* work_desc, int32_t* work_pages, int32_t* info);
 
 /* ---- Paged append (refines inference.cpp:100-103): row t of ckv/krope (fp32)
  * is rounded to 16-bit and written to slot slot_mapping[t] of the pool. */

@@ -38,17 +38,18 @@ def _gpu_metadata(mla, ctx, q, cu_pages, ids, ps, max_pages, P, split, target, m
     return rb
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(9))
 def test_metadata_bit_exact(gpu, orc, seed):
+    """Includes batches above the 4096-session LDS mirror (global-memory path)."""
     from test_metadata_oracle import random_batch
     rng = np.random.default_rng(100 + seed)
-    B = [1, 7, 64, 300, 1025, 2500, 64, 130][seed]
+    B = [1, 7, 64, 300, 1025, 2500, 64, 130, 5000][seed]
     _say(f"metadata seed={seed} B={B}")
     ctx, q, cu_pages, ids, P, max_pages = random_batch(
         rng, B, decode=seed % 2 == 0, share_prefix=seed % 3 == 0, max_ctx=[4096, 70000][seed % 2])
-    split = [0, 1, 3, 0, 2, 0, 5, 0][seed]
+    split = [0, 1, 3, 0, 2, 0, 5, 0, 0][seed]
     target = int(rng.integers(1, 2000))
-    max_work, max_rows = 1 << 18, 1 << 18
+    max_work, max_rows = 65535, 1 << 18
     want = orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, split, target, max_work)
     rb = _gpu_metadata(gpu, ctx, q, cu_pages, ids, 64, max_pages, P, split, target, max_work,
                        max_rows)
@@ -61,6 +62,11 @@ def test_metadata_bit_exact(gpu, orc, seed):
         np.testing.assert_array_equal(getattr(rb, k)[:n].cpu().numpy(), want[k][:n], err_msg=k)
     np.testing.assert_array_equal(rb.page_table[:B * max_pages].cpu().numpy(),
                                   want["page_table"].reshape(-1))
+    desc = rb.work_desc.cpu().numpy().reshape(-1, 8)
+    np.testing.assert_array_equal(desc[:W], want["work_desc"][:W])
+    assert np.all(desc[W:, 0] == -1)
+    np.testing.assert_array_equal(rb.work_pages.cpu().numpy().reshape(-1, 8)[:W],
+                                  want["work_pages"][:W])
 
 
 @pytest.mark.parametrize("case", ["neg_q", "short_pages", "bad_id", "too_many_pages",
@@ -70,7 +76,7 @@ def test_metadata_errors_match_oracle(gpu, orc, case):
     rng = np.random.default_rng(3)
     ctx, q, cu_pages, ids, P, max_pages = random_batch(rng, 20, decode=True, spare=0)
     ctx, q, ids = ctx.copy(), q.copy(), ids.copy()
-    max_work, max_rows = 1 << 20, 1 << 20
+    max_work, max_rows = 65535, 1 << 20
     if case == "neg_q":
         q[7] = -1
     elif case == "short_pages":
@@ -91,6 +97,7 @@ def test_metadata_errors_match_oracle(gpu, orc, case):
     assert e.value.code == "invalid_argument"
     info = rb.info.cpu().numpy().tolist()
     assert info[0] == -1 and info[1] == want[1]
+    assert np.all(rb.work_desc.cpu().numpy().reshape(-1, 8)[:, 0] == -1)  # no work issued
 
 
 def test_metadata_empty_batch(gpu):

@@ -33,18 +33,23 @@ def py_metadata(ctx, q, cu_pages, page_ids, ps, max_pages, pool, split_pages, ta
         cus.append(cus[-1] + ns[b])
         if cus[-1] > max_work:
             return ("error", b)
-    ws, wsp, table, slots = [], [], [], []
+    ws, wsp, table, slots, desc, wpages = [], [], [], [], [], []
     for b in range(B):
         ws += [b] * ns[b]
         wsp += list(range(ns[b]))
         ids = list(page_ids[cu_pages[b]:cu_pages[b + 1]])
+        need = -(-(ctx[b] + q[b]) // ps)
+        for sp in range(ns[b]):
+            p0, p1 = sp * split, min(need, sp * split + split)
+            desc.append([b, cuq[b], ctx[b] + q[b], p0, p1, ns[b], cus[b], q[b]])
+            wpages.append([ids[p0 + j] if p0 + j < p1 else -1 for j in range(8)])
         table.append(ids + [-1] * (max_pages - len(ids)))
         for i in range(q[b]):
             pos = ctx[b] + i
             slots.append(ids[pos // ps] * ps + pos % ps)
     return dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, num_splits=ns, cu_splits=cus,
                 work_session=ws, work_split=wsp, page_table=table, slot_mapping=slots,
-                info=[cus[-1], split, cuq[-1], cuk[-1]])
+                work_desc=desc, work_pages=wpages, info=[cus[-1], split, cuq[-1], cuk[-1]])
 
 
 def random_batch(rng, B, ps=64, max_ctx=4096, decode=True, share_prefix=False, spare=2):
@@ -83,19 +88,25 @@ def test_metadata_matches_independent_builder(orc, seed, split):
                                                        share_prefix=seed % 3 == 0)
     target = int(rng.integers(1, 600))
     want = py_metadata(list(ctx), list(q), list(cu_pages), list(ids), 64, max_pages, P, split,
-                       target, 1 << 20, 1 << 20)
-    got = orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, split, target, 1 << 20)
+                       target, 65535, 1 << 20)
+    got = orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, split, target, 65535)
     for k in ("cu_seqlens_q", "cu_seqlens_k", "num_splits", "cu_splits", "work_session",
               "work_split", "slot_mapping"):
         np.testing.assert_array_equal(got[k], np.array(want[k], np.int32), err_msg=k)
     np.testing.assert_array_equal(got["page_table"], np.array(want["page_table"], np.int32))
     np.testing.assert_array_equal(got["info"], np.array(want["info"], np.int32))
+    W = want["info"][0]
+    np.testing.assert_array_equal(got["work_desc"][:W], np.array(want["work_desc"], np.int32)
+                                  .reshape(-1, 8))
+    np.testing.assert_array_equal(got["work_pages"][:W], np.array(want["work_pages"], np.int32)
+                                  .reshape(-1, 8))
+    assert np.all(got["work_desc"][W:, 0] == -1)
 
 
 def test_metadata_invariants(orc):
     rng = np.random.default_rng(11)
     ctx, q, cu_pages, ids, P, max_pages = random_batch(rng, 64, share_prefix=True)
-    md = orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, 0, 512, 1 << 20)
+    md = orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, 0, 512, 65535)
     W, split, total_q, total_k = md["info"].tolist()
     assert total_q == q.sum() and total_k == (ctx + q).sum()
     assert np.all(np.diff(md["cu_seqlens_k"]) == ctx + q)
@@ -119,7 +130,7 @@ def test_metadata_invariants(orc):
 def test_metadata_errors_name_first_bad_session(orc, case):
     rng = np.random.default_rng(3)
     ctx, q, cu_pages, ids, P, max_pages = random_batch(rng, 20, decode=True, spare=0)
-    max_work, max_rows = 1 << 20, 1 << 20
+    max_work, max_rows = 65535, 1 << 20
     ctx, q, ids = ctx.copy(), q.copy(), ids.copy()
     if case == "neg_q":
         q[7] = -1
@@ -137,10 +148,7 @@ def test_metadata_errors_name_first_bad_session(orc, case):
                        max_work, max_rows)
     assert want[0] == "error"
     with pytest.raises(ValueError) as e:
-        md = orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, 1, 512, max_work)
-        if q.sum() > max_rows:  # the oracle wrapper sizes rows itself; emulate the capacity
-            raise ValueError(f"invalid metadata input (session {want[1]})")
-        assert md is None
+        orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, 1, 512, max_work, max_rows)
     assert f"session {want[1]})" in str(e.value)
 
 
