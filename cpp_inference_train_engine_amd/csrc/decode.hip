@@ -47,62 +47,77 @@ struct UnitRegs {
     u32x4 rop[2][RS];
 };
 
-// Loads rows slot0.. of page record `base`; only the first `valid` rows are read.
+// Loads tokens slot0..slot0+31 of a TILED page record (see page_tiled): every
+// 16-byte lane load of the wave reads one contiguous 1 KB block (or 512 B of rope).
+// Only the first `valid` tokens are read; the rest are zero.
 template <int KV, int RP, int PS>
 __device__ __forceinline__ void load_unit(UnitRegs<KV, RP>& u, const uint16_t* base, int slot0,
                                           int valid, int g, int n) {
     constexpr int KS = UnitRegs<KV, RP>::KS, RS = UnitRegs<KV, RP>::RS;
+    const int lane8 = (16 * g + n) * 8;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        const int r = slot0 + 16 * t + n;
+        const int tile = (slot0 >> 4) + t;
         const bool ok = 16 * t + n < valid;
 #pragma unroll
         for (int j = 0; j < KS; ++j)
-            u.lat[t][j] = ok ? *reinterpret_cast<const u32x4*>(base + r * KV + 32 * j + 8 * g)
+            u.lat[t][j] = ok ? *reinterpret_cast<const u32x4*>(base + (tile * KS + j) * 512 + lane8)
                              : u32x4{0, 0, 0, 0};
 #pragma unroll
         for (int k = 0; k < RS; ++k)
             u.rop[t][k] = ok && 32 * k + 8 * g < RP
-                              ? *reinterpret_cast<const u32x4*>(base + PS * KV + r * RP + 32 * k +
-                                                                8 * g)
+                              ? *reinterpret_cast<const u32x4*>(base + PS * KV +
+                                                                (tile * (RP / 8) + 4 * k) * 128 +
+                                                                lane8)
                               : u32x4{0, 0, 0, 0};
     }
 }
 
 // Scores of one unit, online-softmax update, O^T += C^T . P^T.  `valid` tokens of
 // the unit count; the rest are masked.  myl is this wave's LDS transpose buffer.
+// Transposed latent unit in LDS: [kv_rank][kTransposePitch] 16-bit words (32 tokens
+// + 4 pad words, so rows 8 apart are 64 bytes apart in the banks).
+constexpr int kTransposePitch = 36;
+
+// Q tile in LDS: row h = [latent KV | rope padded to 32*RS | 8 pad], 16 rows.
+template <int KV, int RP>
+constexpr int q_stride() {
+    return KV + 32 * ((RP + 31) / 32) + 8;
+}
+
 template <typename T, int KV, int RP>
 __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int valid,
-                                             const typename T::vec8* bq,
-                                             const typename T::vec8* bqr, float scale_log2,
-                                             float& m_run, float& l_run, floatx4* acc,
-                                             uint16_t* myl, int g, int n) {
+                                             const uint16_t* qs, float scale_log2, float& m_run,
+                                             float& l_run, floatx4* acc, uint16_t* myl, int g,
+                                             int n) {
     constexpr int KS = UnitRegs<KV, RP>::KS, RS = UnitRegs<KV, RP>::RS;
     constexpr int RT = KV / 16;
-    constexpr int STRIDE = KV + 4;
+    constexpr int TS = kTransposePitch;
+    constexpr int QS = q_stride<KV, RP>();
     using V8 = typename T::vec8;
-    // S^T[16t + 4g + i][head n]
-    floatx4 sc[2];
+    // S^T[16t + 4g + i][head n]; B operand Q^T read from the LDS tile (head n).
+    const uint16_t* qrow = qs + n * QS + 8 * g;
+    floatx4 sc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        floatx4 c = {0, 0, 0, 0};
+    for (int j = 0; j < KS + RS; ++j) {
+        const V8 b = *reinterpret_cast<const V8*>(qrow + 32 * j);
 #pragma unroll
-        for (int j = 0; j < KS; ++j)
-            c = T::mma32(__builtin_bit_cast(V8, u.lat[t][j]), bq[j], c);
-#pragma unroll
-        for (int k = 0; k < RS; ++k)
-            c = T::mma32(__builtin_bit_cast(V8, u.rop[t][k]), bqr[k], c);
-        sc[t] = c;
+        for (int t = 0; t < 2; ++t)
+            sc[t] = T::mma32(__builtin_bit_cast(V8, j < KS ? u.lat[t][j] : u.rop[t][j - KS]), b,
+                             sc[t]);
     }
-    // Latent rows to LDS for the transposed read of C^T.
+    // Latent to LDS transposed, [r][token] with pitch TS: lane (g, n) scatters the
+    // 8 values of token 16t+n, columns 32j+8g.. (the 4 lane groups land 8 rows apart,
+    // 64 bytes apart in the banks).
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int j = 0; j < KS; ++j) {
-            uint16_t* dst = myl + (16 * t + n) * STRIDE + 32 * j + 8 * g;
+            uint16_t* dst = myl + (32 * j + 8 * g) * TS + 16 * t + n;
             const u32x4 v = u.lat[t][j];
-            *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
-            *reinterpret_cast<u32x2*>(dst + 4) = u32x2{v[2], v[3]};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                dst[e * TS] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
         }
     float mloc = -INFINITY;
 #pragma unroll
@@ -135,31 +150,28 @@ __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int vali
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // A = C^T (lane: column 16rt+n, tokens 4g+i and 16+4g+i), B = P^T (lane: head n,
-    // the same 8 tokens): the K-slot order agrees between the operands.
+    // A = C^T (lane: column 16rt+n, tokens 4g..4g+3 and 16+4g..16+4g+3: two 8-byte
+    // reads), B = P^T (lane: head n, the same 8 tokens): the K-slot order agrees.
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        V8 ac;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ac[i] = __builtin_bit_cast(typename T::scalar, myl[(4 * g + i) * STRIDE + 16 * rt + n]);
-            ac[4 + i] =
-                __builtin_bit_cast(typename T::scalar, myl[(16 + 4 * g + i) * STRIDE + 16 * rt + n]);
-        }
-        acc[rt] = T::mma32(ac, pb, acc[rt]);
+        const uint16_t* src = myl + (16 * rt + n) * TS + 4 * g;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 16);
+        acc[rt] = T::mma32(__builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb, acc[rt]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// One workgroup of WAVES waves per work item (session, split); wave v takes pages
-// p_begin+v, p_begin+v+WAVES, ... and issues both 32-token halves of a page before
-// computing.  The waves' softmax states merge in LDS; a session split over several
+// One workgroup of WAVES waves per work item (session, split); wave v streams the
+// 32-token units of pages p_begin+v, p_begin+v+WAVES, ... keeping the next unit's
+// loads in flight while it computes the current one.  The waves' softmax states
+// merge in LDS; a session split over several
 // workgroups leaves one partial per workgroup for merge_kernel (the next launch on
 // the stream, so the partials are coherent without device-scope fences).
-// Up to 256 VGPRs (2 waves/SIMD): two 4-wave workgroups per CU; each wave keeps
-// one whole page (18 KB) in flight.
+// Up to 256 VGPRs (2 waves/SIMD); each wave keeps one 32-token unit in flight while
+// computing the other and reads Q^T from the workgroup's LDS tile.
 #ifndef MLA_DECODE_WAVES_PER_EU
 #define MLA_DECODE_WAVES_PER_EU 2
 #endif
@@ -171,12 +183,14 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
     constexpr int UPP = PS / 32;      // 32-token units per page
     constexpr int KS = KV / 32, RS = (RP + 31) / 32;
     constexpr int RT = KV / 16;       // 16-row tiles of O^T
-    constexpr int STRIDE = KV + 4;    // LDS transpose pitch, 16-bit words (bank spread)
+    constexpr int TBUF = KV * kTransposePitch;  // per-wave transpose buffer, 16-bit words
     constexpr int MSTRIDE = KV + 4;   // LDS merge pitch, floats
     constexpr int THREADS = 64 * WAVES;
-    static_assert(16 * MSTRIDE * 4 <= 32 * STRIDE * 2, "merge buffer aliases transpose buffer");
+    static_assert(16 * MSTRIDE * 4 <= TBUF * 2, "merge buffer aliases transpose buffer");
     using V8 = typename T::vec8;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[WAVES][32 * STRIDE];
+    constexpr int QS = q_stride<KV, RP>();
+    __shared__ __attribute__((aligned(16))) uint16_t lds[WAVES][TBUF];
+    __shared__ __attribute__((aligned(16))) uint16_t q_s[16 * QS];
     __shared__ float sm_m[WAVES][16], sm_l[WAVES][16];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -185,35 +199,43 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
     uint16_t* myl = lds[wave];
     float* mb = reinterpret_cast<float*>(&lds[0][0]);  // [WAVES][16][MSTRIDE] after the loop
 
+#ifdef MLA_DECODE_TRACE
+    unsigned long long* trace = reinterpret_cast<unsigned long long*>(a.lse) +
+                                ((long long)blockIdx.x * WAVES + wave) * 8;
+    if (lane == 0)
+        trace[0] = wall_clock64();
+#endif
     for (int w = blockIdx.x; w < a.max_work; w += gridDim.x) {
         // One descriptor load (plus this wave's first page id) starts the item.
         const int32_t* d = a.work_desc + (long long)w * kWorkDescInts;
         const int page0 = wave < kWorkPages ? a.work_pages[(long long)w * kWorkPages + wave] : -1;
+        const int page1 =
+            wave + WAVES < kWorkPages ? a.work_pages[(long long)w * kWorkPages + wave + WAVES] : -1;
         const int s = d[0];
         if (s < 0)
             break;  // items past the last one are all marked empty
         if (d[7] != 1)
             continue;  // not a decode row
         const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
+#ifdef MLA_DECODE_TRACE
+        if (lane == 0)
+            trace[1] = wall_clock64() + (unsigned long long)(row & 0);
+#endif
 
-        // Q^T operands (B of S^T): lane (g, n) = head n.
-        V8 bq[KS], bqr[RS];
-#pragma unroll
-        for (int j = 0; j < KS; ++j) {
+        // Q tile to LDS (heads >= H and the rope padding are zero), shared by the waves.
+        for (int i = tid; i < 16 * (QS / 8); i += THREADS) {
+            const int h = i / (QS / 8), c8 = (i % (QS / 8)) * 8;
             u32x4 v = {0, 0, 0, 0};
-            if (head_ok)
-                v = *reinterpret_cast<const u32x4*>(a.q_latent + ((long long)row * a.H + n) * KV +
-                                                    32 * j + 8 * g);
-            bq[j] = __builtin_bit_cast(V8, v);
+            if (h < a.H) {
+                if (c8 < KV)
+                    v = *reinterpret_cast<const u32x4*>(a.q_latent + ((long long)row * a.H + h) * KV + c8);
+                else if (c8 - KV < RP)
+                    v = *reinterpret_cast<const u32x4*>(a.q_rope + ((long long)row * a.H + h) * RP +
+                                                        c8 - KV);
+            }
+            *reinterpret_cast<u32x4*>(q_s + h * QS + c8) = v;
         }
-#pragma unroll
-        for (int k = 0; k < RS; ++k) {
-            u32x4 v = {0, 0, 0, 0};
-            if (head_ok && 32 * k + 8 * g < RP)
-                v = *reinterpret_cast<const u32x4*>(a.q_rope + ((long long)row * a.H + n) * RP +
-                                                    32 * k + 8 * g);
-            bqr[k] = __builtin_bit_cast(V8, v);
-        }
+        __syncthreads();
 
         float m_run = -INFINITY, l_run = 0.0f;
         floatx4 acc[RT];
@@ -221,25 +243,54 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
         for (int r = 0; r < RT; ++r)
             acc[r] = floatx4{0, 0, 0, 0};
 
-        for (int p = p_begin + wave; p < p_end; p += WAVES) {
-            const int page = p == p_begin + wave ? page0
-                                                  : a.page_table[(long long)s * a.max_pages + p];
-            if ((unsigned)page >= (unsigned)a.num_pool_pages)
-                continue;
-            const uint16_t* base = a.pages + page * rec;
-            const int valid = min(PS, kl - p * PS);
-            UnitRegs<KV, RP> u[UPP];
-#pragma unroll
-            for (int q = 0; q < UPP; ++q)
-                load_unit<KV, RP, PS>(u[q], base, 32 * q, valid - 32 * q, g, n);
-#pragma unroll
-            for (int q = 0; q < UPP; ++q)
-                if (valid > 32 * q)
-                    process_unit<T, KV, RP>(u[q], valid - 32 * q, bq, bqr, a.scale_log2, m_run,
-                                            l_run, acc, myl, g, n);
+        // This wave streams the 32-token units of pages p_begin+wave, +WAVES, ...
+        // with one unit in flight while the other is computed (rolling prefetch).
+        const int np = p_begin + wave < p_end ? (p_end - p_begin - wave + WAVES - 1) / WAVES : 0;
+        const int nk = np * UPP;
+        auto page_of = [&](int pi) -> int {
+            const int rel = wave + WAVES * pi;  // page offset inside the work item
+            const int id = pi == 0 ? page0
+                           : pi == 1 ? page1
+                           : rel < kWorkPages ? a.work_pages[(long long)w * kWorkPages + rel]
+                                              : a.page_table[(long long)s * a.max_pages + p_begin + rel];
+            return __builtin_amdgcn_readfirstlane(id);  // wave-uniform: scalar base address
+        };
+        auto issue = [&](UnitRegs<KV, RP>& u, int k) -> int {  // returns the unit's valid tokens
+            const int p = p_begin + wave + WAVES * (k / UPP);
+            const int page = page_of(k / UPP);
+            const int slot0 = 32 * (k % UPP);
+            const bool ok = (unsigned)page < (unsigned)a.num_pool_pages;
+            const int valid = ok ? min(PS, kl - p * PS) - slot0 : 0;
+            load_unit<KV, RP, PS>(u, a.pages + (ok ? page : 0) * rec, slot0, valid, g, n);
+            return valid;
+        };
+        UnitRegs<KV, RP> ub0, ub1;
+        int v0 = 0, v1 = 0;
+        if (nk > 0)
+            v0 = issue(ub0, 0);
+        if (nk > 1)
+            v1 = issue(ub1, 1);
+        for (int k = 0; k < nk; k += 2) {
+            if (v0 > 0)
+                process_unit<T, KV, RP>(ub0, v0, q_s, a.scale_log2, m_run, l_run, acc, myl, g, n);
+            if (k + 2 < nk)
+                v0 = issue(ub0, k + 2);
+            if (k + 1 < nk) {
+                if (v1 > 0)
+                    process_unit<T, KV, RP>(ub1, v1, q_s, a.scale_log2, m_run, l_run, acc, myl, g,
+                                            n);
+                if (k + 3 < nk)
+                    v1 = issue(ub1, k + 3);
+            }
         }
         l_run += __shfl_xor(l_run, 16, 64);
         l_run += __shfl_xor(l_run, 32, 64);
+#ifdef MLA_DECODE_TRACE
+        if (lane == 0) {
+            trace[2] = wall_clock64() + (unsigned long long)(l_run != l_run);
+            trace[5] = w;
+        }
+#endif
 
         // ---- merge the WAVES softmax states of this work item in LDS ----
         if (g == 0) {
@@ -288,6 +339,10 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
             }
         }
         __syncthreads();  // LDS and sm_* are reused by the next work item
+#ifdef MLA_DECODE_TRACE
+        if (lane == 0)
+            trace[3] = wall_clock64();
+#endif
     }
 }
 
@@ -330,6 +385,7 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
     const int tid = threadIdx.x, h = blockIdx.y;
     const int KV = a.kv_rank, RP = a.rope_dim, PS = a.page_size;
     const long long rec = (long long)PS * (KV + RP);
+    const bool tiled = page_tiled(PS, KV, RP);
     for (int w = blockIdx.x; w < a.max_work; w += gridDim.x) {
         const int32_t* d = a.work_desc + (long long)w * kWorkDescInts;
         const int s = d[0];
@@ -353,13 +409,12 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
                 float x = -INFINITY;
                 if ((unsigned)page < (unsigned)a.num_pool_pages) {
                     const uint16_t* base = a.pages + page * rec;
-                    const uint16_t* c = base + (long long)(tok % PS) * KV;
-                    const uint16_t* k = base + (long long)PS * KV + (long long)(tok % PS) * RP;
+                    const int slot = tok % PS;
                     float d = 0.0f, dr = 0.0f;
                     for (int r = 0; r < KV; ++r)
-                        d += T::to_float(c[r]) * qs[r];
+                        d += T::to_float(base[latent_word(tiled, slot, r, PS, KV)]) * qs[r];
                     for (int j = 0; j < RP; ++j)
-                        dr += T::to_float(k[j]) * qs[KV + j];
+                        dr += T::to_float(base[rope_word(tiled, slot, j, PS, KV, RP)]) * qs[KV + j];
                     x = (dr + d) * a.scale_log2;
                 }
                 sc[t] = x;
@@ -386,7 +441,8 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
                     const int tok = c0 + t;
                     const int page = a.page_table[(long long)s * a.max_pages + tok / PS];
                     if ((unsigned)page < (unsigned)a.num_pool_pages && sc[t] != 0.0f)
-                        v += sc[t] * T::to_float(a.pages[page * rec + (long long)(tok % PS) * KV + r]);
+                        v += sc[t] * T::to_float(
+                                         a.pages[page * rec + latent_word(tiled, tok % PS, r, PS, KV)]);
                 }
                 acc[k] = v;
             }
@@ -503,7 +559,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
 }
 
 #ifndef MLA_DECODE_WAVES
-#define MLA_DECODE_WAVES 4
+#define MLA_DECODE_WAVES 2
 #endif
 constexpr int kMfmaWaves = MLA_DECODE_WAVES;
 

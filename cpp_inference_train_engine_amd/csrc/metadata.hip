@@ -242,6 +242,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     const int width = a.kv_rank + a.rope_dim;
     const long long total = (long long)a.T * width;
     const long long rec = (long long)a.page_size * width;
+    const bool tiled = page_tiled(a.page_size, a.kv_rank, a.rope_dim);
     for (long long e = blockIdx.x * 256LL + threadIdx.x; e < total; e += 256LL * gridDim.x) {
         const int t = (int)(e / width), c = (int)(e % width);
         const int slot = a.slot_mapping[t];
@@ -250,10 +251,11 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
             continue;
         uint16_t* base = a.pages + page * rec;
         if (c < a.kv_rank)
-            base[(long long)off * a.kv_rank + c] = T::from_float(a.ckv[(long long)t * a.kv_rank + c]);
+            base[latent_word(tiled, off, c, a.page_size, a.kv_rank)] =
+                T::from_float(a.ckv[(long long)t * a.kv_rank + c]);
         else {
             const int j = c - a.kv_rank;
-            base[(long long)a.page_size * a.kv_rank + (long long)off * a.rope_dim + j] =
+            base[rope_word(tiled, off, j, a.page_size, a.kv_rank, a.rope_dim)] =
                 T::from_float(a.krope[(long long)t * a.rope_dim + j]);
         }
     }

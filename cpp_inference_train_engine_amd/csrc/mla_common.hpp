@@ -75,3 +75,39 @@ __device__ inline float wave_sum(float v) {
 }
 
 }  // namespace mla
+
+namespace mla {
+
+// ---- Page record layout ------------------------------------------------------
+// A page record holds page_size tokens of one layer: the latent section
+// (page_size * kv_rank words) followed by the rope-key section (page_size *
+// rope_dim words), 16-bit words.  When page_size % 16 == 0, kv_rank % 32 == 0 and
+// rope_dim % 8 == 0 the record is TILED in MFMA-operand order, so that one 64-lane
+// 16-byte load reads 1 KB contiguously:
+//   latent (slot, r): tile t = slot/16, n = slot%16, j = r/32, g = (r%32)/8,
+//                     e = r%8  ->  ((t*(kv_rank/32) + j)*4 + g)*128 + n*8 + e
+//   rope (slot, c):   ch = c/8, e = c%8
+//                     ->  page_size*kv_rank + (t*(rope_dim/8) + ch)*128 + n*8 + e
+// Otherwise the record is row-major: latent slot*kv_rank + r, rope
+// page_size*kv_rank + slot*rope_dim + c.
+__host__ __device__ inline bool page_tiled(int page_size, int kv_rank, int rope_dim) {
+    return page_size % 16 == 0 && kv_rank % 32 == 0 && rope_dim % 8 == 0;
+}
+__host__ __device__ inline long long latent_word(bool tiled, int slot, int r, int page_size,
+                                                 int kv_rank) {
+    (void)page_size;
+    if (!tiled)
+        return (long long)slot * kv_rank + r;
+    const int t = slot >> 4, n = slot & 15, j = r >> 5, g = (r & 31) >> 3, e = r & 7;
+    return ((long long)(t * (kv_rank >> 5) + j) * 4 + g) * 128 + n * 8 + e;
+}
+__host__ __device__ inline long long rope_word(bool tiled, int slot, int c, int page_size,
+                                               int kv_rank, int rope_dim) {
+    const long long base = (long long)page_size * kv_rank;
+    if (!tiled)
+        return base + (long long)slot * rope_dim + c;
+    const int t = slot >> 4, n = slot & 15, ch = c >> 3, e = c & 7;
+    return base + (long long)(t * (rope_dim >> 3) + ch) * 128 + n * 8 + e;
+}
+
+}  // namespace mla

@@ -155,3 +155,26 @@ def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, 
 
 __all__ = ["RaggedBatch", "build_metadata", "PagedLatentCache", "append_latent",
            "decode_workspace_bytes", "decode_workspace", "decode_attention", "DTYPE_F16", "DTYPE_BF16"]
+
+
+# ---------------------------------------------------------------- page layout ----
+def page_tiled(page_size: int, kv_rank: int, rope_dim: int) -> bool:
+    """Page records are tiled in MFMA-operand order for these shapes (see mla_hip.h)."""
+    return page_size % 16 == 0 and kv_rank % 32 == 0 and rope_dim % 8 == 0
+
+
+def latent_word(slot, r, page_size: int, kv_rank: int, rope_dim: int):
+    """Word index of latent column r of token `slot` inside a page record (numpy-friendly)."""
+    if not page_tiled(page_size, kv_rank, rope_dim):
+        return slot * kv_rank + r
+    t, n, j, g, e = slot // 16, slot % 16, r // 32, (r % 32) // 8, r % 8
+    return ((t * (kv_rank // 32) + j) * 4 + g) * 128 + n * 8 + e
+
+
+def rope_word(slot, c, page_size: int, kv_rank: int, rope_dim: int):
+    """Word index of rope column c of token `slot` inside a page record."""
+    base = page_size * kv_rank
+    if not page_tiled(page_size, kv_rank, rope_dim):
+        return base + slot * rope_dim + c
+    t, n = slot // 16, slot % 16
+    return base + (t * (rope_dim // 8) + c // 8) * 128 + n * 8 + c % 8

@@ -24,8 +24,15 @@
  *  - 16-bit element dtype codes: MLA_DTYPE_F16 (0), MLA_DTYPE_BF16 (1).
  *
  * Paged latent cache layout (one pool per layer): page p is one contiguous
- * record of page_size * (kv_rank + rope_dim) 16-bit words:
- *     latent [page_size][kv_rank]  then  rope key [page_size][rope_dim]
+ * record of page_size * (kv_rank + rope_dim) 16-bit words: the latent section
+ * (page_size * kv_rank words) then the rope-key section (page_size * rope_dim).
+ * When page_size % 16 == 0, kv_rank % 32 == 0 and rope_dim % 8 == 0 (every
+ * production shape) the record is tiled in MFMA-operand order so that a wave's
+ * 16-byte-per-lane load reads 1 KB contiguously: with t = slot/16, n = slot%16,
+ *     latent (slot, r) -> ((t*(kv_rank/32) + r/32)*4 + (r%32)/8)*128 + n*8 + r%8
+ *     rope (slot, c)   -> page_size*kv_rank + (t*(rope_dim/8) + c/8)*128 + n*8 + c%8
+ * otherwise it is row-major (latent slot*kv_rank + r, rope
+ * page_size*kv_rank + slot*rope_dim + c).  mla_append_latent writes this format.
  * Token position t of session b lives in page page_table[b][t / page_size],
  * slot t % page_size.  The cache holds the kv_norm-ed latent and the RoPE-ed
  * key exactly as the reference's CpuDecoder cache does

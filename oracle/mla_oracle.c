@@ -577,6 +577,30 @@ int orc_decode(const orc_config* c, const float* params, const float* out_proj, 
 }
 
 /* ------------------------------------------------------------------------ */
+/* Page record layout (the format the GPU kernels read and write).  Tiled    */
+/* when page_size % 16 == 0, kv_rank % 32 == 0 and rope_dim % 8 == 0:        */
+/* 16-token tiles t, 32-column K-steps j, 8-column groups g, token n in the   */
+/* tile, column e in the group; otherwise plain row-major.                   */
+/* ------------------------------------------------------------------------ */
+static int tiled_layout(int page_size, int kv_rank, int rope_dim) {
+    return page_size % 16 == 0 && kv_rank % 32 == 0 && rope_dim % 8 == 0;
+}
+static size_t lat_index(int tiled, int slot, int r, int kv_rank) {
+    if (!tiled)
+        return (size_t)slot * kv_rank + r;
+    const size_t tile = (size_t)(slot / 16), n = (size_t)(slot % 16);
+    const size_t j = (size_t)(r / 32), g = (size_t)((r % 32) / 8), e = (size_t)(r % 8);
+    return ((tile * (size_t)(kv_rank / 32) + j) * 4 + g) * 128 + n * 8 + e;
+}
+static size_t rope_index(int tiled, int slot, int c, int page_size, int kv_rank, int rope_dim) {
+    const size_t base = (size_t)page_size * kv_rank;
+    if (!tiled)
+        return base + (size_t)slot * rope_dim + c;
+    const size_t tile = (size_t)(slot / 16), n = (size_t)(slot % 16);
+    return base + (tile * (size_t)(rope_dim / 8) + (size_t)(c / 8)) * 128 + n * 8 + (size_t)(c % 8);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Absorbed attention over a paged 16-bit cache (inference.cpp:116-153)      */
 /* ------------------------------------------------------------------------ */
 int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, int dtype,
@@ -584,13 +608,12 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
                         int max_pages, const uint16_t* pages, const float* q_latent,
                         const float* q_rope, float scale, float* out, float* lse) {
     const size_t rec = (size_t)page_size * (size_t)(kv_rank + rope_dim);
+    const int tiled = tiled_layout(page_size, kv_rank, rope_dim);
     int max_len = 0;
     for (int b = 0; b < B; ++b)
         if (k_len[b] > max_len)
             max_len = k_len[b];
     float* scores = malloc((size_t)(max_len > 0 ? max_len : 1) * 4);
-    const uint16_t** lat = malloc((size_t)(max_len > 0 ? max_len : 1) * sizeof(void*));
-    const uint16_t** rop = malloc((size_t)(max_len > 0 ? max_len : 1) * sizeof(void*));
     float* cbuf = malloc((size_t)(max_len > 0 ? max_len : 1) * (size_t)kv_rank * 4);
     float* rbuf = malloc((size_t)(max_len > 0 ? max_len : 1) * (size_t)(rope_dim > 0 ? rope_dim : 1) * 4);
     for (int b = 0; b < B; ++b) {
@@ -599,18 +622,18 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
             continue;
         const int kl = k_len[b];
         if (kl < nq || (kl + page_size - 1) / page_size > max_pages) {
-            free(scores), free(lat), free(rop), free(cbuf), free(rbuf);
+            free(scores), free(cbuf), free(rbuf);
             return 1;
         }
         for (int t = 0; t < kl; ++t) {
             const int page = page_table[(size_t)b * max_pages + t / page_size];
             const uint16_t* base = pages + (size_t)page * rec;
-            lat[t] = base + (size_t)(t % page_size) * kv_rank;
-            rop[t] = base + (size_t)page_size * kv_rank + (size_t)(t % page_size) * rope_dim;
+            const int slot = t % page_size;
             for (int r = 0; r < kv_rank; ++r)
-                cbuf[(size_t)t * kv_rank + r] = load16(lat[t] + r, dtype);
+                cbuf[(size_t)t * kv_rank + r] = load16(base + lat_index(tiled, slot, r, kv_rank), dtype);
             for (int j = 0; j < rope_dim; ++j)
-                rbuf[(size_t)t * rope_dim + j] = load16(rop[t] + j, dtype);
+                rbuf[(size_t)t * rope_dim + j] =
+                    load16(base + rope_index(tiled, slot, j, page_size, kv_rank, rope_dim), dtype);
         }
         for (int i = 0; i < nq; ++i) {
             const int row = cu_q[b] + i;
@@ -650,7 +673,7 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
             }
         }
     }
-    free(scores), free(lat), free(rop), free(cbuf), free(rbuf);
+    free(scores), free(cbuf), free(rbuf);
     return 0;
 }
 
@@ -756,13 +779,14 @@ void orc_append_paged(int T, int kv_rank, int rope_dim, int page_size, int dtype
                       const float* ckv, const float* krope, const int32_t* slot_mapping,
                       uint16_t* pages) {
     const size_t rec = (size_t)page_size * (size_t)(kv_rank + rope_dim);
+    const int tiled = tiled_layout(page_size, kv_rank, rope_dim);
     for (int t = 0; t < T; ++t) {
         const int page = slot_mapping[t] / page_size, slot = slot_mapping[t] % page_size;
         uint16_t* base = pages + (size_t)page * rec;
         for (int r = 0; r < kv_rank; ++r)
-            base[(size_t)slot * kv_rank + r] = store16(ckv[(size_t)t * kv_rank + r], dtype);
+            base[lat_index(tiled, slot, r, kv_rank)] = store16(ckv[(size_t)t * kv_rank + r], dtype);
         for (int j = 0; j < rope_dim; ++j)
-            base[(size_t)page_size * kv_rank + (size_t)slot * rope_dim + j] =
+            base[rope_index(tiled, slot, j, page_size, kv_rank, rope_dim)] =
                 store16(krope[(size_t)t * rope_dim + j], dtype);
     }
 }

@@ -83,9 +83,11 @@ int orc_decode(const orc_config* c, const float* params, const float* out_proj, 
                float* logits);
 
 /* ---- Absorbed MLA attention over a paged cache (inference.cpp:116-153, fp32).
- * Page record layout (one per page, per layer):
- *   latent [page_size x kv_rank] then rope [page_size x rope_dim], 16-bit
- *   elements (dtype 0 = fp16, 1 = bf16).
+ * Page record layout (one per page, per layer): latent section
+ * (page_size x kv_rank) then rope section (page_size x rope_dim), 16-bit
+ * elements (dtype 0 = fp16, 1 = bf16); tiled in MFMA-operand order when
+ * page_size % 16 == 0, kv_rank % 32 == 0 and rope_dim % 8 == 0, else row-major
+ * (the format of include/mla_hip.h).
  * Queries are ragged: session b owns rows cu_q[b]..cu_q[b+1]; row i of session b
  * sits at absolute position k_len[b] - q_len[b] + i and attends causally to
  * positions [0, that position].  q_latent [rows x H x kv_rank], q_rope

@@ -234,14 +234,15 @@ def test_decode_skips_prefill_rows_and_tolerates_garbage_slots(gpu, orc):
     untouched by the decode kernel."""
     import torch
     from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    from cpp_inference_train_engine_amd.ops import latent_word, rope_word
     batch = ragged_decode_batch(lengths=[70, 5, 200, 64], seed=8)
     # fill every slot beyond k_len with fp16 NaN
     for b, L in enumerate(batch.k_len):
         lst = batch.page_ids[batch.cu_pages[b]:batch.cu_pages[b + 1]]
         for t in range(L, len(lst) * 64):
             rec = batch.pages[0, lst[t // 64]]
-            rec[(t % 64) * 128:(t % 64 + 1) * 128] = 0x7E00
-            rec[64 * 128 + (t % 64) * 16:64 * 128 + (t % 64 + 1) * 16] = 0x7E00
+            rec[latent_word(t % 64, np.arange(128), 64, 128, 16)] = 0x7E00
+            rec[rope_word(t % 64, np.arange(16), 64, 128, 16)] = 0x7E00
     for flags in (0, 1):
         got, _, _ = _run_decode(gpu, batch, split=1, flags=flags)
         want, _ = _oracle_decode(orc, batch)

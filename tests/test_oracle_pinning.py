@@ -222,6 +222,19 @@ def orc_round(x, dtype):
     return oracle.round_f16(x) if dtype == 0 else oracle.round_bf16(x)
 
 
+def _words(sl, kv, rp, ps):
+    """Independent statement of the page-record format: row-major, or MFMA-tiled
+    (16-token tiles x 32-column K-steps x 8-column groups) when ps%16, kv%32, rp%8 == 0."""
+    r = np.arange(kv)[None, :]
+    c = np.arange(rp)[None, :]
+    s = sl[:, None]
+    if ps % 16 or kv % 32 or rp % 8:
+        return s * kv + r, ps * kv + s * rp + c
+    lat = (((s // 16) * (kv // 32) + r // 32) * 4 + (r % 32) // 8) * 128 + (s % 16) * 8 + r % 8
+    rope = ps * kv + ((s // 16) * (rp // 8) + c // 8) * 128 + (s % 16) * 8 + c % 8
+    return lat, rope
+
+
 def _brute(lens, table, bits, ql, qr, cu_q, H, kv, rp, ps, dtype, scale):
     import oracle
     vals = oracle.bits_to_f32(bits, dtype).astype(np.float64)
@@ -231,8 +244,9 @@ def _brute(lens, table, bits, ql, qr, cu_q, H, kv, rp, ps, dtype, scale):
         toks = np.arange(lens[b])
         pg = table[b, toks // ps]
         sl = toks % ps
-        C = vals[pg[:, None], sl[:, None] * kv + np.arange(kv)[None, :]]
-        K = vals[pg[:, None], ps * kv + sl[:, None] * rp + np.arange(rp)[None, :]]
+        lw, rw = _words(sl, kv, rp, ps)
+        C = vals[pg[:, None], lw]
+        K = vals[pg[:, None], rw]
         for i in range(nq):
             row = cu_q[b] + i
             L = lens[b] - nq + i + 1
@@ -244,11 +258,12 @@ def _brute(lens, table, bits, ql, qr, cu_q, H, kv, rp, ps, dtype, scale):
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
-def test_attention_paged_brute_force_fp64(orc, dtype):
+@pytest.mark.parametrize("shape", [(3, 16, 4, 8), (2, 32, 8, 16)], ids=["rowmajor", "tiled"])
+def test_attention_paged_brute_force_fp64(orc, dtype, shape):
     """Closed form: softmax-weighted latent sum, in fp64 numpy over the same 16-bit data,
-    including causal rows of a prefill chunk (q_len > 1)."""
+    including causal rows of a prefill chunk (q_len > 1); both page-record formats."""
     rng = np.random.default_rng(5 + dtype)
-    H, kv, rp, ps = 3, 16, 4, 8
+    H, kv, rp, ps = shape
     lens, table, bits, ql, qr, cu_q = _paged_case(rng, 5, H, kv, rp, ps, dtype,
                                                    q_lens=[1, 4, 1, 2, 1], max_len=60)
     scale = 1.0 / np.sqrt(12.0)
@@ -304,3 +319,27 @@ def test_greedy_sampler_semantics(orc):
     assert orc.greedy(np.array([1, 3, 3, 0], np.float32)) == 1  # lowest index on ties
     assert orc.greedy(np.array([-2, -1], np.float32), history=[1], repetition_penalty=4) == 0
     assert orc.greedy(np.array([0, np.inf], np.float32)) == -2
+
+
+@pytest.mark.parametrize("shape", [(8, 4, 16), (128, 16, 64), (32, 8, 16)])
+def test_append_places_every_value_at_its_layout_word(orc, shape):
+    """orc_append_paged writes column r of token slot s to the record word that the
+    independent format statement (_words) names, and nowhere else."""
+    kv, rp, ps = shape
+    rng = np.random.default_rng(4)
+    P, T = 3, 2 * ps
+    slots = rng.permutation(P * ps)[:T].astype(np.int32)
+    ckv = (np.arange(T * kv, dtype=np.float32).reshape(T, kv) % 2000) + 1
+    kr = -((np.arange(T * rp, dtype=np.float32).reshape(T, rp) % 2000) + 1)
+    pages = np.zeros((P, ps * (kv + rp)), np.uint16)
+    orc.append_paged(kv, rp, ps, 0, ckv, kr, slots, pages)
+    vals = orc.bits_to_f32(pages, 0)
+    seen = np.zeros(pages.shape, bool)
+    for t in range(T):
+        pg, sl = slots[t] // ps, slots[t] % ps
+        lw, rw = _words(np.array([sl]), kv, rp, ps)
+        np.testing.assert_array_equal(vals[pg, lw[0]], ckv[t])
+        np.testing.assert_array_equal(vals[pg, rw[0]], kr[t])
+        seen[pg, lw[0]] = True
+        seen[pg, rw[0]] = True
+    assert np.all(vals[~seen] == 0)
