@@ -73,11 +73,12 @@ __device__ __forceinline__ void load_unit(UnitRegs<KV, RP>& u, const uint16_t* b
     }
 }
 
-// Scores of one unit, online-softmax update, O^T += C^T . P^T.  `valid` tokens of
-// the unit count; the rest are masked.  myl is this wave's LDS transpose buffer.
-// Transposed latent unit in LDS: [kv_rank][kTransposePitch] 16-bit words (32 tokens
-// + 4 pad words, so rows 8 apart are 64 bytes apart in the banks).
-constexpr int kTransposePitch = 36;
+// Row-major latent unit in LDS for the C^T operand: [32 tokens][kv_rank + 16]
+// 16-bit words (the pad puts consecutive rows 32 bytes apart in the banks).
+template <int KV>
+constexpr int unit_pitch() {
+    return KV + 16;
+}
 
 // Q tile in LDS: row h = [latent KV | rope padded to 32*RS | 8 pad], 16 rows.
 template <int KV, int RP>
@@ -85,6 +86,22 @@ constexpr int q_stride() {
     return KV + 32 * ((RP + 31) / 32) + 8;
 }
 
+// Lazy online softmax: probabilities are taken against a shared reference max that
+// is only raised (with a rescale of the state) when some score exceeds it by more
+// than 2^kRescaleLog2; otherwise p <= 2^8 and the state needs no rescale.
+constexpr float kRescaleLog2 = 8.0f;
+
+// gfx950 LDS transpose read: in each 16-lane group, lane j supplies an 8-byte row
+// R_j; lane i = 4a+b receives {R_a[b], R_{a+4}[b], R_{a+8}[b], R_{a+12}[b]}.
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    const auto v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (s4 __attribute__((address_space(3)))*)((__attribute__((address_space(3))) char*)p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// Scores of one unit, online-softmax update, O^T += C^T . P^T.  `valid` tokens of
+// the unit count; the rest are masked.  myl is this wave's LDS unit tile.
 template <typename T, int KV, int RP>
 __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int valid,
                                              const uint16_t* qs, float scale_log2, float& m_run,
@@ -92,7 +109,7 @@ __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int vali
                                              int n) {
     constexpr int KS = UnitRegs<KV, RP>::KS, RS = UnitRegs<KV, RP>::RS;
     constexpr int RT = KV / 16;
-    constexpr int TS = kTransposePitch;
+    constexpr int UP = unit_pitch<KV>();
     constexpr int QS = q_stride<KV, RP>();
     using V8 = typename T::vec8;
     // S^T[16t + 4g + i][head n]; B operand Q^T read from the LDS tile (head n).
@@ -106,19 +123,12 @@ __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int vali
             sc[t] = T::mma32(__builtin_bit_cast(V8, j < KS ? u.lat[t][j] : u.rop[t][j - KS]), b,
                              sc[t]);
     }
-    // Latent to LDS transposed, [r][token] with pitch TS: lane (g, n) scatters the
-    // 8 values of token 16t+n, columns 32j+8g.. (the 4 lane groups land 8 rows apart,
-    // 64 bytes apart in the banks).
+    // Latent rows to the LDS tile: lane (g, n) stores token 16t+n, columns 32j+8g...
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int j = 0; j < KS; ++j) {
-            uint16_t* dst = myl + (32 * j + 8 * g) * TS + 16 * t + n;
-            const u32x4 v = u.lat[t][j];
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                dst[e * TS] = static_cast<uint16_t>(v[e >> 1] >> (16 * (e & 1)));
-        }
+        for (int j = 0; j < KS; ++j)
+            *reinterpret_cast<u32x4*>(myl + (16 * t + n) * UP + 32 * j + 8 * g) = u.lat[t][j];
     float mloc = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -128,35 +138,39 @@ __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int vali
             sc[t][i] = x;
             mloc = fmaxf(mloc, x);
         }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m_run - m_new);
+    if (__ballot(mloc > m_run + kRescaleLog2)) {  // wave-uniform, rare after the first unit
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+            acc[r] *= alpha;
+        m_run = m_new;
+    }
     float psum = 0.0f;
     V8 pb;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float e = m_new == -INFINITY ? 0.0f : exp2_fast(sc[t][i] - m_new);
+            const float e = m_run == -INFINITY ? 0.0f : exp2_fast(sc[t][i] - m_run);
             psum += e;
             pb[4 * t + i] = static_cast<typename T::scalar>(e);
         }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int r = 0; r < RT; ++r)
-        acc[r] *= alpha;
+    l_run += psum;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // A = C^T (lane: column 16rt+n, tokens 4g..4g+3 and 16+4g..16+4g+3: two 8-byte
-    // reads), B = P^T (lane: head n, the same 8 tokens): the K-slot order agrees.
+    // A = C^T: lane (g, n) needs column 16rt+n of tokens 4g..4g+3 (K-slots 0..3) and
+    // 16+4g..16+4g+3 (slots 4..7); lane (g, j) of the transpose read points at row
+    // 4g+j/4, columns 16rt+4(j%4).. .  B = P^T (lane: head n, the same 8 tokens).
+    const uint16_t* src = myl + (4 * g + (n >> 2)) * UP + 4 * (n & 3);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        const uint16_t* src = myl + (16 * rt + n) * TS + 4 * g;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 16);
+        const u32x2 lo = lds_read_tr16(src + 16 * rt);
+        const u32x2 hi = lds_read_tr16(src + 16 * UP + 16 * rt);
         acc[rt] = T::mma32(__builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb, acc[rt]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -183,7 +197,7 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
     constexpr int UPP = PS / 32;      // 32-token units per page
     constexpr int KS = KV / 32, RS = (RP + 31) / 32;
     constexpr int RT = KV / 16;       // 16-row tiles of O^T
-    constexpr int TBUF = KV * kTransposePitch;  // per-wave transpose buffer, 16-bit words
+    constexpr int TBUF = 32 * unit_pitch<KV>();  // per-wave LDS unit tile, 16-bit words
     constexpr int MSTRIDE = KV + 4;   // LDS merge pitch, floats
     constexpr int THREADS = 64 * WAVES;
     static_assert(16 * MSTRIDE * 4 <= TBUF * 2, "merge buffer aliases transpose buffer");
