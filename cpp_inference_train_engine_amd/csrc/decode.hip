@@ -236,21 +236,6 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
             trace[1] = wall_clock64() + (unsigned long long)(row & 0);
 #endif
 
-        // Q tile to LDS (heads >= H and the rope padding are zero), shared by the waves.
-        for (int i = tid; i < 16 * (QS / 8); i += THREADS) {
-            const int h = i / (QS / 8), c8 = (i % (QS / 8)) * 8;
-            u32x4 v = {0, 0, 0, 0};
-            if (h < a.H) {
-                if (c8 < KV)
-                    v = *reinterpret_cast<const u32x4*>(a.q_latent + ((long long)row * a.H + h) * KV + c8);
-                else if (c8 - KV < RP)
-                    v = *reinterpret_cast<const u32x4*>(a.q_rope + ((long long)row * a.H + h) * RP +
-                                                        c8 - KV);
-            }
-            *reinterpret_cast<u32x4*>(q_s + h * QS + c8) = v;
-        }
-        __syncthreads();
-
         float m_run = -INFINITY, l_run = 0.0f;
         floatx4 acc[RT];
 #pragma unroll
@@ -284,6 +269,22 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
             v0 = issue(ub0, 0);
         if (nk > 1)
             v1 = issue(ub1, 1);
+        // Q tile to LDS (heads >= H and the rope padding are zero), shared by the waves;
+        // fetched while the first units are in flight.
+        for (int i = tid; i < 16 * (QS / 8); i += THREADS) {
+            const int h = i / (QS / 8), c8 = (i % (QS / 8)) * 8;
+            u32x4 v = {0, 0, 0, 0};
+            if (h < a.H) {
+                if (c8 < KV)
+                    v = *reinterpret_cast<const u32x4*>(a.q_latent + ((long long)row * a.H + h) * KV + c8);
+                else if (c8 - KV < RP)
+                    v = *reinterpret_cast<const u32x4*>(a.q_rope + ((long long)row * a.H + h) * RP +
+                                                        c8 - KV);
+            }
+            *reinterpret_cast<u32x4*>(q_s + h * QS + c8) = v;
+        }
+        __syncthreads();
+
         for (int k = 0; k < nk; k += 2) {
             if (v0 > 0)
                 process_unit<T, KV, RP>(ub0, v0, q_s, a.scale_log2, m_run, l_run, acc, myl, g, n);
