@@ -7,16 +7,24 @@ random page permutation), N(0,1) cache contents.
 
 A timed step = the attention path of one batched decode step for all 10 layers:
 GPU metadata build, then per layer the paged latent append and the absorbed
-split-K decode attention.  Inputs are resident in HBM before timing starts.
+split-K decode attention.  Inputs are resident in HBM before timing starts.  The
+step is captured once in a HIP graph and replayed (the launch pattern a serving
+loop uses); K replays are timed between two synchronisations.
 
-Prints ONE JSON line (driver contract); the roofline block reports the decode-
-attention launch (decode kernel + split merge) measured live with HIP events.
+The roofline block reports one mla_decode_attention call (decode_mfma_kernel +
+merge_kernel, one layer), captured back-to-back over the 10 layer pools in a
+graph and timed with HIP events on the capturing stream.  `traffic` comes from
+the FETCH_SIZE / WRITE_SIZE passes recorded under profiles/ (scaled by the same
+counters over a plain copy of known size, run by --copy-probe-mib).
+
+Prints ONE JSON line (driver contract).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -26,26 +34,45 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
+N_LAYERS = 10
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "pmc_decode_attention_config3.txt")
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sessions", type=int, default=64)
     ap.add_argument("--target-blocks", type=int, default=1024)
     ap.add_argument("--split-pages", type=int, default=4)
-    ap.add_argument("--kernel-reps", type=int, default=200)
+    ap.add_argument("--kernel-reps", type=int, default=50,
+                    help="graph replays of 20 back-to-back attention calls")
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="seconds of CPU work per baseline leg (1 thread, then all threads)")
     ap.add_argument("--flags", type=int, default=0)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (counter calibration)")
     return ap.parse_args()
 
 
+def traffic_from_profile(path=TRAFFIC_FILE):
+    """HBM bytes per mla_decode_attention call, as recorded by the counter passes."""
+    try:
+        with open(path) as f:
+            m = re.search(r"^traffic_bytes_per_call:\s*(\d+)", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def cpu_baseline(batch, seconds: float):
-    """Oracle (fp32 C restatement of CpuDecoder's absorbed attention, one thread) on a
-    bounded sample: whole layers of the same 64-session batch, repeated until `seconds`."""
+    """Oracle (fp32 C restatement of CpuDecoder's absorbed attention, inference.cpp:116-153)
+    on a bounded sample: whole layers of the same 64-session batch, repeated for `seconds`,
+    first on one thread (the reference's serial decode) and then one session per thread
+    over the host cores (forks decode concurrently, inference.cpp:238)."""
     import oracle
     B = batch.q_latent.shape[0]
     table = np.full((B, batch.max_pages), -1, np.int32)
@@ -56,23 +83,46 @@ def cpu_baseline(batch, seconds: float):
     ql = oracle.bits_to_f32(batch.q_latent, batch.dtype)
     qr = oracle.bits_to_f32(batch.q_rope, batch.dtype)
     k_len = batch.k_len.astype(np.int32)
-    layers = 0
-    t0 = time.perf_counter()
-    while True:
-        oracle.attention_paged(batch.n_heads, batch.kv_rank, batch.rope_dim, batch.page_size,
-                               batch.dtype, cu_q, k_len, table, batch.pages[layers % len(batch.pages)],
-                               ql, qr, 0.125)
-        layers += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    per_layer = dt / layers
-    n_layers = len(batch.pages) if batch.pages.shape[0] > 1 else 10
-    return {"value": B / (per_layer * 10), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{layers} layers of decode attention over the same 64-session batch "
-                      f"({int(k_len.sum())} cached tokens/layer), fp32 oracle on 1 thread; "
-                      f"{per_layer * 1e3:.1f} ms/layer, scaled to 10 layers/step "
-                      f"(attention only, like the GPU step)"}
+
+    def per_layer(threads):
+        layers = 0
+        t0 = time.perf_counter()
+        while True:
+            oracle.attention_paged(batch.n_heads, batch.kv_rank, batch.rope_dim, batch.page_size,
+                                   batch.dtype, cu_q, k_len, table, batch.pages[0], ql, qr, 0.125,
+                                   threads=threads)
+            layers += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        return (time.perf_counter() - t0) / layers, layers
+
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    one, n_one = per_layer(1)
+    many, n_many = per_layer(cores)
+    return {"value": round(B / (many * N_LAYERS), 1), "unit": "tok/s", "cores": cores,
+            "kind": "port", "one_core_value": round(B / (one * N_LAYERS), 1),
+            "sample": f"decode attention of the same 64-session batch ({int(k_len.sum())} "
+                      f"cached tokens/layer), fp32 oracle: {n_one} layers on 1 thread "
+                      f"({one * 1e3:.1f} ms/layer) and {n_many} layers on {cores} threads, one "
+                      f"session per thread ({many * 1e3:.1f} ms/layer); tok/s = 64 tokens per "
+                      f"{N_LAYERS} layers (attention only, like the GPU step)"}
+
+
+def copy_probe(torch, mib: int):
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / 5
+    print(f"# copy probe: {mib} MiB read + {mib} MiB written per launch, {us:.1f} us, "
+          f"{2 * n / us / 1e3:.0f} GB/s", file=sys.stderr, flush=True)
+    del src, dst
 
 
 def main():
@@ -85,9 +135,10 @@ def main():
     import cpp_inference_train_engine_amd as mla
     from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
 
-    n_layers = 10
+    if args.copy_probe_mib > 0:
+        copy_probe(torch, args.copy_probe_mib)
     t_gen = time.perf_counter()
-    batch = ragged_decode_batch(B=args.sessions, n_layers=n_layers, seed=0)
+    batch = ragged_decode_batch(B=args.sessions, n_layers=N_LAYERS, seed=0)
     print(f"# workload generated in {time.perf_counter() - t_gen:.1f}s: "
           f"{int(batch.k_len.sum())} tokens/layer, {batch.num_pages} pages/layer", file=sys.stderr,
           flush=True)
@@ -95,13 +146,13 @@ def main():
     B, H = batch.q_latent.shape[:2]
     ctx_len, q_len = dev(batch.ctx_len), dev(batch.q_len)
     cu_pages, page_ids = dev(batch.cu_pages), dev(batch.page_ids)
-    cache = mla.PagedLatentCache(n_layers, batch.num_pages, 64, 128, 16, mla.DTYPE_F16,
+    cache = mla.PagedLatentCache(N_LAYERS, batch.num_pages, 64, 128, 16, mla.DTYPE_F16,
                                  storage=dev(batch.pages.view(np.int16)).view(torch.float16))
     ql = dev(batch.q_latent.view(np.int16)).view(torch.float16)
     qr = dev(batch.q_rope.view(np.int16)).view(torch.float16)
     g = torch.Generator(device="cuda").manual_seed(1)
-    new_ckv = torch.randn((n_layers, B, 128), device="cuda", generator=g)
-    new_kr = torch.randn((n_layers, B, 16), device="cuda", generator=g)
+    new_ckv = torch.randn((N_LAYERS, B, 128), device="cuda", generator=g)
+    new_kr = torch.randn((N_LAYERS, B, 16), device="cuda", generator=g)
     max_work = args.target_blocks + 2 * B
     out = torch.empty((B, H, 128), dtype=torch.float32, device="cuda")
     ws = mla.decode_workspace(max_work, B, H, 128)
@@ -113,41 +164,66 @@ def main():
                                   target_blocks=args.target_blocks, max_work=max_work,
                                   max_rows=B)
 
-    rb = meta()
-    info = rb.read_info()
-
-    def step(rb):
+    def step():
         rb = meta()
-        for l in range(n_layers):
+        for l in range(N_LAYERS):
             mla.append_latent(cache, l, new_ckv[l], new_kr[l], rb.slot_mapping)
             mla.decode_attention(rb, cache.layer(l), ql, qr, scale, kv_rank=128, rope_dim=16,
                                  out=out, workspace=ws, flags=args.flags)
         return rb
 
+    rb = step()
+    info = rb.read_info()  # raises on a metadata error
+    torch.cuda.synchronize()
+
+    def attn_calls(n):
+        for i in range(n):
+            mla.decode_attention(rb, cache.layer(i % N_LAYERS), ql, qr, scale, kv_rank=128,
+                                 rope_dim=16, out=out, workspace=ws, flags=args.flags)
+
+    calls_per_replay = 2 * N_LAYERS
+    if args.no_graph:
+        run_step, run_calls = step, (lambda: attn_calls(calls_per_replay))
+    else:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):  # warm the allocator outside capture
+            step()
+            attn_calls(1)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g_step, g_attn = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_step):
+            step()
+        with torch.cuda.graph(g_attn):
+            attn_calls(calls_per_replay)
+        run_step, run_calls = g_step.replay, g_attn.replay
+
     for _ in range(args.warmup):
-        rb = step(rb)
+        run_step()
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
     for _ in range(args.steps):
-        rb = step(rb)
+        run_step()
     t1.record()
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / args.steps
-    # Dominant kernel: decode attention per layer, back-to-back over the 10 layer pools
-    # (389 MB working set > the 256 MB Infinity Cache), timed with HIP events.
-    reps = args.kernel_reps
+
+    # Dominant kernel: one decode attention call per layer, back-to-back over the 10 layer
+    # pools (389 MB working set > the 256 MB Infinity Cache).
+    run_calls()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(reps):
-        mla.decode_attention(rb, cache.layer(i % n_layers), ql, qr, scale, kv_rank=128,
-                             rope_dim=16, out=out, workspace=ws, flags=args.flags)
+    for _ in range(args.kernel_reps):
+        run_calls()
     e1.record()
     torch.cuda.synchronize()
-    us_launch = e0.elapsed_time(e1) * 1e3 / reps
+    us_call = e0.elapsed_time(e1) * 1e3 / (args.kernel_reps * calls_per_replay)
     rb.read_info()
     bytes_layer = batch.cache_bytes_per_layer()
-    achieved = bytes_layer / (us_launch * 1e-6) / 1e9
+    achieved = bytes_layer / (us_call * 1e-6) / 1e9
     result = {
         "metric": "MLA decode tok/s + attn-kernel HBM GB/s (% of peak), 64 ragged sessions",
         "value": round(B / (ms_step * 1e-3), 1),
@@ -164,13 +240,16 @@ def main():
         "config": {"workload": "config 3 attention path: 64 ragged sessions, len U[128,4096], "
                                "mla36m latent shape (H=8, kv_rank=128, rope=16), 10 layers, "
                                "fp16 64-token pages; step = metadata + 10 x (append + decode "
-                               "attention); projections/FFN/logits not in this step yet",
+                               "attention), one HIP graph; projections/FFN/logits not in this "
+                               "step",
                    "sessions": B, "cached_tokens_per_layer": int(batch.k_len.sum()),
-                   "split_pages": info[1], "work_items": info[0]},
+                   "split_pages": info[1], "work_items": info[0],
+                   "timing": "eager" if args.no_graph else "hip graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "mla_decode_attention (decode + merge)",
-                     "us_per_launch": round(us_launch, 3), "bytes_per_launch": bytes_layer},
+                     "traffic": traffic_from_profile(),
+                     "kernel": "mla_decode_attention = decode_mfma_kernel + merge_kernel",
+                     "us_per_call": round(us_call, 3), "bytes_per_call": bytes_layer},
     }
     if not args.no_cpu_baseline:
         one = ragged_decode_batch(B=args.sessions, n_layers=1, seed=0)

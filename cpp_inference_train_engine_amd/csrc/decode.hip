@@ -10,19 +10,24 @@
 // softmax state (m, l, o) of its pages; sessions with one item write the
 // final row directly, the rest are combined by merge_kernel (log-sum-exp).
 //
-// decode_mfma_kernel -- one wave per work item, pages of 64 tokens:
-//   S^T[tok][head] = K[tok][:] . Q^T  on v_mfma_f32_16x16x32 (latent) and
-//   16x16x16 (rope): the cache tile is the A operand straight from HBM (each
-//   lane loads 16 contiguous bytes of one token row) and Q^T (heads padded to
-//   16) is the B operand held in registers for the whole item.  The S^T
-//   output layout puts, in lane (g, n), head n and tokens 16t+4g+{0..3}: for a
-//   32-token block those 8 probabilities are exactly the lane's B operand of
-//   O^T = C^T . P^T, so P never leaves registers.  Only C^T needs a transpose:
-//   the already-loaded latent rows are written to LDS (32 tokens at a time) and
-//   read back column-wise.  Online softmax runs in the log2 domain with
-//   cross-lane max/sum over the 4 lanes that share a head (xor 16, 32).
-// decode_generic_kernel -- any H / kv_rank / rope / page size: one 256-thread
-//   block per (work item, head), VALU fp32.
+// decode_mfma_kernel -- one workgroup of 2 waves per work item, pages of 64 tokens
+//   in the tiled record layout, processed as 32-token units:
+//   S^T[tok][head] = K[tok][:] . Q^T on v_mfma_f32_16x16x32 (latent K-steps, then
+//   the rope key zero-padded to one 32-wide K-step): the unit's cache tile is the
+//   A operand straight from HBM (each 16-byte lane load reads 1 KB contiguously)
+//   and Q^T (heads padded to 16) is the B operand, read from the workgroup's LDS
+//   Q tile.  The S^T output layout puts, in lane (g, n), head n and tokens
+//   16t+4g+{0..3}: exactly the lane's B operand of O^T = C^T . P^T, so P never
+//   leaves registers.  C^T is obtained by writing the unit's latent rows to a
+//   per-wave row-major LDS tile and reading it back with the gfx950 transpose
+//   load (ds_read_b64_tr_b16).  Online softmax runs in the log2 domain with a
+//   lazy rescale (the shared max is only raised when a score exceeds it by 2^8).
+//   Each wave keeps the next unit's loads in flight while computing the current
+//   one; the two waves' states merge in LDS at the end of the item.
+// decode_generic_kernel -- any H / kv_rank / rope / page size / layout: one
+//   256-thread block per (work item, head), VALU fp32.
+// merge_kernel -- log-sum-exp combine of the split partials, one block per
+//   (session, head), launched after the decode kernel on the same stream.
 #include "mla_common.hpp"
 #include "mla_internal.hpp"
 
@@ -74,11 +79,18 @@ __device__ __forceinline__ void load_unit(UnitRegs<KV, RP>& u, const uint16_t* b
 }
 
 // Row-major latent unit in LDS for the C^T operand: [32 tokens][kv_rank + 16]
-// 16-bit words (the pad puts consecutive rows 32 bytes apart in the banks).
+// 16-bit words.  The pad puts consecutive rows 32 bytes apart in the banks, which
+// makes the transpose reads (4 rows x 32 bytes per 16 lanes) conflict-free; the
+// 16-byte row writes (8 or 16 lanes at a time, rows n = 0..15) then hit every bank
+// pair twice, so each row's 16-byte chunks are swapped in pairs (chunk c stored at
+// c ^ lds_swz(row)) when bit 2 and bit 3 of the row differ.  That XOR only flips the
+// lane-constant part of a transpose read's column, so the reads stay conflict-free
+// and keep immediate offsets.
 template <int KV>
 constexpr int unit_pitch() {
     return KV + 16;
 }
+__device__ __forceinline__ int lds_swz(int row) { return ((row >> 2) ^ (row >> 3)) & 1; }
 
 // Q tile in LDS: row h = [latent KV | rope padded to 32*RS | 8 pad], 16 rows.
 template <int KV, int RP>
@@ -123,12 +135,14 @@ __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int vali
             sc[t] = T::mma32(__builtin_bit_cast(V8, j < KS ? u.lat[t][j] : u.rop[t][j - KS]), b,
                              sc[t]);
     }
-    // Latent rows to the LDS tile: lane (g, n) stores token 16t+n, columns 32j+8g...
+    // Latent rows to the LDS tile: lane (g, n) stores token 16t+n, columns 32j+8g..+7 at
+    // 8-column chunk g ^ swz(n) (see lds_swz).
+    const int wchunk = g ^ lds_swz(n);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int j = 0; j < KS; ++j)
-            *reinterpret_cast<u32x4*>(myl + (16 * t + n) * UP + 32 * j + 8 * g) = u.lat[t][j];
+            *reinterpret_cast<u32x4*>(myl + (16 * t + n) * UP + 32 * j + 8 * wchunk) = u.lat[t][j];
     float mloc = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -166,7 +180,7 @@ __device__ __forceinline__ void process_unit(const UnitRegs<KV, RP>& u, int vali
     // A = C^T: lane (g, n) needs column 16rt+n of tokens 4g..4g+3 (K-slots 0..3) and
     // 16+4g..16+4g+3 (slots 4..7); lane (g, j) of the transpose read points at row
     // 4g+j/4, columns 16rt+4(j%4).. .  B = P^T (lane: head n, the same 8 tokens).
-    const uint16_t* src = myl + (4 * g + (n >> 2)) * UP + 4 * (n & 3);
+    const uint16_t* src = myl + (4 * g + (n >> 2)) * UP + 4 * ((n & 3) ^ (2 * lds_swz(4 * g)));
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const u32x2 lo = lds_read_tr16(src + 16 * rt);
@@ -213,12 +227,6 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
     uint16_t* myl = lds[wave];
     float* mb = reinterpret_cast<float*>(&lds[0][0]);  // [WAVES][16][MSTRIDE] after the loop
 
-#ifdef MLA_DECODE_TRACE
-    unsigned long long* trace = reinterpret_cast<unsigned long long*>(a.lse) +
-                                ((long long)blockIdx.x * WAVES + wave) * 8;
-    if (lane == 0)
-        trace[0] = wall_clock64();
-#endif
     for (int w = blockIdx.x; w < a.max_work; w += gridDim.x) {
         // One descriptor load (plus this wave's first page id) starts the item.
         const int32_t* d = a.work_desc + (long long)w * kWorkDescInts;
@@ -231,10 +239,6 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
         if (d[7] != 1)
             continue;  // not a decode row
         const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
-#ifdef MLA_DECODE_TRACE
-        if (lane == 0)
-            trace[1] = wall_clock64() + (unsigned long long)(row & 0);
-#endif
 
         float m_run = -INFINITY, l_run = 0.0f;
         floatx4 acc[RT];
@@ -300,12 +304,6 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
         }
         l_run += __shfl_xor(l_run, 16, 64);
         l_run += __shfl_xor(l_run, 32, 64);
-#ifdef MLA_DECODE_TRACE
-        if (lane == 0) {
-            trace[2] = wall_clock64() + (unsigned long long)(l_run != l_run);
-            trace[5] = w;
-        }
-#endif
 
         // ---- merge the WAVES softmax states of this work item in LDS ----
         if (g == 0) {
@@ -354,10 +352,6 @@ __attribute__((amdgpu_waves_per_eu(MLA_DECODE_WAVES_PER_EU, 8))) void decode_mfm
             }
         }
         __syncthreads();  // LDS and sm_* are reused by the next work item
-#ifdef MLA_DECODE_TRACE
-        if (lane == 0)
-            trace[3] = wall_clock64();
-#endif
     }
 }
 

@@ -80,6 +80,7 @@ def _declare(L):
         "orc_forward": (i, [vp, vp, vp, i, vp, vp, vp]),
         "orc_output_projection": (None, [vp, vp, vp]),
         "orc_decode": (i, [vp, vp, vp, vp, vp, i, C.c_uint16, i, i, vp]),
+        "orc_set_threads": (None, [i]),
         "orc_attention_paged": (i, [i, i, i, i, i, i, vp, vp, vp, i, vp, vp, vp, f, vp, vp]),
         "orc_build_metadata": (i, [i, vp, vp, vp, vp, i, i, i, i, i, i, i,
                                    vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
@@ -227,7 +228,7 @@ class Decoder:
 
 # --------------------------------------------------- paged attention ----
 def attention_paged(H, kv_rank, rope_dim, page_size, dtype, cu_q, k_len, page_table, pages,
-                    q_latent, q_rope, scale, want_lse=False):
+                    q_latent, q_rope, scale, want_lse=False, threads=1):
     cu_q = np.ascontiguousarray(cu_q, np.int32)
     k_len = np.ascontiguousarray(k_len, np.int32)
     page_table = np.ascontiguousarray(page_table, np.int32)
@@ -238,6 +239,7 @@ def attention_paged(H, kv_rank, rope_dim, page_size, dtype, cu_q, k_len, page_ta
     rows = int(cu_q[-1])
     out = np.zeros((rows, H, kv_rank), np.float32)
     lse = np.zeros((rows, H), np.float32) if want_lse else None
+    lib().orc_set_threads(int(threads))
     st = lib().orc_attention_paged(B, H, kv_rank, rope_dim, page_size, dtype, _p(cu_q),
                                    _p(k_len), _p(page_table), page_table.shape[1], _p(pages),
                                    _p(q_latent), _p(q_rope), float(scale), _p(out), _p(lse))

@@ -603,77 +603,99 @@ static size_t rope_index(int tiled, int slot, int c, int page_size, int kv_rank,
 /* ------------------------------------------------------------------------ */
 /* Absorbed attention over a paged 16-bit cache (inference.cpp:116-153)      */
 /* ------------------------------------------------------------------------ */
+static int g_threads = 1;
+
+void orc_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+
+/* One session of orc_attention_paged; cbuf/rbuf/scores hold k_len rows. */
+static void attend_session(int b, int H, int kv_rank, int rope_dim, int page_size, int dtype,
+                           int tiled, size_t rec, const int32_t* cu_q, const int32_t* k_len,
+                           const int32_t* page_table, int max_pages, const uint16_t* pages,
+                           const float* q_latent, const float* q_rope, float scale, float* out,
+                           float* lse, float* scores, float* cbuf, float* rbuf) {
+    const int nq = cu_q[b + 1] - cu_q[b];
+    const int kl = k_len[b];
+    for (int t = 0; t < kl; ++t) {
+        const int page = page_table[(size_t)b * max_pages + t / page_size];
+        const uint16_t* base = pages + (size_t)page * rec;
+        const int slot = t % page_size;
+        for (int r = 0; r < kv_rank; ++r)
+            cbuf[(size_t)t * kv_rank + r] = load16(base + lat_index(tiled, slot, r, kv_rank), dtype);
+        for (int j = 0; j < rope_dim; ++j)
+            rbuf[(size_t)t * rope_dim + j] =
+                load16(base + rope_index(tiled, slot, j, page_size, kv_rank, rope_dim), dtype);
+    }
+    for (int i = 0; i < nq; ++i) {
+        const int row = cu_q[b] + i;
+        const int len = kl - nq + i + 1;
+        for (int h = 0; h < H; ++h) {
+            const float* lq = q_latent + ((size_t)row * H + h) * kv_rank;
+            const float* qr = q_rope + ((size_t)row * H + h) * rope_dim;
+            for (int t = 0; t < len; ++t) {
+                float s = 0, sr = 0;
+                for (int r = 0; r < kv_rank; ++r)
+                    s += cbuf[(size_t)t * kv_rank + r] * lq[r];
+                for (int j = 0; j < rope_dim; ++j)
+                    sr += rbuf[(size_t)t * rope_dim + j] * qr[j];
+                scores[t] = sr + s;
+            }
+            float mx = scores[0] * scale;
+            for (int t = 0; t < len; ++t) {
+                scores[t] *= scale;
+                mx = fmaxf(mx, scores[t]);
+            }
+            float sum = 0;
+            for (int t = 0; t < len; ++t) {
+                scores[t] = expf(scores[t] - mx);
+                sum += scores[t];
+            }
+            for (int t = 0; t < len; ++t)
+                scores[t] /= sum;
+            float* o = out + ((size_t)row * H + h) * kv_rank;
+            for (int r = 0; r < kv_rank; ++r) {
+                float s = 0;
+                for (int t = 0; t < len; ++t)
+                    s += cbuf[(size_t)t * kv_rank + r] * scores[t];
+                o[r] = s;
+            }
+            if (lse)
+                lse[(size_t)row * H + h] = mx + logf(sum);
+        }
+    }
+}
+
 int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, int dtype,
                         const int32_t* cu_q, const int32_t* k_len, const int32_t* page_table,
                         int max_pages, const uint16_t* pages, const float* q_latent,
                         const float* q_rope, float scale, float* out, float* lse) {
     const size_t rec = (size_t)page_size * (size_t)(kv_rank + rope_dim);
     const int tiled = tiled_layout(page_size, kv_rank, rope_dim);
-    int max_len = 0;
-    for (int b = 0; b < B; ++b)
-        if (k_len[b] > max_len)
-            max_len = k_len[b];
-    float* scores = malloc((size_t)(max_len > 0 ? max_len : 1) * 4);
-    float* cbuf = malloc((size_t)(max_len > 0 ? max_len : 1) * (size_t)kv_rank * 4);
-    float* rbuf = malloc((size_t)(max_len > 0 ? max_len : 1) * (size_t)(rope_dim > 0 ? rope_dim : 1) * 4);
+    int max_len = 1;
     for (int b = 0; b < B; ++b) {
         const int nq = cu_q[b + 1] - cu_q[b];
         if (nq <= 0)
             continue;
-        const int kl = k_len[b];
-        if (kl < nq || (kl + page_size - 1) / page_size > max_pages) {
-            free(scores), free(cbuf), free(rbuf);
+        if (k_len[b] < nq || (k_len[b] + page_size - 1) / page_size > max_pages)
             return 1;
-        }
-        for (int t = 0; t < kl; ++t) {
-            const int page = page_table[(size_t)b * max_pages + t / page_size];
-            const uint16_t* base = pages + (size_t)page * rec;
-            const int slot = t % page_size;
-            for (int r = 0; r < kv_rank; ++r)
-                cbuf[(size_t)t * kv_rank + r] = load16(base + lat_index(tiled, slot, r, kv_rank), dtype);
-            for (int j = 0; j < rope_dim; ++j)
-                rbuf[(size_t)t * rope_dim + j] =
-                    load16(base + rope_index(tiled, slot, j, page_size, kv_rank, rope_dim), dtype);
-        }
-        for (int i = 0; i < nq; ++i) {
-            const int row = cu_q[b] + i;
-            const int len = kl - nq + i + 1;
-            for (int h = 0; h < H; ++h) {
-                const float* lq = q_latent + ((size_t)row * H + h) * kv_rank;
-                const float* qr = q_rope + ((size_t)row * H + h) * rope_dim;
-                for (int t = 0; t < len; ++t) {
-                    float s = 0, sr = 0;
-                    for (int r = 0; r < kv_rank; ++r)
-                        s += cbuf[(size_t)t * kv_rank + r] * lq[r];
-                    for (int j = 0; j < rope_dim; ++j)
-                        sr += rbuf[(size_t)t * rope_dim + j] * qr[j];
-                    scores[t] = sr + s;
-                }
-                float mx = scores[0] * scale;
-                for (int t = 0; t < len; ++t) {
-                    scores[t] *= scale;
-                    mx = fmaxf(mx, scores[t]);
-                }
-                float sum = 0;
-                for (int t = 0; t < len; ++t) {
-                    scores[t] = expf(scores[t] - mx);
-                    sum += scores[t];
-                }
-                for (int t = 0; t < len; ++t)
-                    scores[t] /= sum;
-                float* o = out + ((size_t)row * H + h) * kv_rank;
-                for (int r = 0; r < kv_rank; ++r) {
-                    float s = 0;
-                    for (int t = 0; t < len; ++t)
-                        s += cbuf[(size_t)t * kv_rank + r] * scores[t];
-                    o[r] = s;
-                }
-                if (lse)
-                    lse[(size_t)row * H + h] = mx + logf(sum);
-            }
-        }
+        if (k_len[b] > max_len)
+            max_len = k_len[b];
     }
-    free(scores), free(cbuf), free(rbuf);
+    /* Sessions are independent (the reference decodes one session per fork and
+       thread, src/infer/inference.cpp:238); the thread count does not change any
+       result bit. */
+#pragma omp parallel num_threads(g_threads)
+    {
+        float* scores = malloc((size_t)max_len * 4);
+        float* cbuf = malloc((size_t)max_len * (size_t)kv_rank * 4);
+        float* rbuf = malloc((size_t)max_len * (size_t)(rope_dim > 0 ? rope_dim : 1) * 4);
+#pragma omp for schedule(dynamic, 1)
+        for (int b = 0; b < B; ++b)
+            if (cu_q[b + 1] - cu_q[b] > 0)
+                attend_session(b, H, kv_rank, rope_dim, page_size, dtype, tiled, rec, cu_q, k_len,
+                               page_table, max_pages, pages, q_latent, q_rope, scale, out, lse,
+                               scores, cbuf, rbuf);
+        free(scores), free(cbuf), free(rbuf);
+    }
     return 0;
 }
 

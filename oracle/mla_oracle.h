@@ -82,6 +82,9 @@ int orc_decode(const orc_config* c, const float* params, const float* out_proj, 
                float* rope, int position, uint16_t token, int absorbed, int round_cache,
                float* logits);
 
+/* Threads used by orc_attention_paged (default 1; sessions run in parallel). */
+void orc_set_threads(int n);
+
 /* ---- Absorbed MLA attention over a paged cache (inference.cpp:116-153, fp32).
  * Page record layout (one per page, per layer): latent section
  * (page_size x kv_rank) then rope section (page_size x rope_dim), 16-bit

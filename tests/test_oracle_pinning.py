@@ -294,6 +294,20 @@ def test_attention_paged_equals_contiguous_decoder_cache(orc):
     assert bits.shape[1] == rec
 
 
+def test_attention_paged_threads_change_no_bit(orc):
+    """The CPU baseline runs sessions on several threads; every result bit must equal the
+    one-thread run (sessions are independent)."""
+    rng = np.random.default_rng(13)
+    H, kv, rp, ps = 4, 32, 8, 16
+    lens, table, bits, ql, qr, cu_q = _paged_case(rng, 9, H, kv, rp, ps, 0, max_len=90)
+    one = orc.attention_paged(H, kv, rp, ps, 0, cu_q, lens, table, bits, ql, qr, 0.3,
+                              want_lse=True, threads=1)
+    many = orc.attention_paged(H, kv, rp, ps, 0, cu_q, lens, table, bits, ql, qr, 0.3,
+                               want_lse=True, threads=4)
+    np.testing.assert_array_equal(one[0], many[0])
+    np.testing.assert_array_equal(one[1], many[1])
+
+
 def test_attention_lse(orc):
     rng = np.random.default_rng(2)
     H, kv, rp, ps = 2, 8, 4, 4
