@@ -11,11 +11,13 @@ split-K decode attention.  Inputs are resident in HBM before timing starts.  The
 step is captured once in a HIP graph and replayed (the launch pattern a serving
 loop uses); K replays are timed between two synchronisations.
 
-The roofline block reports one mla_decode_attention call (decode_mfma_kernel +
-merge_kernel, one layer), captured back-to-back over the 10 layer pools in a
-graph and timed with HIP events on the capturing stream.  `traffic` comes from
-the FETCH_SIZE / WRITE_SIZE passes recorded under profiles/ (scaled by the same
-counters over a plain copy of known size, run by --copy-probe-mib).
+The roofline block reports the dominant kernel, decode_page_kernel (one
+mla_decode_partials call per layer), launched back-to-back over the 10 layer
+pools in a graph and timed with HIP events on the stream the graph replays on;
+`attention_call` reports the whole mla_decode_attention call (+ merge_kernel)
+the same way.  `traffic` comes from the FETCH_SIZE / WRITE_SIZE passes recorded
+under profiles/ (scaled by the same counters over a plain copy of known size,
+run by --copy-probe-mib).
 
 Prints ONE JSON line (driver contract).
 """
@@ -35,7 +37,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
 N_LAYERS = 10
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "pmc_decode_attention_config3.txt")
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "pmc_decode_page_kernel_config3.txt")
 
 
 def parse():
@@ -59,10 +61,10 @@ def parse():
 
 
 def traffic_from_profile(path=TRAFFIC_FILE):
-    """HBM bytes per mla_decode_attention call, as recorded by the counter passes."""
+    """HBM bytes per decode_page_kernel launch, as recorded by the counter passes."""
     try:
         with open(path) as f:
-            m = re.search(r"^traffic_bytes_per_call:\s*(\d+)", f.read(), re.M)
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
         return int(m.group(1)) if m else None
     except OSError:
         return None
@@ -153,7 +155,9 @@ def main():
     g = torch.Generator(device="cuda").manual_seed(1)
     new_ckv = torch.randn((N_LAYERS, B, 128), device="cuda", generator=g)
     new_kr = torch.randn((N_LAYERS, B, 16), device="cuda", generator=g)
-    max_work = args.target_blocks + 2 * B
+    # The host knows every session's length, so the work-item count is exact.
+    pages_per_session = (batch.k_len + 63) // 64
+    max_work = int(((pages_per_session + args.split_pages - 1) // args.split_pages).sum())
     out = torch.empty((B, H, 128), dtype=torch.float32, device="cuda")
     ws = mla.decode_workspace(max_work, B, H, 128)
     scale = 1.0 / 8.0
@@ -176,28 +180,35 @@ def main():
     info = rb.read_info()  # raises on a metadata error
     torch.cuda.synchronize()
 
-    def attn_calls(n):
+    def attn_calls(n, fn):
         for i in range(n):
-            mla.decode_attention(rb, cache.layer(i % N_LAYERS), ql, qr, scale, kv_rank=128,
-                                 rope_dim=16, out=out, workspace=ws, flags=args.flags)
+            fn(rb, cache.layer(i % N_LAYERS), ql, qr, scale, kv_rank=128, rope_dim=16, out=out,
+               workspace=ws, flags=args.flags)
 
     calls_per_replay = 2 * N_LAYERS
+    kinds = {"partials": mla.decode_partials, "attention": mla.decode_attention}
     if args.no_graph:
-        run_step, run_calls = step, (lambda: attn_calls(calls_per_replay))
+        run_step = step
+        runners = {k: (lambda f=f: attn_calls(calls_per_replay, f)) for k, f in kinds.items()}
     else:
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):  # warm the allocator outside capture
             step()
-            attn_calls(1)
+            attn_calls(1, mla.decode_attention)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
-        g_step, g_attn = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        g_step = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g_step):
             step()
-        with torch.cuda.graph(g_attn):
-            attn_calls(calls_per_replay)
-        run_step, run_calls = g_step.replay, g_attn.replay
+        runners = {}
+        for k, f in kinds.items():
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                attn_calls(calls_per_replay, f)
+            runners[k] = g
+        run_step = g_step.replay
+        runners = {k: g.replay for k, g in runners.items()}
 
     for _ in range(args.warmup):
         run_step()
@@ -210,20 +221,25 @@ def main():
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / args.steps
 
-    # Dominant kernel: one decode attention call per layer, back-to-back over the 10 layer
-    # pools (389 MB working set > the 256 MB Infinity Cache).
-    run_calls()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.kernel_reps):
-        run_calls()
-    e1.record()
-    torch.cuda.synchronize()
-    us_call = e0.elapsed_time(e1) * 1e3 / (args.kernel_reps * calls_per_replay)
+    # Per-launch time of the dominant kernel (decode_page_kernel, one mla_decode_partials
+    # call) and of the whole attention call (+ merge_kernel), each from back-to-back calls
+    # over the 10 layer pools (389 MB working set > the 256 MB Infinity Cache), timed with
+    # HIP events on the stream the graphs replay on.
+    us = {}
+    for k, run in runners.items():
+        run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.kernel_reps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        us[k] = e0.elapsed_time(e1) * 1e3 / (args.kernel_reps * calls_per_replay)
     rb.read_info()
     bytes_layer = batch.cache_bytes_per_layer()
-    achieved = bytes_layer / (us_call * 1e-6) / 1e9
+    achieved = bytes_layer / (us["partials"] * 1e-6) / 1e9
+    attn_gbs = bytes_layer / (us["attention"] * 1e-6) / 1e9
     result = {
         "metric": "MLA decode tok/s + attn-kernel HBM GB/s (% of peak), 64 ragged sessions",
         "value": round(B / (ms_step * 1e-3), 1),
@@ -248,8 +264,11 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profile(),
-                     "kernel": "mla_decode_attention = decode_mfma_kernel + merge_kernel",
-                     "us_per_call": round(us_call, 3), "bytes_per_call": bytes_layer},
+                     "kernel": "decode_page_kernel (mla_decode_partials, one layer)",
+                     "us_per_launch": round(us["partials"], 3), "bytes_per_launch": bytes_layer},
+        "attention_call": {"kernels": "decode_page_kernel + merge_kernel (mla_decode_attention)",
+                           "us": round(us["attention"], 3), "GB/s": round(attn_gbs, 1),
+                           "frac": round(attn_gbs / HBM_PEAK_GBS, 4)},
     }
     if not args.no_cpu_baseline:
         one = ragged_decode_batch(B=args.sessions, n_layers=1, seed=0)

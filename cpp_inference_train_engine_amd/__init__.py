@@ -46,6 +46,12 @@ _SIGNATURES = {
                              [C.c_void_p] * 2 + [C.c_int] * 2 + [C.c_void_p] * 8 +
                              [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
                               C.c_int]),
+    "mla_decode_partials": (C.c_int, [C.c_void_p] + [C.c_int] * 6 + [C.c_float] +
+                            [C.c_void_p] * 2 + [C.c_int] * 2 + [C.c_void_p] * 8 +
+                            [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t,
+                             C.c_int]),
+    "mla_decode_merge": (C.c_int, [C.c_void_p] + [C.c_int] * 3 + [C.c_void_p] * 4 +
+                         [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
 }
 
 
@@ -91,8 +97,9 @@ def stream_handle(stream=None) -> int | None:
 
 from .ops import (  # noqa: E402  (re-exported operator interface)
     PagedLatentCache, RaggedBatch, append_latent, build_metadata, decode_attention,
-    decode_workspace, decode_workspace_bytes)
+    decode_merge, decode_partials, decode_workspace, decode_workspace_bytes)
 
 __all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
+           "decode_partials", "decode_merge",
            "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",
            "DTYPE_BF16"]

@@ -103,30 +103,34 @@ size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, i
     return partial_bytes(max_work, n_heads, kv_rank);
 }
 
-int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
-                         int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
-                         const int32_t* page_table, int max_pages, int num_pool_pages,
-                         const void* pages, const void* q_latent, const void* q_rope,
-                         const int32_t* num_splits, const int32_t* cu_splits,
-                         const int32_t* work_desc, const int32_t* work_pages, const int32_t* info,
-                         int max_work, float* out, float* lse, void* workspace,
-                         size_t workspace_bytes, int flags) {
+}  // extern "C"
+
+namespace {
+
+// Validates the decode-attention arguments and fills `a`; MLA_OK or an error status.
+int decode_args(const char* fn, int B, int n_heads, int kv_rank, int rope_dim, int page_size,
+                int dtype, float scale, const int32_t* cu_seqlens_q, const int32_t* page_table,
+                int max_pages, int num_pool_pages, const void* pages, const void* q_latent,
+                const void* q_rope, const int32_t* num_splits, const int32_t* cu_splits,
+                const int32_t* work_desc, const int32_t* work_pages, const int32_t* info,
+                int max_work, float* out, float* lse, void* workspace, size_t workspace_bytes,
+                DecodeArgs& a) {
     if (B < 0 || n_heads < 1 || kv_rank < 1 || kv_rank > 1024 || rope_dim < 0 || rope_dim > 1024 ||
         page_size < 1 || max_pages < 0 || num_pool_pages < 0 || max_work < 0 ||
-        max_work > kMaxWork ||
-        (dtype != MLA_DTYPE_F16 && dtype != MLA_DTYPE_BF16) || !(scale > 0.0f))
-        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: invalid argument");
+        max_work > kMaxWork || (dtype != MLA_DTYPE_F16 && dtype != MLA_DTYPE_BF16) ||
+        !(scale > 0.0f))
+        return fail(MLA_ERR_INVALID_ARGUMENT, std::string(fn) + ": invalid argument");
     if (B == 0 || max_work == 0)
         return MLA_OK;
     if (!cu_seqlens_q || !page_table || !pages || !q_latent || (rope_dim > 0 && !q_rope) ||
         !num_splits || !cu_splits || !work_desc || !work_pages || !info || !out)
-        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_attention: null buffer");
+        return fail(MLA_ERR_INVALID_ARGUMENT, std::string(fn) + ": null buffer");
     const size_t need = mla_decode_workspace_bytes(max_work, B, n_heads, kv_rank);
     if (!workspace || workspace_bytes < need)
         return fail(MLA_ERR_INVALID_ARGUMENT,
-                    "mla_decode_attention: workspace needs " + std::to_string(need) + " bytes");
-    const float* ws = static_cast<const float*>(workspace);
-    DecodeArgs a{};
+                    std::string(fn) + ": workspace needs " + std::to_string(need) + " bytes");
+    float* ws = static_cast<float*>(workspace);
+    a = DecodeArgs{};
     a.B = B;
     a.H = n_heads;
     a.kv_rank = kv_rank;
@@ -148,15 +152,90 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
     a.q_rope = static_cast<const uint16_t*>(q_rope);
     a.out = out;
     a.lse = lse;
-    a.part_o = const_cast<float*>(ws);
-    a.part_ml = const_cast<float*>(ws) + (size_t)max_work * n_heads * kv_rank;
-    // The MFMA kernel issues 16-byte loads of q and of cache rows.
-    const bool aligned = ((reinterpret_cast<uintptr_t>(pages) | reinterpret_cast<uintptr_t>(q_latent) |
-                           reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out) |
-                           reinterpret_cast<uintptr_t>(workspace)) & 15) == 0;
-    const bool generic = (flags & MLA_DECODE_FORCE_GENERIC) || !aligned;
-    return gpu_status(launch_decode(a, dtype, generic, static_cast<hipStream_t>(stream)),
-                      "mla_decode_attention");
+    a.part_o = ws;
+    a.part_ml = ws + (size_t)max_work * n_heads * kv_rank;
+    return MLA_OK;
+}
+
+// The MFMA kernel issues 16-byte loads of q and of cache rows and 16-byte stores.
+bool use_generic(const DecodeArgs& a, const void* workspace, int flags) {
+    const bool aligned =
+        ((reinterpret_cast<uintptr_t>(a.pages) | reinterpret_cast<uintptr_t>(a.q_latent) |
+          reinterpret_cast<uintptr_t>(a.q_rope) | reinterpret_cast<uintptr_t>(a.out) |
+          reinterpret_cast<uintptr_t>(workspace)) &
+         15) == 0;
+    return (flags & MLA_DECODE_FORCE_GENERIC) || !aligned;
+}
+
+}  // namespace
+
+extern "C" {
+
+#define MLA_DECODE_PARAMS                                                                       \
+    void *stream, int B, int n_heads, int kv_rank, int rope_dim, int page_size, int dtype,       \
+        float scale, const int32_t *cu_seqlens_q, const int32_t *page_table, int max_pages,      \
+        int num_pool_pages, const void *pages, const void *q_latent, const void *q_rope,         \
+        const int32_t *num_splits, const int32_t *cu_splits, const int32_t *work_desc,           \
+        const int32_t *work_pages, const int32_t *info, int max_work, float *out, float *lse,    \
+        void *workspace, size_t workspace_bytes, int flags
+#define MLA_DECODE_ARGS(fn)                                                                     \
+    fn, B, n_heads, kv_rank, rope_dim, page_size, dtype, scale, cu_seqlens_q, page_table,        \
+        max_pages, num_pool_pages, pages, q_latent, q_rope, num_splits, cu_splits, work_desc,    \
+        work_pages, info, max_work, out, lse, workspace, workspace_bytes
+
+int mla_decode_attention(MLA_DECODE_PARAMS) {
+    DecodeArgs a;
+    if (int st = decode_args(MLA_DECODE_ARGS("mla_decode_attention"), a))
+        return st;
+    if (B == 0 || max_work == 0)
+        return MLA_OK;
+    const auto s = static_cast<hipStream_t>(stream);
+    if (int st = gpu_status(launch_decode_partials(a, dtype, use_generic(a, workspace, flags), s),
+                            "mla_decode_attention"))
+        return st;
+    return gpu_status(launch_merge(a, s), "mla_decode_attention");
+}
+
+int mla_decode_partials(MLA_DECODE_PARAMS) {
+    DecodeArgs a;
+    if (int st = decode_args(MLA_DECODE_ARGS("mla_decode_partials"), a))
+        return st;
+    if (B == 0 || max_work == 0)
+        return MLA_OK;
+    return gpu_status(launch_decode_partials(a, dtype, use_generic(a, workspace, flags),
+                                             static_cast<hipStream_t>(stream)),
+                      "mla_decode_partials");
+}
+
+int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_t* cu_seqlens_q,
+                     const int32_t* num_splits, const int32_t* cu_splits, const int32_t* info,
+                     int max_work, float* out, float* lse, const void* workspace,
+                     size_t workspace_bytes) {
+    if (B < 0 || n_heads < 1 || kv_rank < 1 || kv_rank > 1024 || max_work < 0 ||
+        max_work > kMaxWork)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_merge: invalid argument");
+    if (B == 0 || max_work == 0)
+        return MLA_OK;
+    if (!cu_seqlens_q || !num_splits || !cu_splits || !info || !out)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_merge: null buffer");
+    const size_t need = mla_decode_workspace_bytes(max_work, B, n_heads, kv_rank);
+    if (!workspace || workspace_bytes < need)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "mla_decode_merge: workspace needs " + std::to_string(need) + " bytes");
+    DecodeArgs a{};
+    a.B = B;
+    a.H = n_heads;
+    a.kv_rank = kv_rank;
+    a.max_work = max_work;
+    a.cu_q = cu_seqlens_q;
+    a.num_splits = num_splits;
+    a.cu_splits = cu_splits;
+    a.info = info;
+    a.out = out;
+    a.lse = lse;
+    a.part_o = const_cast<float*>(static_cast<const float*>(workspace));
+    a.part_ml = a.part_o + (size_t)max_work * n_heads * kv_rank;
+    return gpu_status(launch_merge(a, static_cast<hipStream_t>(stream)), "mla_decode_merge");
 }
 
 }  // extern "C"

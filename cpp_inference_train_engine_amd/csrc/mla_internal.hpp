@@ -45,8 +45,12 @@ struct DecodeArgs {
 
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
 hipError_t launch_append(const AppendArgs& a, int dtype, hipStream_t stream);
-// Returns hipErrorNotSupported-free status; picks MFMA or generic kernels.
-hipError_t launch_decode(const DecodeArgs& a, int dtype, bool force_generic, hipStream_t stream);
+// Decode kernel only (MFMA page kernel, or the generic one when force_generic or the
+// shape is outside it): final rows of one-item sessions, partials of the others.
+hipError_t launch_decode_partials(const DecodeArgs& a, int dtype, bool force_generic,
+                                  hipStream_t stream);
+// Log-sum-exp merge of the partials into the rows of split sessions.
+hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream);
 bool decode_mfma_supported(int H, int kv_rank, int rope_dim, int page_size);
 
 }  // namespace mla

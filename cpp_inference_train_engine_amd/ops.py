@@ -132,19 +132,15 @@ def decode_workspace(max_work: int, max_sessions: int, n_heads: int, kv_rank: in
     return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
-def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
-                     kv_rank: int, rope_dim: int, dtype: int = DTYPE_F16, out=None, lse=None,
-                     workspace=None, flags: int = 0, stream=None):
-    """(c) Absorbed MLA decode attention for every session with one query row.
-    q_latent [rows, H, kv_rank], q_rope [rows, H, rope_dim] in the cache dtype;
-    returns out [rows, H, kv_rank] fp32 (and fills lse [rows, H] if given)."""
+def _decode_call(fn, batch: RaggedBatch, pages, q_latent, q_rope, scale, kv_rank, rope_dim,
+                 dtype, out, lse, workspace, flags, stream):
     torch = _torch()
     rows, H = int(q_latent.shape[0]), int(q_latent.shape[1])
     if out is None:
         out = torch.zeros((rows, H, kv_rank), dtype=torch.float32, device=q_latent.device)
     if workspace is None:
         workspace = decode_workspace(batch.max_work, batch.B, H, kv_rank, q_latent.device)
-    check(lib().mla_decode_attention(
+    check(getattr(lib(), fn)(
         stream_handle(stream), batch.B, H, kv_rank, rope_dim, batch.page_size, dtype,
         float(scale), ptr(batch.cu_seqlens_q), ptr(batch.page_table), batch.max_pages,
         batch.num_pool_pages, ptr(pages), ptr(q_latent), ptr(q_rope), ptr(batch.num_splits),
@@ -153,8 +149,38 @@ def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, 
     return out
 
 
+def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
+                     kv_rank: int, rope_dim: int, dtype: int = DTYPE_F16, out=None, lse=None,
+                     workspace=None, flags: int = 0, stream=None):
+    """(c) Absorbed MLA decode attention for every session with one query row.
+    q_latent [rows, H, kv_rank], q_rope [rows, H, rope_dim] in the cache dtype;
+    returns out [rows, H, kv_rank] fp32 (and fills lse [rows, H] if given)."""
+    return _decode_call("mla_decode_attention", batch, pages, q_latent, q_rope, scale, kv_rank,
+                        rope_dim, dtype, out, lse, workspace, flags, stream)
+
+
+def decode_partials(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
+                    kv_rank: int, rope_dim: int, dtype: int = DTYPE_F16, out=None, lse=None,
+                    workspace=None, flags: int = 0, stream=None):
+    """First launch of decode_attention: final rows of one-item sessions, split partials
+    of the others in ``workspace`` (pass the same workspace to ``decode_merge``)."""
+    return _decode_call("mla_decode_partials", batch, pages, q_latent, q_rope, scale, kv_rank,
+                        rope_dim, dtype, out, lse, workspace, flags, stream)
+
+
+def decode_merge(batch: RaggedBatch, n_heads: int, kv_rank: int, out, workspace, lse=None,
+                 stream=None):
+    """Second launch of decode_attention: log-sum-exp merge of the split partials."""
+    check(lib().mla_decode_merge(
+        stream_handle(stream), batch.B, n_heads, kv_rank, ptr(batch.cu_seqlens_q),
+        ptr(batch.num_splits), ptr(batch.cu_splits), ptr(batch.info), batch.max_work, ptr(out),
+        ptr(lse), ptr(workspace), int(workspace.numel())))
+    return out
+
+
 __all__ = ["RaggedBatch", "build_metadata", "PagedLatentCache", "append_latent",
-           "decode_workspace_bytes", "decode_workspace", "decode_attention", "DTYPE_F16", "DTYPE_BF16"]
+           "decode_workspace_bytes", "decode_workspace", "decode_attention", "decode_partials",
+           "decode_merge", "DTYPE_F16", "DTYPE_BF16"]
 
 
 # ---------------------------------------------------------------- page layout ----

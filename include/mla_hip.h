@@ -139,10 +139,14 @@ int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_s
  * (may be NULL).  Rows of sessions with q_len != 1 are not written.
  * Work is split over the metadata's work items (split-K over pages); the
  * split partials of a session are merged with a log-sum-exp combine by a
- * second launch on the same stream.  `workspace` (device) must hold
+ * second launch on the same stream (the pair is also exposed separately:
+ * mla_decode_partials and mla_decode_merge, below).  `workspace` (device) must hold
  * mla_decode_workspace_bytes(max_work, B, H, kv_rank) bytes (partials; no
  * initialisation needed).  Calls that share a workspace must be ordered on
- * one stream. */
+ * one stream.  The production kernel runs one wave per page of a work item,
+ * so metadata built with split_pages == MLA_DECODE_SPLIT_PAGES keeps a whole
+ * item in flight. */
+#define MLA_DECODE_SPLIT_PAGES 4
 size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, int kv_rank);
 /* The metadata arguments (cu_seqlens_q, page_table, num_splits, cu_splits,
  * work_desc, work_pages, info, max_work) are the outputs of one
@@ -155,6 +159,25 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
                          const int32_t* work_desc, const int32_t* work_pages, const int32_t* info,
                          int max_work, float* out, float* lse, void* workspace,
                          size_t workspace_bytes, int flags);
+
+/* The two launches of mla_decode_attention, for callers that fold the merge into
+ * their own next kernel or run it later on the stream.  mla_decode_partials
+ * (same arguments) writes the final rows of sessions with one work item and
+ * leaves the other sessions' partials in `workspace`; mla_decode_merge then
+ * combines those partials into their rows of `out` (and `lse`).  Both must see
+ * the same metadata and workspace, in this order on one stream. */
+int mla_decode_partials(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
+                        int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
+                        const int32_t* page_table, int max_pages, int num_pool_pages,
+                        const void* pages, const void* q_latent, const void* q_rope,
+                        const int32_t* num_splits, const int32_t* cu_splits,
+                        const int32_t* work_desc, const int32_t* work_pages, const int32_t* info,
+                        int max_work, float* out, float* lse, void* workspace,
+                        size_t workspace_bytes, int flags);
+int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_t* cu_seqlens_q,
+                     const int32_t* num_splits, const int32_t* cu_splits, const int32_t* info,
+                     int max_work, float* out, float* lse, const void* workspace,
+                     size_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -48,6 +48,7 @@ def test_invalid_arguments_are_rejected_on_the_host():
     st = L.mla_decode_attention(None, 4, 8, 128, 16, 64, 0, 0.125, *([None] * 2), 4, 10,
                                 *([None] * 8), 16, None, None, None, 0, 0)
     assert st == 1  # null buffers
+    # partials [max_work][H][kv_rank + 2] fp32, rounded up to 256 bytes
     assert L.mla_decode_workspace_bytes(16, 4, 8, 128) == (16 * 8 * 130 * 4 + 255) // 256 * 256
     with pytest.raises(mla.MlaError) as e:
         mla.check(1)

@@ -282,3 +282,79 @@ def test_decode_workspace_reuse_across_calls(gpu, orc):
             torch.cuda.synchronize()
             want, _ = _oracle_decode(orc, batch, layer=layer)
             _check(out.cpu().numpy(), want, f"seed={seed} split={split} layer={layer}")
+
+
+def test_decode_split_merge_repeated_calls_and_graph_replays(gpu, orc):
+    """Production split (MLA_DECODE_SPLIT_PAGES pages per work item, one wave per page):
+    repeated eager calls on alternating layers and HIP-graph replays (with eager work in
+    between) share one workspace and must all match the oracle."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    batch = ragged_decode_batch(B=64, n_layers=2, seed=5)
+    _say(f"split merge: tokens={int(batch.k_len.sum())}")
+    B, H = batch.q_latent.shape[:2]
+    rb = gpu.build_metadata(_dev(batch.ctx_len), _dev(batch.q_len), _dev(batch.cu_pages),
+                            _dev(batch.page_ids), 64, batch.max_pages, batch.num_pages,
+                            split_pages=4, max_work=1024)
+    info = rb.read_info()
+    assert info[1] == 4 and info[0] > 2 * B
+    pages = _dev(batch.pages.view(np.int16)).view(torch.float16)
+    ql = _dev(batch.q_latent.view(np.int16)).view(torch.float16)
+    qr = _dev(batch.q_rope.view(np.int16)).view(torch.float16)
+    want = [_oracle_decode(orc, batch, layer=l)[0] for l in range(2)]
+    ws = gpu.decode_workspace(1024, B, H, 128)
+    out = torch.zeros((B, H, 128), dtype=torch.float32, device="cuda")
+    for call in range(4):
+        out.fill_(float("nan"))
+        gpu.decode_attention(rb, pages[call % 2], ql, qr, 0.125, kv_rank=128, rope_dim=16,
+                             out=out, workspace=ws)
+        torch.cuda.synchronize()
+        _check(out.cpu().numpy(), want[call % 2], f"eager call {call}")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gpu.decode_attention(rb, pages[1], ql, qr, 0.125, kv_rank=128, rope_dim=16,
+                                 out=out, workspace=ws)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _check(out.cpu().numpy(), want[1], f"graph replay {rep}")
+        gpu.decode_attention(rb, pages[0], ql, qr, 0.125, kv_rank=128, rope_dim=16, out=out,
+                             workspace=ws)
+        torch.cuda.synchronize()
+        _check(out.cpu().numpy(), want[0], f"eager call after replay {rep}")
+
+
+@pytest.mark.parametrize("flags", [0, 1], ids=["mfma", "generic"])
+def test_decode_partials_then_merge_equals_attention(gpu, orc, flags):
+    """mla_decode_partials + mla_decode_merge are the two launches of mla_decode_attention:
+    bit-identical output and lse, and the oracle bar."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    batch = ragged_decode_batch(B=40, seed=9)
+    _say(f"partials+merge flags={flags}")
+    B, H = batch.q_latent.shape[:2]
+    rb = gpu.build_metadata(_dev(batch.ctx_len), _dev(batch.q_len), _dev(batch.cu_pages),
+                            _dev(batch.page_ids), 64, batch.max_pages, batch.num_pages,
+                            split_pages=4)
+    pages = _dev(batch.pages[0].view(np.int16)).view(torch.float16)
+    ql = _dev(batch.q_latent.view(np.int16)).view(torch.float16)
+    qr = _dev(batch.q_rope.view(np.int16)).view(torch.float16)
+    lse_a = torch.zeros((B, H), dtype=torch.float32, device="cuda")
+    lse_b = torch.zeros((B, H), dtype=torch.float32, device="cuda")
+    ref = gpu.decode_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16, lse=lse_a,
+                               flags=flags)
+    ws = gpu.decode_workspace(rb.max_work, B, H, 128)
+    out = torch.full((B, H, 128), float("nan"), dtype=torch.float32, device="cuda")
+    gpu.decode_partials(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16, out=out,
+                        lse=lse_b, workspace=ws, flags=flags)
+    gpu.decode_merge(rb, H, 128, out, ws, lse=lse_b)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref) and torch.equal(lse_a, lse_b)
+    want, _ = _oracle_decode(orc, batch)
+    _check(out.cpu().numpy(), want, f"flags={flags}")
