@@ -1,23 +1,27 @@
 """Benchmark of the MLA ragged decode hot path on one MI355X.
 
-Workload ("config 3"): mla36m latent shape (8 heads,
-kv_rank 128, rope 16, 10 layers), 64 sessions with context lengths uniform in
-[128, 4096], one decode token each, fp16 paged latent cache (64-token pages at a
-random page permutation), N(0,1) cache contents.
+Workload ("config 3"): the mla36m model (10 blocks,
+d=512, 8 MLA heads, q-rank 192, KV rank 128, tied 16384 vocab; random-init
+weights with Model::create's scales, fp16 on the device), 64 sessions with
+context lengths uniform in [128, 4096], one decode token each, fp16 paged latent
+cache (64-token pages at a random page permutation), N(0,1) cache contents.
 
-A timed step = the attention path of one batched decode step for all 10 layers:
-GPU metadata build, then per layer the paged latent append and the absorbed
-split-K decode attention.  Inputs are resident in HBM before timing starts.  The
-step is captured once in a HIP graph and replayed (the launch pattern a serving
-loop uses); K replays are timed between two synchronisations.
+A timed step = one full batched decode step: the GPU metadata build, then
+mla_model_step (token embedding; per layer RMSNorm, the q / kv projections with
+the paged append, the W_uk absorption, the paged decode attention with its split
+merge, the combined W_uv.W_o output projection, the SwiGLU FFN; final RMSNorm,
+tied logits and the greedy token).  Each step feeds its greedy tokens back as the
+next step's tokens; the positions stay those of config 3 (each replay rewrites the
+same cache slots).  The step is captured once in a HIP graph and replayed; K
+replays are timed between two synchronisations.  Inputs are resident in HBM.
 
-The roofline block reports the dominant kernel, decode_page_kernel (one
-mla_decode_partials call per layer), launched back-to-back over the 10 layer
-pools in a graph and timed with HIP events on the stream the graph replays on;
-`attention_call` reports the whole mla_decode_attention call (+ merge_kernel)
-the same way.  `traffic` comes from the FETCH_SIZE / WRITE_SIZE passes recorded
-under profiles/ (scaled by the same counters over a plain copy of known size,
-run by --copy-probe-mib).
+The roofline block reports the dominant kernel of the path, decode_page_kernel
+(one mla_decode_partials call per layer), launched back-to-back over the 10
+layer pools in a graph and timed with HIP events on the stream the graph
+replays on; `attention_call` reports the whole mla_decode_attention call
+(+ merge_kernel) the same way.  `traffic` comes from the FETCH_SIZE /
+WRITE_SIZE passes recorded under profiles/ (scaled by the same counters over a
+plain copy of known size, run by --copy-probe-mib).
 
 Prints ONE JSON line (driver contract).
 """
@@ -52,8 +56,8 @@ def parse():
                     help="graph replays of 20 back-to-back attention calls")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0,
-                    help="seconds of CPU work per baseline leg (1 thread, then all threads)")
+    ap.add_argument("--cpu-seconds", type=float, default=6.0,
+                    help="seconds of CPU work per baseline leg (all threads, then 1 thread)")
     ap.add_argument("--flags", type=int, default=0)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
@@ -70,44 +74,52 @@ def traffic_from_profile(path=TRAFFIC_FILE):
         return None
 
 
-def cpu_baseline(batch, seconds: float):
-    """Oracle (fp32 C restatement of CpuDecoder's absorbed attention, inference.cpp:116-153)
-    on a bounded sample: whole layers of the same 64-session batch, repeated for `seconds`,
-    first on one thread (the reference's serial decode) and then one session per thread
-    over the host cores (forks decode concurrently, inference.cpp:238)."""
+def cpu_baseline(batch, params, seconds: float):
+    """The reference CPU path for the same step: the oracle's fp32 restatement of
+    CpuDecoder::decode (inference.cpp:69-174: projections, absorbed attention over the
+    session's contiguous cache, FFN, tied logits) on a bounded sample of the batch's
+    sessions, one session per thread (forks decode concurrently, inference.cpp:238),
+    repeated for `seconds`; then the same sample on one thread."""
+    import concurrent.futures as cf
     import oracle
-    B = batch.q_latent.shape[0]
-    table = np.full((B, batch.max_pages), -1, np.int32)
-    for b in range(B):
-        lst = batch.page_ids[batch.cu_pages[b]:batch.cu_pages[b + 1]]
-        table[b, :len(lst)] = lst
-    cu_q = np.arange(B + 1, dtype=np.int32)
-    ql = oracle.bits_to_f32(batch.q_latent, batch.dtype)
-    qr = oracle.bits_to_f32(batch.q_rope, batch.dtype)
-    k_len = batch.k_len.astype(np.int32)
-
-    def per_layer(threads):
-        layers = 0
-        t0 = time.perf_counter()
-        while True:
-            oracle.attention_paged(batch.n_heads, batch.kv_rank, batch.rope_dim, batch.page_size,
-                                   batch.dtype, cu_q, k_len, table, batch.pages[0], ql, qr, 0.125,
-                                   threads=threads)
-            layers += 1
-            if time.perf_counter() - t0 >= seconds:
-                break
-        return (time.perf_counter() - t0) / layers, layers
-
+    from cpp_inference_train_engine_amd.workloads import MLA36M
+    cfg = oracle.Config.from_dict(MLA36M)
     cores = max(1, min(16, len(os.sched_getaffinity(0))))
-    one, n_one = per_layer(1)
-    many, n_many = per_layer(cores)
-    return {"value": round(B / (many * N_LAYERS), 1), "unit": "tok/s", "cores": cores,
-            "kind": "port", "one_core_value": round(B / (one * N_LAYERS), 1),
-            "sample": f"decode attention of the same 64-session batch ({int(k_len.sum())} "
-                      f"cached tokens/layer), fp32 oracle: {n_one} layers on 1 thread "
-                      f"({one * 1e3:.1f} ms/layer) and {n_many} layers on {cores} threads, one "
-                      f"session per thread ({many * 1e3:.1f} ms/layer); tok/s = 64 tokens per "
-                      f"{N_LAYERS} layers (attention only, like the GPU step)"}
+    pick = np.argsort(batch.k_len)[np.linspace(0, len(batch.k_len) - 1, cores).astype(int)]
+    decs = []
+    proj = oracle.output_projection(cfg, params)  # prepare_projections, once per model
+    for b in pick:  # each sampled session at its config-3 length (cache contents N(0,1))
+        d = oracle.Decoder(cfg, params, absorbed=True, proj=proj)
+        n = int(batch.ctx_len[b])
+        gen = np.random.default_rng(int(b))
+        d.latent[:, :n] = gen.standard_normal((cfg.n_layers, n, cfg.kv_lora_rank), np.float32)
+        d.rope[:, :n] = gen.standard_normal((cfg.n_layers, n, cfg.head_dim_rope), np.float32)
+        decs.append((d, n))
+
+    def one(i):
+        d, n = decs[i]
+        d.position = n
+        d.decode(1)
+
+    def run(threads):
+        done, t0 = 0, time.perf_counter()
+        with cf.ThreadPoolExecutor(threads) as ex:
+            while True:
+                list(ex.map(one, range(len(decs))))
+                done += len(decs)
+                if time.perf_counter() - t0 >= seconds:
+                    break
+        return done / (time.perf_counter() - t0), done
+
+    many, n_many = run(cores)
+    single, n_single = run(1)
+    mean_ctx = float(np.mean([n for _, n in decs]))
+    return {"value": round(many, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+            "one_core_value": round(single, 2),
+            "sample": f"full decode step (oracle CpuDecoder restatement, fp32) of {len(decs)} "
+                      f"sessions spread over the batch's lengths (mean context {mean_ctx:.0f}): "
+                      f"{n_many} tokens on {cores} threads, one session per thread; "
+                      f"{n_single} tokens on 1 thread"}
 
 
 def copy_probe(torch, mib: int):
@@ -139,9 +151,12 @@ def main():
 
     if args.copy_probe_mib > 0:
         copy_probe(torch, args.copy_probe_mib)
+    from cpp_inference_train_engine_amd.workloads import MLA36M, model_params
     t_gen = time.perf_counter()
     batch = ragged_decode_batch(B=args.sessions, n_layers=N_LAYERS, seed=0)
-    print(f"# workload generated in {time.perf_counter() - t_gen:.1f}s: "
+    params = model_params(MLA36M, seed=0)
+    model = mla.HipModel(mla.ModelConfig.from_dict(MLA36M), params, max_batch=args.sessions)
+    print(f"# workload and model ready in {time.perf_counter() - t_gen:.1f}s: "
           f"{int(batch.k_len.sum())} tokens/layer, {batch.num_pages} pages/layer", file=sys.stderr,
           flush=True)
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
@@ -150,11 +165,11 @@ def main():
     cu_pages, page_ids = dev(batch.cu_pages), dev(batch.page_ids)
     cache = mla.PagedLatentCache(N_LAYERS, batch.num_pages, 64, 128, 16, mla.DTYPE_F16,
                                  storage=dev(batch.pages.view(np.int16)).view(torch.float16))
+    pools = [cache.layer(l) for l in range(N_LAYERS)]
     ql = dev(batch.q_latent.view(np.int16)).view(torch.float16)
     qr = dev(batch.q_rope.view(np.int16)).view(torch.float16)
-    g = torch.Generator(device="cuda").manual_seed(1)
-    new_ckv = torch.randn((N_LAYERS, B, 128), device="cuda", generator=g)
-    new_kr = torch.randn((N_LAYERS, B, 16), device="cuda", generator=g)
+    tokens = dev(np.random.default_rng(1).integers(0, MLA36M["vocab_size"], B).astype(np.int32))
+    logits = torch.empty((B, MLA36M["vocab_size"]), dtype=torch.float32, device="cuda")
     # The host knows every session's length, so the work-item count is exact.
     pages_per_session = (batch.k_len + 63) // 64
     max_work = int(((pages_per_session + args.split_pages - 1) // args.split_pages).sum())
@@ -170,10 +185,7 @@ def main():
 
     def step():
         rb = meta()
-        for l in range(N_LAYERS):
-            mla.append_latent(cache, l, new_ckv[l], new_kr[l], rb.slot_mapping)
-            mla.decode_attention(rb, cache.layer(l), ql, qr, scale, kv_rank=128, rope_dim=16,
-                                 out=out, workspace=ws, flags=args.flags)
+        model.step(rb, tokens, ctx_len, pools, ws, logits=logits, next_tokens=tokens)
         return rb
 
     rb = step()
@@ -251,13 +263,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 cache, f32 accumulate",
+        "dtype": "f16 weights/cache/MFMA operands, f32 accumulate",
         "data": "synthetic",
-        "config": {"workload": "config 3 attention path: 64 ragged sessions, len U[128,4096], "
-                               "mla36m latent shape (H=8, kv_rank=128, rope=16), 10 layers, "
-                               "fp16 64-token pages; step = metadata + 10 x (append + decode "
-                               "attention), one HIP graph; projections/FFN/logits not in this "
-                               "step",
+        "config": {"workload": "config 3: mla36m (10 layers, d=512, 8 MLA heads, q-rank 192, "
+                               "KV rank 128, tied 16384 vocab), random-init fp16 weights, 64 "
+                               "ragged sessions, len U[128,4096], fp16 64-token pages; step = "
+                               "metadata + full decode step (projections, paged append, "
+                               "attention, FFN, logits, greedy), one HIP graph",
                    "sessions": B, "cached_tokens_per_layer": int(batch.k_len.sum()),
                    "split_pages": info[1], "work_items": info[0],
                    "timing": "eager" if args.no_graph else "hip graph"},
@@ -270,9 +282,9 @@ def main():
                            "us": round(us["attention"], 3), "GB/s": round(attn_gbs, 1),
                            "frac": round(attn_gbs / HBM_PEAK_GBS, 4)},
     }
+    model.close()
     if not args.no_cpu_baseline:
-        one = ragged_decode_batch(B=args.sessions, n_layers=1, seed=0)
-        result["cpu_baseline"] = cpu_baseline(one, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(batch, params, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 

@@ -1,0 +1,79 @@
+// Device layout and launchers of the batched decode step (model.hip, model_capi.hip).
+//
+// Weight tiling.  A projection y = x.W with W [K x N] (the reference's [in x out],
+// ops.cpp:8-18) is stored as fp16 in MFMA B-operand order: K padded to a multiple of
+// 32, N to a multiple of 16 (padding is zero), and element (k, col) at
+//     ((nt * KT + kt) * 4 + g) * 128 + n * 8 + e
+// with nt = col/16, n = col%16, kt = k/32, g = (k%32)/8, e = k%8, KT = Kpad/32.  The
+// 64 lanes of a wave loading tile (nt, kt) read 1 KB contiguously (lane l: 16 bytes at
+// (nt*KT + kt)*512 + 8l).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace mla {
+
+struct ModelDims {
+    int vocab, d_model, H, nope, rope, dv, q_rank, kv_rank, d_ff, n_layers;
+    int qk;                    // nope + rope
+    float eps, theta;
+    int page_size;
+    int max_seq;   // max_sequence_length: RoPE table rows
+    // padded sizes (K dimensions to 32, N dimensions to 16; see above)
+    int d_pad;      // d_model -> 32
+    int q_pad;      // q_rank -> 32 (N of w_dq, K of w_uq)
+    int kvw_pad;    // kv_rank + rope -> 16 (N of w_dkv)
+    int qk_pad;     // qk -> 16 (per-head N of w_uq)
+    int nope_pad;   // nope -> 32 (K of the absorption)
+    int kv_pad;     // kv_rank -> 16 (N of the absorption)
+    int ctx_pad;    // H * kv_rank -> 32 (K of the output projection)
+    int ff_pad;     // d_ff -> 32 (N of gate/up, K of down)
+    int vocab_pad;  // vocab -> 16 (N of the tied logits)
+};
+
+struct LayerWeights {
+    const float *attn_norm, *q_norm, *kv_norm, *ffn_norm;
+    const uint16_t* w_dq_dkv;   // [d x (q_pad + kvw_pad)] tiled: q columns, then kv columns
+    const uint16_t* w_uq;       // [q_rank x H*qk_pad] tiled, head h at columns h*qk_pad..
+    const uint16_t* w_uk;       // H blocks [nope x kv_rank] tiled (W_uk_h^T)
+    const uint16_t* w_out;      // [H*kv_rank x d] tiled: combined W_uv.W_o
+    const uint16_t* w_gate_up;  // [d x 2*ff_pad] tiled, gate/up tiles interleaved
+    const uint16_t* w_down;     // [d_ff x d] tiled
+};
+
+struct StepArgs {
+    ModelDims dims;
+    int B, m_pad;              // rows, rows padded to 64
+    const int32_t* tokens;     // [B]
+    const int32_t* positions;  // [B] position of each new token (= cached tokens)
+    const int32_t* slot_mapping;
+    int num_pool_pages;
+    const uint16_t* embed;     // token_embedding [V x d] tiled as the logits W (K=d, N=V)
+    const float* final_norm;
+    const float2* rope_tab;    // [max_seq x rope/2] (cos, sin) of pos * theta^(-j/rope)
+    // activations (rows padded to m_pad; padding rows stay zero)
+    float *x, *res, *cq, *ctx;  // [m_pad x d_pad], [m_pad x d_pad], [m_pad x q_pad], [m_pad x H*kv_rank]
+    float* kvraw;               // [m_pad x kvw_pad] kv columns of [w_dq | w_dkv]
+    uint16_t *u;                // [m_pad x ff_pad] fp16
+    uint16_t *q_latent, *q_rope;  // [B x H x kv_rank], [B x H x rope] in the cache dtype
+    float* logits;              // [B x vocab]
+    float* arg_v;               // [B x parts] greedy partials
+    int32_t* arg_c;
+    int32_t* next_tokens;       // [B]
+};
+
+int g7_parts(const ModelDims& m);
+size_t g1_lds_bytes(const ModelDims& m);
+size_t g23_lds_bytes(const ModelDims& m);
+size_t dpad_lds_bytes(const ModelDims& m);
+hipError_t model_kernel_attributes();
+hipError_t launch_embed(const StepArgs& s, hipStream_t st);
+hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
+                            hipStream_t st);  // g1, then g23 (which appends to `pool`)
+hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, hipStream_t st);
+hipError_t launch_logits(const StepArgs& s, hipStream_t st);
+
+}  // namespace mla

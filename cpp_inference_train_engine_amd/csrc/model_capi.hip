@@ -1,0 +1,433 @@
+// C ABI of the batched decode step (include/mla_hip.h, "model" section): model
+// config validation, weight upload (fp16, tiled; see mla_model.hpp) and the step
+// driver that chains the model kernels (model.hip) with the paged decode attention
+// (decode.hip).
+#include "mla_capi_util.hpp"
+#include "mla_hip.h"
+#include "mla_internal.hpp"
+#include "mla_model.hpp"
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace mla {
+namespace {
+
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// ModelConfig::validate (src/model/config.cpp:20-48) and parameter_count (:7-19).
+size_t parameter_count(const mla_model_config& c) {
+    const size_t d = c.d_model, h = c.n_heads, q = c.q_lora_rank, kv = c.kv_lora_rank;
+    const size_t qk = (size_t)c.head_dim_nope + c.head_dim_rope;
+    const size_t kvw = kv + c.head_dim_rope;
+    return (size_t)c.vocab_size * d + d +
+           (size_t)c.n_layers * (d * q + q * h * qk + d * kvw +
+                                 kv * h * ((size_t)c.head_dim_nope + c.head_dim_value) +
+                                 h * (size_t)c.head_dim_value * d + 3 * d * (size_t)c.d_ff +
+                                 2 * d + q + kv);
+}
+
+int validate(const mla_model_config* c) {
+    if (!c)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "model config: null");
+    const std::pair<const char*, int> fields[] = {
+        {"vocab_size", c->vocab_size},       {"max_sequence_length", c->max_sequence_length},
+        {"n_layers", c->n_layers},           {"d_model", c->d_model},
+        {"n_heads", c->n_heads},             {"head_dim_nope", c->head_dim_nope},
+        {"head_dim_rope", c->head_dim_rope}, {"head_dim_value", c->head_dim_value},
+        {"q_lora_rank", c->q_lora_rank},     {"kv_lora_rank", c->kv_lora_rank},
+        {"d_ff", c->d_ff}};
+    for (const auto& [name, v] : fields)
+        if (v < 1 || v > 65535)
+            return fail(MLA_ERR_INVALID_ARGUMENT, std::string(name) + " must be in [1, 65535]");
+    if (c->vocab_size > 65535 || c->n_layers > 128 || c->n_heads > 256 ||
+        c->d_model % c->n_heads || c->head_dim_rope % 2)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "Invalid vocabulary/layer/head count, d_model divisibility, or odd RoPE "
+                    "dimension");
+    if (!std::isfinite(c->norm_epsilon) || c->norm_epsilon <= 0 || !std::isfinite(c->rope_theta) ||
+        c->rope_theta <= 1)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "Invalid normalization epsilon or RoPE theta");
+    if (parameter_count(*c) > 1000000000ULL)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "Configuration exceeds one billion parameters");
+    return MLA_OK;
+}
+
+uint16_t to_f16(float x) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x)); }
+
+// Packs W [K x N] (element (k, col) from `at`) into the tiled fp16 layout.
+template <typename F>
+std::vector<uint16_t> pack(int K, int N, int Kpad, int Npad, F at) {
+    const int KT = Kpad / 32, NT = Npad / 16;
+    std::vector<uint16_t> out((size_t)NT * KT * 512, 0);
+    for (int nt = 0; nt < NT; ++nt)
+        for (int kt = 0; kt < KT; ++kt) {
+            uint16_t* t = out.data() + ((size_t)nt * KT + kt) * 512;
+            for (int g = 0; g < 4; ++g)
+                for (int n = 0; n < 16; ++n)
+                    for (int e = 0; e < 8; ++e) {
+                        const int k = kt * 32 + g * 8 + e, col = nt * 16 + n;
+                        if (k < K && col < N)
+                            t[(g * 16 + n) * 8 + e] = to_f16(at(k, col));
+                    }
+        }
+    return out;
+}
+
+// Offsets of the reference parameter registry (include/mini_mla/model.hpp:15-30,
+// src/model/model.cpp:40-63): token_embedding, final_norm, then per layer attn_norm,
+// w_dq, q_norm, w_uq, w_dkv, kv_norm, w_uk, w_uv, w_o, ffn_norm, w_gate, w_up, w_down.
+enum { P_ATTN_NORM, P_W_DQ, P_Q_NORM, P_W_UQ, P_W_DKV, P_KV_NORM, P_W_UK, P_W_UV, P_W_O,
+       P_FFN_NORM, P_W_GATE, P_W_UP, P_W_DOWN, P_COUNT };
+
+struct Registry {
+    const float* embed;
+    const float* final_norm;
+    std::vector<const float*> layer;  // [L * P_COUNT]
+};
+
+Registry view(const mla_model_config& c, const float* p) {
+    const size_t d = c.d_model, q = c.q_lora_rank, kv = c.kv_lora_rank, H = c.n_heads;
+    const size_t qk = (size_t)c.head_dim_nope + c.head_dim_rope, kvw = kv + c.head_dim_rope;
+    const size_t sizes[P_COUNT] = {d,      d * q,  q,      q * H * qk, d * kvw,
+                                   kv,     kv * H * c.head_dim_nope,    kv * H * c.head_dim_value,
+                                   H * c.head_dim_value * d,           d,
+                                   d * c.d_ff, d * c.d_ff, (size_t)c.d_ff * d};
+    Registry r;
+    r.embed = p;
+    p += (size_t)c.vocab_size * d;
+    r.final_norm = p;
+    p += d;
+    for (int l = 0; l < c.n_layers; ++l)
+        for (int k = 0; k < P_COUNT; ++k) {
+            r.layer.push_back(p);
+            p += sizes[k];
+        }
+    return r;
+}
+
+struct Model {
+    mla_model_config cfg;
+    ModelDims dims;
+    int max_batch, m_pad_max, parts;
+    std::vector<void*> allocations;
+    std::vector<LayerWeights> layers;
+    const uint16_t* embed = nullptr;
+    const float* final_norm = nullptr;
+    const float* rope_tab = nullptr;
+    float *x, *res, *cq, *ctx, *kvraw, *logits, *arg_v;
+    uint16_t *u, *q_latent, *q_rope;
+    int32_t* arg_c;
+
+    ~Model() {
+        for (void* p : allocations)
+            (void)hipFree(p);
+    }
+    template <typename T>
+    hipError_t alloc(T*& out, size_t count) {
+        void* p = nullptr;
+        const hipError_t e = hipMalloc(&p, count * sizeof(T) + 16);
+        if (e != hipSuccess)
+            return e;
+        allocations.push_back(p);
+        out = static_cast<T*>(p);
+        return hipMemset(p, 0, count * sizeof(T) + 16);
+    }
+    template <typename T>
+    hipError_t upload(const T*& out, const std::vector<T>& host) {
+        T* p = nullptr;
+        hipError_t e = alloc(p, host.size());
+        if (e == hipSuccess)
+            e = hipMemcpy(p, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice);
+        out = p;
+        return e;
+    }
+};
+
+ModelDims make_dims(const mla_model_config& c, int page_size) {
+    ModelDims m{};
+    m.vocab = c.vocab_size;
+    m.d_model = c.d_model;
+    m.H = c.n_heads;
+    m.nope = c.head_dim_nope;
+    m.rope = c.head_dim_rope;
+    m.dv = c.head_dim_value;
+    m.q_rank = c.q_lora_rank;
+    m.kv_rank = c.kv_lora_rank;
+    m.d_ff = c.d_ff;
+    m.n_layers = c.n_layers;
+    m.qk = c.head_dim_nope + c.head_dim_rope;
+    m.eps = c.norm_epsilon;
+    m.theta = c.rope_theta;
+    m.page_size = page_size;
+    m.max_seq = c.max_sequence_length;
+    m.d_pad = round_up(c.d_model, 32);
+    m.q_pad = round_up(c.q_lora_rank, 32);
+    m.kvw_pad = round_up(c.kv_lora_rank + c.head_dim_rope, 16);
+    m.qk_pad = round_up(m.qk, 16);
+    m.nope_pad = round_up(c.head_dim_nope, 32);
+    m.kv_pad = round_up(c.kv_lora_rank, 16);
+    m.ctx_pad = round_up(c.n_heads * c.kv_lora_rank, 32);
+    m.ff_pad = round_up(c.d_ff, 32);
+    m.vocab_pad = round_up(c.vocab_size, 16);
+    return m;
+}
+
+}  // namespace
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" {
+
+int mla_config_validate(const mla_model_config* config) { return validate(config); }
+
+size_t mla_config_parameter_count(const mla_model_config* config) {
+    return config ? parameter_count(*config) : 0;
+}
+
+int mla_model_create(const mla_model_config* config, const float* params, int max_batch,
+                     int page_size, void** model_out) {
+    if (!model_out)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_create: null output");
+    *model_out = nullptr;
+    if (int st = validate(config))
+        return st;
+    if (!params || max_batch < 1 || max_batch > 65536 || page_size < 1)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_create: invalid argument");
+    const mla_model_config& c = *config;
+    const ModelDims m = make_dims(c, page_size);
+    // Shapes the step kernels cover: the kv row of [w_dq | w_dkv] within one wave's
+    // registers (<= 256 columns), a head's q within one workgroup (<= 4 tiles) and its
+    // absorption within 4 waves x 2 tiles, rows of at most 1024 (norm prologues) and
+    // 256 k-steps per split-K wave group, attention rows a multiple of 8 floats.
+    if (c.kv_lora_rank + c.head_dim_rope > 256 || m.qk_pad / 16 > 4 || m.kv_pad / 16 > 8 ||
+        (c.n_heads * c.kv_lora_rank) % 8 || m.d_pad > 1024 || m.q_pad > 256 ||
+        m.nope_pad > 128 || m.ctx_pad / 32 > 64 || m.ff_pad / 32 > 64)
+        return fail(MLA_ERR_UNSUPPORTED,
+                    "mla_model_create: shape outside the step kernels (kv_lora_rank + "
+                    "head_dim_rope <= 256, head_dim_nope + head_dim_rope <= 64, kv_lora_rank "
+                    "<= 128, head_dim_nope <= 128, q_lora_rank <= 256, d_model <= 1024, "
+                    "n_heads*kv_lora_rank <= 2048 and a multiple of 8, d_ff <= 2048)");
+    auto* M = new (std::nothrow) Model();
+    if (!M)
+        return fail(MLA_ERR_OUT_OF_MEMORY, "mla_model_create: host allocation");
+    M->cfg = c;
+    M->dims = m;
+    M->max_batch = max_batch;
+    M->m_pad_max = round_up(max_batch, 64);
+    M->parts = g7_parts(m);
+    const Registry R = view(c, params);
+    const int d = c.d_model, q = c.q_lora_rank, H = c.n_heads, nope = c.head_dim_nope;
+    const int qk = m.qk, kv = c.kv_lora_rank, kvw = kv + c.head_dim_rope, dv = c.head_dim_value;
+    const int ff = c.d_ff;
+    hipError_t e = model_kernel_attributes();
+    auto bail = [&](hipError_t err) {
+        delete M;
+        return gpu_status(err, "mla_model_create");
+    };
+    if (e != hipSuccess)
+        return bail(e);
+    // Tied embedding as the logits weight: K = d_model, N = vocab.
+    e = M->upload(M->embed, pack(d, c.vocab_size, m.d_pad, m.vocab_pad,
+                                 [&](int k, int col) { return R.embed[(size_t)col * d + k]; }));
+    if (e == hipSuccess)
+        e = M->upload(M->final_norm, std::vector<float>(R.final_norm, R.final_norm + d));
+    if (e == hipSuccess) {  // RoPE angles exactly as ops.cpp:88-108 forms them, per position
+        const int half = c.head_dim_rope / 2;
+        std::vector<float> tab((size_t)c.max_sequence_length * half * 2);
+        for (int pos = 0; pos < c.max_sequence_length; ++pos)
+            for (int j = 0; j < c.head_dim_rope; j += 2) {
+                const float angle =
+                    (float)pos * powf(c.rope_theta, -(float)j / (float)c.head_dim_rope);
+                tab[((size_t)pos * half + j / 2) * 2] = cosf(angle);
+                tab[((size_t)pos * half + j / 2) * 2 + 1] = sinf(angle);
+            }
+        e = M->upload(M->rope_tab, tab);
+    }
+    std::vector<float> proj((size_t)H * kv * d);
+    for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
+        const float* const* P = R.layer.data() + (size_t)l * P_COUNT;
+        LayerWeights w{};
+        e = M->upload(w.attn_norm, std::vector<float>(P[P_ATTN_NORM], P[P_ATTN_NORM] + d));
+        if (e == hipSuccess)
+            e = M->upload(w.q_norm, std::vector<float>(P[P_Q_NORM], P[P_Q_NORM] + q));
+        if (e == hipSuccess)
+            e = M->upload(w.kv_norm, std::vector<float>(P[P_KV_NORM], P[P_KV_NORM] + kv));
+        if (e == hipSuccess)
+            e = M->upload(w.ffn_norm, std::vector<float>(P[P_FFN_NORM], P[P_FFN_NORM] + d));
+        if (e == hipSuccess)  // [w_dq | w_dkv]: q columns padded to q_pad, then the kv columns
+            e = M->upload(w.w_dq_dkv,
+                          pack(d, m.q_pad + kvw, m.d_pad, m.q_pad + m.kvw_pad, [&](int k, int col) {
+                              if (col < q)
+                                  return P[P_W_DQ][(size_t)k * q + col];
+                              if (col < m.q_pad)
+                                  return 0.0f;
+                              return P[P_W_DKV][(size_t)k * kvw + (col - m.q_pad)];
+                          }));
+        if (e == hipSuccess)  // w_uq: head h at columns h*qk_pad ..
+            e = M->upload(w.w_uq, pack(q, H * m.qk_pad, m.q_pad, H * m.qk_pad, [&](int k, int col) {
+                              const int h = col / m.qk_pad, cc = col % m.qk_pad;
+                              return cc < qk ? P[P_W_UQ][(size_t)k * H * qk + h * qk + cc] : 0.0f;
+                          }));
+        if (e == hipSuccess) {  // W_uk_h^T per head: (k = nope index, col = latent index)
+            std::vector<uint16_t> all;
+            for (int h = 0; h < H; ++h) {
+                auto blk = pack(nope, kv, m.nope_pad, m.kv_pad, [&](int k, int col) {
+                    return P[P_W_UK][(size_t)col * H * nope + h * nope + k];
+                });
+                all.insert(all.end(), blk.begin(), blk.end());
+            }
+            e = M->upload(w.w_uk, all);
+        }
+        if (e == hipSuccess) {  // combined W_uv.W_o (CpuDecoder::prepare_projections, inference.cpp:28-46)
+            for (int h = 0; h < H; ++h)
+                for (int r = 0; r < kv; ++r) {
+                    float* row = proj.data() + ((size_t)h * kv + r) * d;
+                    std::memset(row, 0, (size_t)d * sizeof(float));
+                    for (int t = 0; t < dv; ++t) {
+                        const float a = P[P_W_UV][(size_t)r * H * dv + h * dv + t];
+                        const float* b = P[P_W_O] + (size_t)(h * dv + t) * d;
+                        for (int j = 0; j < d; ++j)
+                            row[j] += a * b[j];
+                    }
+                }
+            e = M->upload(w.w_out, pack(H * kv, d, m.ctx_pad, m.d_pad, [&](int k, int col) {
+                              return proj[(size_t)k * d + col];
+                          }));
+        }
+        if (e == hipSuccess)  // gate/up tiles interleaved: tile 2j gate, 2j+1 up, columns 16j..
+            e = M->upload(w.w_gate_up, pack(d, 2 * m.ff_pad, m.d_pad, 2 * m.ff_pad, [&](int k, int col) {
+                              const int t = col / 16, fcol = (t / 2) * 16 + col % 16;
+                              if (fcol >= ff)
+                                  return 0.0f;
+                              return (t % 2 ? P[P_W_UP] : P[P_W_GATE])[(size_t)k * ff + fcol];
+                          }));
+        if (e == hipSuccess)
+            e = M->upload(w.w_down, pack(ff, d, m.ff_pad, m.d_pad, [&](int k, int col) {
+                              return P[P_W_DOWN][(size_t)k * d + col];
+                          }));
+        M->layers.push_back(w);
+    }
+    const size_t rows = M->m_pad_max;
+    if (e == hipSuccess) e = M->alloc(M->x, rows * m.d_pad);
+    if (e == hipSuccess) e = M->alloc(M->res, rows * m.d_pad);
+    if (e == hipSuccess) e = M->alloc(M->cq, rows * m.q_pad);
+    if (e == hipSuccess) e = M->alloc(M->ctx, rows * (size_t)H * kv);
+    if (e == hipSuccess) e = M->alloc(M->kvraw, rows * m.kvw_pad);
+    if (e == hipSuccess) e = M->alloc(M->u, rows * m.ff_pad);
+    if (e == hipSuccess) e = M->alloc(M->q_latent, (size_t)max_batch * H * kv);
+    if (e == hipSuccess) e = M->alloc(M->q_rope, (size_t)max_batch * H * c.head_dim_rope);
+    if (e == hipSuccess) e = M->alloc(M->logits, (size_t)max_batch * c.vocab_size);
+    if (e == hipSuccess) e = M->alloc(M->arg_v, (size_t)max_batch * M->parts);
+    if (e == hipSuccess) e = M->alloc(M->arg_c, (size_t)max_batch * M->parts);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess)
+        return bail(e);
+    *model_out = M;
+    return MLA_OK;
+}
+
+int mla_model_destroy(void* model) {
+    delete static_cast<Model*>(model);
+    return MLA_OK;
+}
+
+int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
+                   const int32_t* positions, const int32_t* cu_seqlens_q,
+                   const int32_t* page_table, int max_pages, int num_pool_pages,
+                   const int32_t* slot_mapping, const int32_t* num_splits,
+                   const int32_t* cu_splits, const int32_t* work_desc, const int32_t* work_pages,
+                   const int32_t* info, int max_work, void* const* pages, void* workspace,
+                   size_t workspace_bytes, float* logits, int32_t* next_tokens) {
+    auto* M = static_cast<Model*>(model);
+    if (!M || B < 0 || B > (M ? M->max_batch : 0) || max_work < 0 || max_work > kMaxWork ||
+        max_pages < 0 || num_pool_pages < 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_step: invalid argument");
+    if (B == 0)
+        return MLA_OK;
+    if (!tokens || !positions || !cu_seqlens_q || !page_table || !slot_mapping || !num_splits ||
+        !cu_splits || !work_desc || !work_pages || !info || !pages || !next_tokens)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_step: null buffer");
+    for (int l = 0; l < M->cfg.n_layers; ++l)
+        if (!pages[l])
+            return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_step: null page pool");
+    const ModelDims& m = M->dims;
+    const size_t need = mla_decode_workspace_bytes(max_work, B, m.H, m.kv_rank);
+    if (!workspace || workspace_bytes < need)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "mla_model_step: workspace needs " + std::to_string(need) + " bytes");
+    const auto st = static_cast<hipStream_t>(stream);
+    StepArgs s{};
+    s.dims = m;
+    s.B = B;
+    s.m_pad = round_up(B, 64);
+    s.tokens = tokens;
+    s.positions = positions;
+    s.slot_mapping = slot_mapping;
+    s.num_pool_pages = num_pool_pages;
+    s.embed = M->embed;
+    s.final_norm = M->final_norm;
+    s.rope_tab = reinterpret_cast<const float2*>(M->rope_tab);
+    s.x = M->x;
+    s.res = M->res;
+    s.cq = M->cq;
+    s.ctx = M->ctx;
+    s.kvraw = M->kvraw;
+    s.u = M->u;
+    s.q_latent = M->q_latent;
+    s.q_rope = M->q_rope;
+    s.logits = logits ? logits : M->logits;
+    s.arg_v = M->arg_v;
+    s.arg_c = M->arg_c;
+    s.next_tokens = next_tokens;
+    DecodeArgs a{};
+    a.B = B;
+    a.H = m.H;
+    a.kv_rank = m.kv_rank;
+    a.rope_dim = m.rope;
+    a.page_size = m.page_size;
+    a.max_pages = max_pages;
+    a.num_pool_pages = num_pool_pages;
+    a.max_work = max_work;
+    a.scale_log2 = 1.4426950408889634f / std::sqrt((float)m.qk);  // inference.cpp:133
+    a.cu_q = cu_seqlens_q;
+    a.page_table = page_table;
+    a.num_splits = num_splits;
+    a.cu_splits = cu_splits;
+    a.work_desc = work_desc;
+    a.work_pages = work_pages;
+    a.info = info;
+    a.q_latent = M->q_latent;
+    a.q_rope = M->q_rope;
+    a.out = M->ctx;
+    a.lse = nullptr;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = a.part_o + (size_t)max_work * m.H * m.kv_rank;
+    const bool generic = (reinterpret_cast<uintptr_t>(workspace) & 15) != 0;
+    hipError_t e = launch_embed(s, st);
+    for (int l = 0; l < m.n_layers && e == hipSuccess; ++l) {
+        uint16_t* pool = static_cast<uint16_t*>(pages[l]);
+        e = launch_layer_pre(s, M->layers[l], pool, st);
+        if (e != hipSuccess)
+            break;
+        a.pages = pool;
+        e = launch_decode_partials(a, MLA_DTYPE_F16, generic, st);
+        if (e == hipSuccess)
+            e = launch_merge(a, st);
+        if (e == hipSuccess)
+            e = launch_layer_post(s, M->layers[l], st);
+    }
+    if (e == hipSuccess)
+        e = launch_logits(s, st);
+    return gpu_status(e, "mla_model_step");
+}
+
+const float* mla_model_logits(void* model) {
+    return model ? static_cast<Model*>(model)->logits : nullptr;
+}
+
+}  // extern "C"

@@ -114,3 +114,40 @@ def ragged_decode_batch(B=64, min_len=128, max_len=4096, page_size=64, n_heads=8
                        max_pages=int(counts.max()), pages=pages, q_latent=q_latent,
                        q_rope=q_rope, page_size=page_size, kv_rank=kv_rank, rope_dim=rope_dim,
                        n_heads=n_heads, dtype=dtype)
+
+
+# mla36m-v1 (config/mla36m-v1.json of the reference), max_sequence_length raised so a
+# session can hold config 3's 4096-token contexts (legal up to 65535, config.cpp:21-34).
+MLA36M = dict(vocab_size=16384, max_sequence_length=4608, n_layers=10, d_model=512, n_heads=8,
+              head_dim_nope=48, head_dim_rope=16, head_dim_value=64, q_lora_rank=192,
+              kv_lora_rank=128, d_ff=1360, norm_epsilon=1e-5, rope_theta=10000.0)
+
+
+def parameter_shapes(cfg: dict):
+    """(rows, cols) of every tensor in the reference registry order
+    (include/mini_mla/model.hpp:15-30, src/model/model.cpp:40-63)."""
+    d, q, kv, H = cfg["d_model"], cfg["q_lora_rank"], cfg["kv_lora_rank"], cfg["n_heads"]
+    nope, rope, dv, ff = (cfg["head_dim_nope"], cfg["head_dim_rope"], cfg["head_dim_value"],
+                          cfg["d_ff"])
+    shapes = [(cfg["vocab_size"], d), (1, d)]
+    for _ in range(cfg["n_layers"]):
+        shapes += [(1, d), (d, q), (1, q), (q, H * (nope + rope)), (d, kv + rope), (1, kv),
+                   (kv, H * nope), (kv, H * dv), (H * dv, d), (1, d), (d, ff), (d, ff), (ff, d)]
+    return shapes
+
+
+def model_params(cfg: dict, seed: int = 0) -> np.ndarray:
+    """Random-init parameters with Model::create's scales (src/model/model.cpp:20-75):
+    N(0, 0.02), the residual projections w_o and w_down scaled by 1/sqrt(2L), norms 1.
+    Drawn from numpy's generator (the reference draws them from its own Rng), in fp32."""
+    gen = np.random.default_rng(seed)
+    out = []
+    resid = 0.02 / np.sqrt(2 * cfg["n_layers"])
+    for i, (r, c) in enumerate(parameter_shapes(cfg)):
+        slot = -1 if i < 2 else (i - 2) % 13
+        if i == 1 or slot in (0, 2, 5, 9):  # final_norm, attn/q/kv/ffn norms
+            out.append(np.ones(r * c, np.float32))
+        else:
+            scale = resid if slot in (8, 12) else 0.02
+            out.append((gen.standard_normal(r * c, dtype=np.float32) * scale).astype(np.float32))
+    return np.concatenate(out)

@@ -179,6 +179,63 @@ int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_
                      int max_work, float* out, float* lse, const void* workspace,
                      size_t workspace_bytes);
 
+/* ------------------------------------------------------------------ model
+ * The batched decode step around the attention: everything of
+ * CpuDecoder::decode (src/infer/inference.cpp:76-173) for B sessions at once,
+ * one new token each, on fp16 weights with fp32 accumulation.  The drop-in
+ * counterpart of MpsExecution::decode / GraphBuilder::decode
+ * (src/backends/mps_backend.mm:496-583,940-977), batched. */
+
+/* The fields of mini_mla::ModelConfig (include/mini_mla/model_config.hpp:5-19). */
+typedef struct {
+    int vocab_size, max_sequence_length, n_layers, d_model, n_heads;
+    int head_dim_nope, head_dim_rope, head_dim_value;
+    int q_lora_rank, kv_lora_rank, d_ff;
+    float norm_epsilon, rope_theta;
+} mla_model_config;
+
+/* ModelConfig::validate (src/model/config.cpp:20-48): MLA_OK or
+ * MLA_ERR_INVALID_ARGUMENT with the reference's message. */
+int mla_config_validate(const mla_model_config* config);
+/* ModelConfig::parameter_count (src/model/config.cpp:7-19). */
+size_t mla_config_parameter_count(const mla_model_config* config);
+
+/* Uploads a model: `params` (host fp32) holds every parameter in the reference
+ * registry order (include/mini_mla/model.hpp:15-30, src/model/model.cpp:40-63:
+ * token_embedding, final_norm, then per layer attn_norm, w_dq, q_norm, w_uq,
+ * w_dkv, kv_norm, w_uk, w_uv, w_o, ffn_norm, w_gate, w_up, w_down; row-major
+ * [in x out]).  Weights are rounded to fp16 on the device (the MPS backend's
+ * fp16 storage, mps_backend.mm:623-635); W_uv.W_o is combined per head first,
+ * in fp32 (CpuDecoder::prepare_projections, inference.cpp:28-46).  The model
+ * owns device activations for up to max_batch rows; page_size is the cache's.
+ * The handle is used from one thread / stream at a time. */
+int mla_model_create(const mla_model_config* config, const float* params, int max_batch,
+                     int page_size, void** model);
+int mla_model_destroy(void* model);
+
+/* One decode step for B sessions (B <= max_batch): tokens[b] (device int32, in
+ * [0, vocab)) at position positions[b] (device int32: the tokens already cached,
+ * in [0, max_sequence_length); the caller rejects others, as inference.cpp:71-75
+ * does, and the kernels clamp them so no access leaves its buffer).
+ * The metadata arguments come from one mla_build_metadata call with q_len = 1
+ * and ctx_len = positions; pages is a HOST array of n_layers device page pools
+ * (fp16, the mla_append_latent format); the step appends each token's latent
+ * and key to them before attending (inference.cpp:100-103).  workspace is a
+ * decode workspace (mla_decode_workspace_bytes).  Outputs: logits [B x vocab]
+ * fp32 (device; NULL = the model's own buffer, see mla_model_logits) and
+ * next_tokens[B] (device int32): the greedy token of sample_token with
+ * temperature 0 and no penalty (inference.cpp:345-380: lowest index among the
+ * maxima), or -1 when a logit is not finite (numerical_error). */
+int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
+                   const int32_t* positions, const int32_t* cu_seqlens_q,
+                   const int32_t* page_table, int max_pages, int num_pool_pages,
+                   const int32_t* slot_mapping, const int32_t* num_splits,
+                   const int32_t* cu_splits, const int32_t* work_desc, const int32_t* work_pages,
+                   const int32_t* info, int max_work, void* const* pages, void* workspace,
+                   size_t workspace_bytes, float* logits, int32_t* next_tokens);
+/* The model's own logits buffer [max_batch x vocab] (device). */
+const float* mla_model_logits(void* model);
+
 #ifdef __cplusplus
 }
 #endif

@@ -190,10 +190,11 @@ class Decoder:
     """CpuDecoder (src/infer/inference.cpp:10-174) with a contiguous fp32 cache."""
 
     def __init__(self, cfg: Config, params: np.ndarray, absorbed: bool = True,
-                 round_cache: bool = False):
+                 round_cache: bool = False, proj: np.ndarray | None = None):
         self.cfg, self.params = cfg, params
         self.absorbed, self.round_cache = absorbed, round_cache
-        self.proj = output_projection(cfg, params)
+        # prepare_projections' result may be shared between decoders of one model
+        self.proj = output_projection(cfg, params) if proj is None else proj
         S = cfg.max_sequence_length
         self.latent = np.zeros((cfg.n_layers, S, cfg.kv_lora_rank), np.float32)
         self.rope = np.zeros((cfg.n_layers, S, cfg.head_dim_rope), np.float32)

@@ -1,0 +1,172 @@
+"""The batched decode step (mla_model_*) against the oracle's CpuDecoder restatement.
+
+CPU: ModelConfig validation and parameter counts (src/model/config.cpp:7-48,
+tests/test_model.cpp:21-28 known answers).
+
+GPU: one step for B sessions with random fp16 caches of different lengths, compared
+with oracle.Decoder (absorbed, fp16-rounded cache, inference.cpp:69-174) run per
+session on the same fp16-rounded weights and cache rows.  The GPU rounds the
+activations feeding every projection to fp16 (as the reference's fp16 MPS path does)
+and keeps q_latent in the cache dtype (mps_backend.mm:561), so logits agree to
+LOGIT_ATOL; the reference records 3.5e-3 to 3.9e-3 max-abs logit error for its own
+fp16 GPU decode against its CPU path (docs/benchmarks/throughput-followup/
+inference.json).  Appended cache rows agree to CACHE_ATOL + CACHE_RTOL*|x|; greedy
+tokens are equal wherever the oracle's top-2 margin exceeds twice LOGIT_ATOL.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import MLA36M, TINY
+
+LOGIT_ATOL = 5e-3
+CACHE_ATOL, CACHE_RTOL = 2e-2, 1e-2
+
+
+def _cfg(d, **over):
+    import cpp_inference_train_engine_amd as mla
+    d = dict(d, **over)
+    return mla.ModelConfig.from_dict(d)
+
+
+# ------------------------------------------------------------------ CPU ----
+def test_parameter_counts_match_reference_known_answers():
+    import cpp_inference_train_engine_amd as mla
+    assert mla.config_parameter_count(_cfg(MLA36M)) == 35_763_840
+    assert mla.config_parameter_count(_cfg(TINY)) == 26_704
+    mla.config_validate(_cfg(MLA36M))
+    mla.config_validate(_cfg(TINY))
+
+
+@pytest.mark.parametrize("over, words", [
+    (dict(head_dim_rope=3), "odd RoPE"),
+    (dict(d_model=30), "divisibility"),
+    (dict(n_heads=0), "n_heads must be in [1, 65535]"),
+    (dict(vocab_size=70000), "vocab_size must be in [1, 65535]"),
+    (dict(n_layers=129), "layer"),
+    (dict(norm_epsilon=0.0), "epsilon"),
+    (dict(rope_theta=1.0), "theta"),
+    (dict(d_model=65535, n_heads=1, d_ff=65535, n_layers=100), "one billion"),
+])
+def test_invalid_configs_are_rejected_like_the_reference(over, words):
+    import cpp_inference_train_engine_amd as mla
+    with pytest.raises(mla.MlaError) as e:
+        mla.config_validate(_cfg(MLA36M, **over))
+    assert e.value.code == "invalid_argument" and words in str(e.value)
+
+
+def test_config_from_reference_json_keys():
+    import json
+    import cpp_inference_train_engine_amd as mla
+    d = dict(MLA36M, model_type="mla_dense_decoder", version=1, norm="rmsnorm")
+    c = mla.ModelConfig.from_dict(json.loads(json.dumps(d)))
+    assert c.to_dict()["kv_lora_rank"] == 128 and c.qk_dim == 64
+    with pytest.raises(ValueError):
+        mla.ModelConfig.from_dict({k: v for k, v in MLA36M.items() if k != "d_ff"})
+
+
+# ------------------------------------------------------------------ GPU ----
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _dev(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def _step_case(cfgd, B, max_ctx, seed, page_size=64):
+    """Random model (reference init, seed), B sessions with ctx lengths in [1, max_ctx] and
+    N(0,1) fp16 caches; returns GPU and oracle results."""
+    import torch
+    import oracle
+    import cpp_inference_train_engine_amd as mla
+    from cpp_inference_train_engine_amd.ops import latent_word, rope_word
+    ocfg = oracle.Config.from_dict(cfgd)
+    params = oracle.bits_to_f32(oracle.round_f16(oracle.model_init(ocfg, seed)))
+    L, kv, rp, V = ocfg.n_layers, ocfg.kv_lora_rank, ocfg.head_dim_rope, ocfg.vocab_size
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(1, max_ctx + 1, size=B).astype(np.int32)
+    tokens = rng.integers(0, V, size=B).astype(np.int32)
+    # page lists with room for the appended token, physical ids permuted
+    need = (ctx + 1 + page_size - 1) // page_size
+    P = int(need.sum())
+    perm = rng.permutation(P).astype(np.int32)
+    cu_pages = np.concatenate([[0], np.cumsum(need)]).astype(np.int32)
+    rec = page_size * (kv + rp)
+    pages = np.zeros((L, P, rec), np.uint16)
+    lat = [oracle.round_f16(rng.standard_normal((L, c, kv), dtype=np.float32)) for c in ctx]
+    rop = [oracle.round_f16(rng.standard_normal((L, c, rp), dtype=np.float32)) for c in ctx]
+    for b in range(B):
+        t = np.arange(ctx[b])
+        pg = perm[cu_pages[b] + t // page_size]
+        slot = t % page_size
+        r = np.arange(kv)
+        c = np.arange(rp)
+        lw = latent_word(slot[:, None], r[None, :], page_size, kv, rp)
+        rw = rope_word(slot[:, None], c[None, :], page_size, kv, rp)
+        for l in range(L):
+            pages[l, pg[:, None], lw] = lat[b][l]
+            pages[l, pg[:, None], rw] = rop[b][l]
+    model = mla.HipModel(mla.ModelConfig.from_dict(cfgd), params, max_batch=B,
+                         page_size=page_size)
+    rb = mla.build_metadata(_dev(ctx), _dev(np.ones(B, np.int32)), _dev(cu_pages), _dev(perm),
+                            page_size, int(need.max()), P, split_pages=4)
+    gpu_pages = [_dev(pages[l].view(np.int16)).view(torch.float16) for l in range(L)]
+    ws = mla.decode_workspace(rb.max_work, B, ocfg.n_heads, kv)
+    logits, nxt = model.step(rb, _dev(tokens), _dev(ctx), gpu_pages, ws)
+    torch.cuda.synchronize()
+    rb.read_info()
+    got_pages = np.stack([p.view(torch.int16).cpu().numpy().view(np.uint16) for p in gpu_pages])
+    model.close()
+    want_logits, want_lat, want_rope, got_lat, got_rope = [], [], [], [], []
+    for b in range(B):
+        dec = oracle.Decoder(ocfg, params, absorbed=True, round_cache=True)
+        dec.latent[:, :ctx[b]] = oracle.bits_to_f32(lat[b])
+        dec.rope[:, :ctx[b]] = oracle.bits_to_f32(rop[b])
+        dec.position = int(ctx[b])
+        want_logits.append(dec.decode(int(tokens[b])))
+        want_lat.append(dec.latent[:, ctx[b]].copy())
+        want_rope.append(dec.rope[:, ctx[b]].copy())
+        pg = perm[cu_pages[b] + ctx[b] // page_size]
+        slot = ctx[b] % page_size
+        got_lat.append(oracle.bits_to_f32(
+            got_pages[:, pg, latent_word(slot, np.arange(kv), page_size, kv, rp)]))
+        got_rope.append(oracle.bits_to_f32(
+            got_pages[:, pg, rope_word(slot, np.arange(rp), page_size, kv, rp)]))
+    return dict(logits=logits.cpu().numpy(), next=nxt.cpu().numpy(),
+                want_logits=np.stack(want_logits), lat=np.stack(got_lat),
+                want_lat=np.stack(want_lat), rope=np.stack(got_rope),
+                want_rope=np.stack(want_rope))
+
+
+def _check_step(r, what):
+    err = np.abs(r["logits"] - r["want_logits"]).max()
+    lat_exc = (np.abs(r["lat"] - r["want_lat"]) - (CACHE_ATOL + CACHE_RTOL * np.abs(r["want_lat"]))).max()
+    rope_exc = (np.abs(r["rope"] - r["want_rope"]) - (CACHE_ATOL + CACHE_RTOL * np.abs(r["want_rope"]))).max()
+    _say(f"{what}: max |logit err| {err:.3e}, latent excess {lat_exc:.3e}, rope excess {rope_exc:.3e}")
+    assert err <= LOGIT_ATOL, f"{what}: logits max abs error {err}"
+    assert lat_exc <= 0 and rope_exc <= 0, f"{what}: appended cache rows"
+    want = r["want_logits"]
+    top2 = np.sort(want, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 2 * LOGIT_ATOL
+    ref_tok = np.argmax(want, axis=1)  # numpy argmax: lowest index among the maxima
+    assert (r["next"][clear] == ref_tok[clear]).all(), f"{what}: greedy tokens"
+    assert (r["next"] >= 0).all()
+
+
+@pytest.mark.gpu
+def test_model_step_tiny_matches_oracle(gpu, orc):
+    """tiny-test config (H=2, kv_rank=8, rope=4): generic attention path, padded tiles."""
+    r = _step_case(dict(TINY, max_sequence_length=512), B=5, max_ctx=300, seed=3, page_size=16)
+    _check_step(r, "tiny")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B, max_ctx, seed", [(16, 700, 0), (70, 300, 1)])
+def test_model_step_mla36m_matches_oracle(gpu, orc, B, max_ctx, seed):
+    """mla36m (config 2/3 model): MFMA attention path; B=70 spans two 64-row chunks."""
+    r = _step_case(dict(MLA36M, max_sequence_length=1024), B=B, max_ctx=max_ctx, seed=seed)
+    _check_step(r, f"mla36m B={B}")
