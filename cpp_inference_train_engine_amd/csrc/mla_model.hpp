@@ -63,12 +63,16 @@ struct StepArgs {
     float* arg_v;               // [B x parts] greedy partials
     int32_t* arg_c;
     int32_t* next_tokens;       // [B]
+    // Per-row sums of squares of each 16-column tile of an activation, written by its
+    // producer and summed (in tile order) into 1/rms by the RMSNorm-ing consumer.
+    float* ss_x;    // [m_pad x d_pad/16] of x (embed, g6) -> attn_norm (g1), final_norm (g7)
+    float* ss_res;  // [m_pad x d_pad/16] of res (g4) -> ffn_norm (g5)
+    float* ss_q;    // [m_pad x q_pad/16] of cq (g1) -> q_norm (g23)
+    float* ss_kv;   // [m_pad x kv_pad/16] of the latent columns of kvraw (g1) -> kv_norm
 };
 
 int g7_parts(const ModelDims& m);
-size_t g1_lds_bytes(const ModelDims& m);
 size_t g23_lds_bytes(const ModelDims& m);
-size_t dpad_lds_bytes(const ModelDims& m);
 hipError_t model_kernel_attributes();
 hipError_t launch_embed(const StepArgs& s, hipStream_t st);
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,

@@ -3,13 +3,13 @@
 // each.
 //
 // Per layer, in launch order (y = x.W for every projection, as in ops.cpp:8-18):
-//   g1_kernel   RMSNorm(x, attn_norm) -> [w_dq | w_dkv]; the q part is stored for g23,
-//               the kv part is kv_norm-ed (latent) / RoPE-d (key), rounded to the cache
-//               dtype and appended to the paged cache (inference.cpp:84-103)
+//   g1_kernel   RMSNorm(x, attn_norm) . [w_dq | w_dkv] -> q part (cq) and kv part (kvraw)
 //   g23_kernel  per head: q_norm -> w_uq -> RoPE of the rope columns (q_rope, stored in
 //               the cache dtype) -> absorption q_latent = W_uk_h^T q_nope
 //               (inference.cpp:85-90,121-124; the MPS graph keeps q_latent in the
-//               storage dtype, mps_backend.mm:561)
+//               storage dtype, mps_backend.mm:561); four more workgroups kv_norm the
+//               latent, RoPE the key, round both and append them to the paged cache
+//               (inference.cpp:91-103)
 //   (decode attention partials + merge: decode.hip)
 //   g4_kernel   latent_ctx [H*kv_rank] . out_proj + x  (inference.cpp:154-156; out_proj
 //               is the combined W_uv.W_o of prepare_projections, inference.cpp:28-46)
@@ -20,9 +20,16 @@
 // argmax_kernel (sample_token's greedy rule, inference.cpp:345-380).
 //
 // Every projection is a skinny GEMM (M = the batch rows, 64 per chunk) on
-// v_mfma_f32_16x16x32_f16: activations are rounded to fp16 as A operands, weights are
-// fp16 in the TILED layout below (each wave's B-operand load reads 1 KB contiguously),
-// accumulation is fp32, norms / RoPE / SwiGLU / residuals run in fp32.
+// v_mfma_f32_16x16x32_f16, fp16 operands, fp32 accumulation.  A workgroup owns one or
+// two 16-column output tiles and its 8 waves split K; each wave fetches its weight
+// tiles (fp16, TILED: each wave load reads 1 KB contiguously) and its slice of the
+// activation rows into registers at kernel start, so a GEMM pays about one memory
+// round trip, and the partial sums meet in LDS.
+//
+// RMSNorm (ops.cpp:33-45) never re-reads a row: the kernel that writes a normalised
+// activation also writes, per row and 16-column tile, the sum of squares of its
+// columns; the consumer adds those partials (in a fixed order) into 1/rms per row
+// and scales its A operands by it and by the norm weight while rounding them to fp16.
 #include "mla_common.hpp"
 #include "mla_internal.hpp"
 #include "mla_model.hpp"
@@ -33,98 +40,25 @@ namespace mla {
 namespace {
 
 using V8 = half8;
+constexpr int kWaves = 8;  // split-K waves per GEMM workgroup
+constexpr int kLdsPad = 8;
 
 __device__ __forceinline__ floatx4 mma(V8 a, V8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// ---- A operands: lane (g, n) supplies A[16mt + n][32kt + 8g .. +7] ----------------
-struct ALds16 {  // fp16 rows in LDS
-    const _Float16* p;
-    int ld;
-    __device__ V8 operator()(int m, int k) const { return *reinterpret_cast<const V8*>(p + m * ld + k); }
-};
-struct AGlb16 {  // fp16 rows in global memory
-    const uint16_t* p;
-    int ld;
-    __device__ V8 operator()(int m, int k) const {
-        return *reinterpret_cast<const V8*>(p + (long long)m * ld + k);
-    }
-};
-struct AGlb32 {  // fp32 rows in global memory (K columns, K % 8 == 0), rounded to fp16
-    const float* p;
-    int ld, K;
-    __device__ V8 operator()(int m, int k) const {
-        if (k >= K)
-            return V8{};
-        const floatx4* q = reinterpret_cast<const floatx4*>(p + (long long)m * ld + k);
-        const floatx4 a = q[0], b = q[1];
-        return V8{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
-                  (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
-    }
-};
+__device__ __forceinline__ V8 to_half8(floatx4 a, floatx4 b) {
+    return V8{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
+              (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
+}
 
-// Weight (B operand) registers of one wave: k-steps [kt0, kt0+KW) of tiles
-// [nt0, nt0+NT), fetched at kernel start, before the activations are ready, so every
-// GEMM pays one weight round trip.  W is tiled (see mla_model.hpp): tile (nt, kt) is
-// 512 contiguous fp16 words; tiles past `ntv` or k-steps past KT stay zero.
-template <int NT, int KW>
-struct BPre {
-    V8 b[KW][NT];
-    __device__ __forceinline__ void load(const uint16_t* w, int nt0, int ntv, int KT, int kt0,
-                                         int lane) {
+// Sum over the 16 lanes of an MFMA output row group (lanes with equal g hold the same
+// rows, one column each).
+__device__ __forceinline__ float sum16(float v) {
 #pragma unroll
-        for (int kk = 0; kk < KW; ++kk)
-#pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                b[kk][j] = V8{};
-                if (kt0 + kk < KT && j < ntv)
-                    b[kk][j] = *reinterpret_cast<const V8*>(
-                        w + ((long long)(nt0 + j) * KT + kt0 + kk) * 512 + lane * 8);
-            }
-    }
-    // acc[mt][j] += A[16mt.., 32kt..] . W[32kt.., 16(nt0+j)..] over the fetched k-steps.
-    template <typename A>
-    __device__ __forceinline__ void mma_all(floatx4 (&acc)[4][NT], const A& a, int KT, int kt0,
-                                            int lane) const {
-        const int g = lane >> 4, n = lane & 15;
-#pragma unroll
-        for (int kk = 0; kk < KW; ++kk) {
-            if (kt0 + kk >= KT)
-                break;
-            V8 av[4];
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                av[mt] = a(16 * mt + n, 32 * (kt0 + kk) + 8 * g);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int j = 0; j < NT; ++j)
-                    acc[mt][j] = mma(av[mt], b[kk][j], acc[mt][j]);
-        }
-    }
-};
-
-// Split-K reduction over the W waves of a workgroup through LDS (`part` holds at least
-// W*4*NT*64 floatx4); then epi(mt, j, v) for every (M-tile, N-tile) pair, pairs dealt
-// round-robin to the waves.  v is lane (g, n)'s C[16mt + 4g + i][16(nt0+j) + n].
-template <int NT, int W, typename Epi>
-__device__ __forceinline__ void splitk_reduce(floatx4 (&acc)[4][NT], floatx4* part, Epi epi) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-            part[((wave * 4 + mt) * NT + j) * 64 + lane] = acc[mt][j];
-    __syncthreads();
-    for (int p = wave; p < 4 * NT; p += W) {
-        const int mt = p / NT, j = p % NT;
-        floatx4 v = {0, 0, 0, 0};
-#pragma unroll
-        for (int w = 0; w < W; ++w)
-            v += part[((w * 4 + mt) * NT + j) * 64 + lane];
-        epi(mt, j, v);
-    }
+    for (int off = 8; off > 0; off >>= 1)
+        v += __shfl_xor(v, off, 16);
+    return v;
 }
 
 template <int NT>
@@ -136,241 +70,421 @@ __device__ __forceinline__ void zero(floatx4 (&acc)[4][NT]) {
             acc[mt][j] = floatx4{0, 0, 0, 0};
 }
 
-// RMSNorm of 64 fp32 rows of width K (ops.cpp:33-45: inv = 1/sqrt(mean(x^2) + eps),
-// fp32 sums) times the norm weight, rounded to fp16 into LDS rows of pitch ld (the
-// padding columns [K, Kpad) are zero).  One wave per 16 rows, RB rows at a time with
-// every load of the batch in flight (lane l holds columns l, l+64, ...; CPL >= Kpad/64
-// columns per lane; RB*CPL <= 64 registers), so a prologue costs a few global round
-// trips, not two per row.
-template <int CPL, int RB = 64 / CPL < 8 ? 64 / CPL : 8>
-__device__ __forceinline__ void rmsnorm_rows_to_lds_t(const float* x, int ldx, int K, int Kpad, const float* wn,
-                                      float eps, _Float16* lds, int ld) {
-    constexpr int kRowBatch = RB;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float w[CPL];
+// ---- operand prefetch ----------------------------------------------------------
+// A wave's k-steps are kt0, kt0 + ks, kt0 + 2ks, ... (KW of them; kt0 = the wave's
+// index and ks = the waves splitting K, so uneven K spreads evenly); k-steps past KT
+// load zeros and add nothing.
+//
+// Weight (B operand) registers of one wave: its k-steps of tiles [nt0, nt0+NT); tiles
+// past `ntv` stay zero.  Tile (nt, kt) of a tiled W (mla_model.hpp) is 512 contiguous
+// fp16 words; lane l reads 16 bytes at 8l.
+template <int NT, int KW>
+struct BPre {
+    V8 b[KW][NT];
+    __device__ __forceinline__ void load(const uint16_t* w, int nt0, int ntv, int KT, int kt0,
+                                         int ks, int lane) {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c = lane + 64 * j;
-        w[j] = c < K ? wn[c] : 0.0f;
-    }
-#pragma unroll 1
-    for (int r0 = wave * 16; r0 < wave * 16 + 16; r0 += kRowBatch) {
-        float v[kRowBatch][CPL];
+        for (int kk = 0; kk < KW; ++kk)
 #pragma unroll
-        for (int rr = 0; rr < kRowBatch; ++rr)
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const int c = lane + 64 * j;
-                v[rr][j] = c < K ? x[(long long)(r0 + rr) * ldx + c] : 0.0f;
+            for (int j = 0; j < NT; ++j) {
+                const int kt = kt0 + kk * ks;
+                b[kk][j] = V8{};
+                if (kt < KT && j < ntv)
+                    b[kk][j] = *reinterpret_cast<const V8*>(
+                        w + ((long long)(nt0 + j) * KT + kt) * 512 + lane * 8);
             }
+    }
+};
+
+// Activation (A operand) registers: lane (g, n) needs rows 16mt + n (mt = 0..3) and
+// columns 32kt + 8g .. +7 of each of its k-steps.  Columns past K read as zero
+// (K % 8 == 0, so an 8-column chunk is wholly in or out).
+template <int KW>
+struct APre32 {  // fp32 rows
+    floatx4 x[KW][4][2];
+    __device__ __forceinline__ void load(const float* X, int ld, int K, int KT, int kt0, int ks,
+                                         int lane) {
+        const int g = lane >> 4, n = lane & 15;
 #pragma unroll
-        for (int rr = 0; rr < kRowBatch; ++rr) {
-            float ss = 0.0f;
+        for (int kk = 0; kk < KW; ++kk) {
+            const int kt = kt0 + kk * ks;
+            const int k = 32 * kt + 8 * g;
+            const bool ok = kt < KT && k < K;
 #pragma unroll
-            for (int j = 0; j < CPL; ++j)
-                ss += v[rr][j] * v[rr][j];
-            ss = wave_sum(ss);
-            const float inv = 1.0f / sqrtf(ss / (float)K + eps);
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const int c = lane + 64 * j;
-                if (c < Kpad)
-                    lds[(r0 + rr) * ld + c] = (_Float16)(v[rr][j] * inv * w[j]);
+            for (int mt = 0; mt < 4; ++mt) {
+                x[kk][mt][0] = x[kk][mt][1] = floatx4{0, 0, 0, 0};
+                if (ok) {
+                    const floatx4* p =
+                        reinterpret_cast<const floatx4*>(X + (long long)(16 * mt + n) * ld + k);
+                    x[kk][mt][0] = p[0];
+                    x[kk][mt][1] = p[1];
+                }
             }
         }
     }
+};
+template <int KW>
+struct ANorm32 : APre32<KW> {  // fp32 rows, RMSNorm-ed on the fly: x * inv[row] * w[col]
+    floatx4 w[KW][2];
+    __device__ __forceinline__ void load_w(const float* wn, int K, int KT, int kt0, int ks,
+                                           int lane) {
+        const int g = lane >> 4;
+#pragma unroll
+        for (int kk = 0; kk < KW; ++kk) {
+            const int kt = kt0 + kk * ks;
+            const int k = 32 * kt + 8 * g;
+            w[kk][0] = w[kk][1] = floatx4{0, 0, 0, 0};
+            if (kt < KT && k < K) {
+                w[kk][0] = *reinterpret_cast<const floatx4*>(wn + k);
+                w[kk][1] = *reinterpret_cast<const floatx4*>(wn + k + 4);
+            }
+        }
+    }
+};
+template <int KW>
+struct AHalf32 {  // fp32 rows rounded to fp16 operands as they arrive (half the registers)
+    V8 x[KW][4];
+    __device__ __forceinline__ void load(const float* X, int ld, int K, int KT, int kt0, int ks,
+                                         int lane) {
+        const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+        for (int kk = 0; kk < KW; ++kk) {
+            const int kt = kt0 + kk * ks;
+            const int k = 32 * kt + 8 * g;
+            const bool ok = kt < KT && k < K;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                x[kk][mt] = V8{};
+                if (ok) {
+                    const floatx4* p =
+                        reinterpret_cast<const floatx4*>(X + (long long)(16 * mt + n) * ld + k);
+                    x[kk][mt] = to_half8(p[0], p[1]);
+                }
+            }
+        }
+    }
+};
+template <int KW>
+struct APre16 {  // fp16 rows (the buffer is zero-padded to KT*32 columns)
+    V8 x[KW][4];
+    __device__ __forceinline__ void load(const uint16_t* X, int ld, int KT, int kt0, int ks,
+                                         int lane) {
+        const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+        for (int kk = 0; kk < KW; ++kk)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const int kt = kt0 + kk * ks;
+                x[kk][mt] = V8{};
+                if (kt < KT)
+                    x[kk][mt] = *reinterpret_cast<const V8*>(X + (long long)(16 * mt + n) * ld +
+                                                             32 * kt + 8 * g);
+            }
+    }
+};
+
+template <int NT, int KW, typename AOp>
+__device__ __forceinline__ void mma_steps(floatx4 (&acc)[4][NT], const BPre<NT, KW>& b, AOp aop) {
+#pragma unroll
+    for (int kk = 0; kk < KW; ++kk)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const V8 a = aop(kk, mt);
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                acc[mt][j] = mma(a, b.b[kk][j], acc[mt][j]);
+        }
 }
 
-__device__ __forceinline__ void rmsnorm_rows_to_lds(const float* x, int ldx, int K, int Kpad,
-                                                    const float* wn, float eps, _Float16* lds,
-                                                    int ld) {
-    if (Kpad <= 256)
-        rmsnorm_rows_to_lds_t<4>(x, ldx, K, Kpad, wn, eps, lds, ld);
-    else if (Kpad <= 512)
-        rmsnorm_rows_to_lds_t<8>(x, ldx, K, Kpad, wn, eps, lds, ld);
-    else
-        rmsnorm_rows_to_lds_t<16>(x, ldx, K, Kpad, wn, eps, lds, ld);
+// 1/rms of `rows` rows (ops.cpp:33-45: inv = 1/sqrt(mean(x^2) + eps)) from the
+// producer's per-tile partial sums of squares (n_tiles <= 64): four threads a row each
+// load every fourth tile at once (one round trip), then combine in a fixed order.
+// Threads [0, 4*rows) take part; rows is 16 or 64, so they fill whole waves.
+__device__ __forceinline__ void inv_rms_to_lds(const float* ss, int n_tiles, int K, float eps,
+                                               int row0, float* inv_s, int rows = 64) {
+    const int t = threadIdx.x;
+    if (t < 4 * rows) {
+        const float* p = ss + (long long)(row0 + (t >> 2)) * n_tiles;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int tile = (t & 3) + 4 * i;
+            v[i] = tile < n_tiles ? p[tile] : 0.0f;
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            sum += v[i];
+        sum += __shfl_xor(sum, 1, 4);
+        sum += __shfl_xor(sum, 2, 4);
+        if ((t & 3) == 0)
+            inv_s[t >> 2] = 1.0f / sqrtf(sum / (float)K + eps);
+    }
 }
 
-// Adjacent-pair RoPE (ops.cpp:88-108) of the value v in column col_in_span of the
-// rotated span, for a lane whose partner column is lane ^ 1 (the MFMA output layout
-// puts adjacent columns in adjacent lanes).  cos/sin of pos * theta^(-j/rope) come
-// from the model's table (computed on the host with the reference's float formula).
-// Positions past the table (the caller rejects them, as inference.cpp:71-75 does) are
-// clamped so the lookup stays in bounds.
-__device__ __forceinline__ float rope_lane(float v, int col_in_span, int rope, int pos,
-                                           int max_seq, const float2* tab) {
-    const float other = __shfl_xor(v, 1, 64);
-    pos = min(max(pos, 0), max_seq - 1);
-    const float2 cs = tab[(long long)pos * (rope / 2) + (col_in_span >> 1)];
-    return (col_in_span & 1) ? other * cs.y + v * cs.x : v * cs.x - other * cs.y;
+// Split-K reduction over the W waves of a workgroup through LDS `part` (W*4*NT*64
+// floatx4): wave w < 4*NT gets the full sums of pair (mt, j) = (w % 4, w / 4) in `v`
+// (lane (g, n)'s C[16mt + 4g + i][16(nt0+j) + n]); the other waves get false.
+template <int NT, int W>
+__device__ __forceinline__ bool splitk_sum(floatx4 (&acc)[4][NT], floatx4* part, int& mt, int& j,
+                                           floatx4& v) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int q = 0; q < NT; ++q)
+            part[((wave * 4 + m) * NT + q) * 64 + lane] = acc[m][q];
+    __syncthreads();
+    if (wave >= 4 * NT)
+        return false;
+    mt = wave % 4;
+    j = wave / 4;
+    v = floatx4{0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+        v += part[((w * 4 + mt) * NT + j) * 64 + lane];
+    return true;
+}
+
+// Per-row sum of squares of this lane group's 16 columns (v holds rows 4g+i of one
+// column; columns that do not count add 0), written by lane n == 0 to
+// ss[row * n_tiles + tile] for rows < B.
+__device__ __forceinline__ void write_ss(floatx4 v, bool col_counts, float* ss, int n_tiles,
+                                         int tile, int row0, int B) {
+    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float q = sum16(col_counts ? v[i] * v[i] : 0.0f);
+        const int row = row0 + 4 * g + i;
+        if (n == 0 && row < B)
+            ss[(long long)row * n_tiles + tile] = q;
+    }
 }
 
 // ------------------------------------------------------------------ embed ----
-// x[b] = E[token[b]] (fp32), rows [B, Mpad) zeroed.  E is read from its tiled
-// logits layout (K = d_model, N = vocab).
+// x[b] = E[token[b]] (fp32) and its per-tile sums of squares; rows [B, m_pad) zeroed.
+// E is read from its tiled logits layout (K = d_model, N = vocab).
 __global__ __launch_bounds__(256) void embed_kernel(StepArgs s) {
     const int b = blockIdx.x;
     const ModelDims& m = s.dims;
-    float* x = s.x + (long long)b * m.d_pad;
-    if (b >= s.B) {
-        for (int c = threadIdx.x; c < m.d_pad; c += 256)
-            x[c] = 0.0f;
-        return;
-    }
-    int tok = s.tokens[b];
+    const int d_tiles = m.d_pad / 16, KT = m.d_pad / 32;
+    int tok = b < s.B ? s.tokens[b] : 0;
     tok = tok < 0 || tok >= m.vocab ? 0 : tok;  // the caller validates tokens
-    const int KT = m.d_pad / 32;
-    for (int c = threadIdx.x; c < m.d_pad; c += 256) {
+    for (int c0 = 0; c0 < m.d_pad; c0 += 256) {
+        const int c = c0 + threadIdx.x;
         float v = 0.0f;
-        if (c < m.d_model) {
+        if (b < s.B && c < m.d_model) {
             const long long w = ((long long)(tok >> 4) * KT + (c >> 5)) * 512 +
                                 (((c & 31) >> 3) * 16 + (tok & 15)) * 8 + (c & 7);
             v = (float)__builtin_bit_cast(_Float16, s.embed[w]);
         }
-        x[c] = v;
+        if (c < m.d_pad)
+            s.x[(long long)b * m.d_pad + c] = v;
+        const float q = sum16(v * v);
+        if ((threadIdx.x & 15) == 0 && c < m.d_pad)
+            s.ss_x[(long long)b * d_tiles + c / 16] = q;
     }
 }
 
-constexpr int kLdsPad = 8;
-
 // --------------------------------------------------------------------- g1 ----
-// RMSNorm(x, attn_norm) . [w_dq | w_dkv] -> cq (q columns) and kvraw (kv columns), fp32.
-// One workgroup per 16-column tile; its 4 waves split K.
+// RMSNorm(x, attn_norm) . [w_dq | w_dkv], one 16-column tile per workgroup: q columns
+// to cq (+ their sums of squares for q_norm), kv columns to kvraw (+ the sums of
+// squares of the latent columns for kv_norm).
 template <int KW>
-__global__ __launch_bounds__(256) void g1_kernel(StepArgs s, LayerWeights L) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+__global__ __launch_bounds__(64 * kWaves) void g1_kernel(StepArgs s, LayerWeights L) {
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * 64];
+    __shared__ float inv_s[64];
     const ModelDims& m = s.dims;
-    const int mc = blockIdx.y, nt = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+    const int mc = blockIdx.y, nt = blockIdx.x, row0 = mc * 64;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
     const int KT = m.d_pad / 32;
     BPre<1, KW> bw;
-    bw.load(L.w_dq_dkv, nt, 1, KT, wave * KW, lane);
-    const int lda = m.d_pad + kLdsPad;
-    _Float16* a_s = reinterpret_cast<_Float16*>(smem);
-    rmsnorm_rows_to_lds(s.x + (long long)mc * 64 * m.d_pad, m.d_pad, m.d_model, m.d_pad, L.attn_norm,
-                        m.eps, a_s, lda);
+    bw.load(L.w_dq_dkv, nt, 1, KT, wave, kWaves, lane);
+    ANorm32<KW> a;
+    a.load(s.x + (long long)row0 * m.d_pad, m.d_pad, m.d_model, KT, wave, kWaves, lane);
+    a.load_w(L.attn_norm, m.d_model, KT, wave, kWaves, lane);
+    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s);
     __syncthreads();
     floatx4 acc[4][1];
     zero(acc);
-    bw.mma_all(acc, ALds16{a_s, lda}, KT, wave * KW, lane);
-    __syncthreads();  // the A tile is dead: its LDS holds the split-K partials
-    splitk_reduce<1, 4>(acc, reinterpret_cast<floatx4*>(smem), [&](int mt, int, floatx4 v) {
-        const int col = nt * 16 + n;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const long long r = (long long)mc * 64 + 16 * mt + 4 * g + i;
-            if (col < m.q_pad)
-                s.cq[r * m.q_pad + col] = v[i];
-            else
-                s.kvraw[r * m.kvw_pad + (col - m.q_pad)] = v[i];
-        }
+    mma_steps(acc, bw, [&](int kk, int mt) {
+        const float inv = inv_s[16 * mt + n];
+        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
     });
+    int mt, j;
+    floatx4 v;
+    if (!splitk_sum<1, kWaves>(acc, part, mt, j, v))
+        return;
+    const int col = nt * 16 + n, g = lane >> 4;
+    const int q_tiles = m.q_pad / 16;
+    const int r0 = row0 + 16 * mt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const long long r = r0 + 4 * g + i;
+        if (col < m.q_pad)
+            s.cq[r * m.q_pad + col] = v[i];
+        else
+            s.kvraw[r * m.kvw_pad + (col - m.q_pad)] = v[i];
+    }
+    if (nt < q_tiles)
+        write_ss(v, true, s.ss_q, q_tiles, nt, r0, s.B);
+    else if ((nt - q_tiles) * 16 < m.kv_rank)
+        write_ss(v, col - m.q_pad < m.kv_rank, s.ss_kv, m.kv_pad / 16, nt - q_tiles, r0, s.B);
 }
 
 // -------------------------------------------------------------------- g23 ----
-// Workgroups h < H: per head, q_norm of the q rows (prologue, fp32 -> fp16 LDS),
-// q_h = cq . w_uq[:, head columns] (one tile per wave) with RoPE on the rope columns
-// (q_rope, stored in the cache dtype), then q_latent_h = q_h[:, :nope] . W_uk_h^T.
-// Workgroup H: kv_norm of the latent, RoPE of the key, rounding to the cache dtype
-// and the paged append of every row (inference.cpp:94-103).
+// Workgroups h < H (4 waves): q_h = q_norm(cq) . w_uq[:, head columns], the waves
+// splitting K over all of the head's tiles; RoPE of the rope columns (pairs read from
+// LDS; cos/sin from the model's table, computed on the host with ops.cpp:88-108's
+// float formula); q_rope stored in the cache dtype; q_latent_h = q_h[:, :nope] .
+// W_uk_h^T.  Workgroups H ..: kv_norm of the latent, RoPE of the key, rounding, append.
+constexpr int kQTiles = 4;  // q tiles of a head (qk <= 64)
+constexpr int kKvWGs = 4, kKvRows = 64 / kKvWGs;  // kv-append workgroups per 64 rows
+constexpr int kKvItems = (kKvRows * (128 + 32) + 255) / 256;  // kv_rank <= 128, rope <= 64
+
+__device__ __forceinline__ float2 rope_cs(const StepArgs& s, int pos, int j) {
+    const ModelDims& m = s.dims;
+    pos = min(max(pos, 0), m.max_seq - 1);  // the caller rejects others (inference.cpp:71-75)
+    return s.rope_tab[(long long)pos * (m.rope / 2) + (j >> 1)];
+}
+
 template <int KWQ, int KWU>
 __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, uint16_t* pool) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const ModelDims& m = s.dims;
-    const int h = blockIdx.x, mc = blockIdx.y;
+    const int h = blockIdx.x, mc = blockIdx.y, row0 = mc * 64;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    if (h == m.H) {  // ---- kv append ----
+    __shared__ float inv_s[64];
+    if (h >= m.H) {  // ---- kv append: kKvRows rows per workgroup, elementwise ----
+        const int r0 = row0 + (h - m.H) * kKvRows;
+        inv_rms_to_lds(s.ss_kv, m.kv_pad / 16, m.kv_rank, m.eps, r0, inv_s, kKvRows);
         const bool tiled = page_tiled(m.page_size, m.kv_rank, m.rope);
-        const int width = m.kv_rank + m.rope;
-        const int r0 = wave * 16;
-        float v[16][4];  // this wave's 16 rows, columns lane + 64 j (width <= 256)
+        const int width = m.kv_rank + m.rope, half = m.rope / 2;
+        const int per_row = m.kv_rank + half;  // latent columns, then rope pairs
+        // every load in flight first (per_row <= 160: kKvItems items a thread) ...
+        float va[kKvItems], vb[kKvItems], wn[kKvItems];
+        int slot[kKvItems], pos[kKvItems];
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = lane + 64 * j;
-                v[rr][j] = c < width ? s.kvraw[((long long)mc * 64 + r0 + rr) * m.kvw_pad + c] : 0.0f;
+        for (int i = 0; i < kKvItems; ++i) {
+            const int e = threadIdx.x + 256 * i, r = e / per_row, c = e % per_row;
+            const int row = r0 + r;
+            va[i] = vb[i] = wn[i] = 0.0f;
+            slot[i] = -1;
+            pos[i] = 0;
+            if (r < kKvRows && row < s.B) {
+                slot[i] = s.slot_mapping[row];
+                const float* kr = s.kvraw + (long long)row * m.kvw_pad;
+                if (c < m.kv_rank) {
+                    va[i] = kr[c];
+                    wn[i] = L.kv_norm[c];
+                } else {
+                    va[i] = kr[m.kv_rank + 2 * (c - m.kv_rank)];
+                    vb[i] = kr[m.kv_rank + 2 * (c - m.kv_rank) + 1];
+                    pos[i] = s.positions[row];
+                }
             }
+        }
+        float2 cs[kKvItems];  // ... then the RoPE table rows of the positions ...
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) {
-            const int row = mc * 64 + r0 + rr;
-            float ss = 0.0f;
+        for (int i = 0; i < kKvItems; ++i) {
+            const int c = (threadIdx.x + 256 * i) % per_row;
+            cs[i] = slot[i] >= 0 && c >= m.kv_rank ? rope_cs(s, pos[i], 2 * (c - m.kv_rank))
+                                                   : float2{1.0f, 0.0f};
+        }
+        __syncthreads();
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                ss += lane + 64 * j < m.kv_rank ? v[rr][j] * v[rr][j] : 0.0f;
-            ss = wave_sum(ss);
-            const float inv = 1.0f / sqrtf(ss / (float)m.kv_rank + m.eps);
-            const int pos = row < s.B ? s.positions[row] : 0;
-            const int slot = row < s.B ? s.slot_mapping[row] : -1;
-            const int page = slot / m.page_size, off = slot % m.page_size;
-            const bool ok = row < s.B && slot >= 0 && page < s.num_pool_pages;
-            uint16_t* base = pool + (long long)(ok ? page : 0) * m.page_size * width;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int c = lane + 64 * j;
-                const bool key = c >= m.kv_rank && c < width;
-                // key pairs (c, c+1) sit in adjacent lanes: the shuffle runs on every lane
-                const float rv = rope_lane(v[rr][j], key ? c - m.kv_rank : 0, m.rope, pos, m.max_seq,
-                                           s.rope_tab);
-                if (!ok || c >= width)
-                    continue;
-                if (c < m.kv_rank)
-                    base[latent_word(tiled, off, c, m.page_size, m.kv_rank)] =
-                        F16::from_float(v[rr][j] * inv * L.kv_norm[c]);
-                else
-                    base[rope_word(tiled, off, c - m.kv_rank, m.page_size, m.kv_rank, m.rope)] =
-                        F16::from_float(rv);
+        for (int i = 0; i < kKvItems; ++i) {  // ... then the rounded stores
+            const int e = threadIdx.x + 256 * i, r = e / per_row, c = e % per_row;
+            const int page = slot[i] / m.page_size, off = slot[i] % m.page_size;
+            if (slot[i] < 0 || page >= s.num_pool_pages)
+                continue;
+            uint16_t* base = pool + (long long)page * m.page_size * width;
+            if (c < m.kv_rank) {
+                base[latent_word(tiled, off, c, m.page_size, m.kv_rank)] =
+                    F16::from_float(va[i] * inv_s[r] * wn[i]);
+            } else {
+                const int jp = 2 * (c - m.kv_rank);
+                base[rope_word(tiled, off, jp, m.page_size, m.kv_rank, m.rope)] =
+                    F16::from_float(va[i] * cs[i].x - vb[i] * cs[i].y);
+                base[rope_word(tiled, off, jp + 1, m.page_size, m.kv_rank, m.rope)] =
+                    F16::from_float(va[i] * cs[i].y + vb[i] * cs[i].x);
             }
         }
         return;
     }
-    // ---- one head ----
+    // ---- one head: q_h over the head's tiles, 4 waves splitting K ----
     const int qk_tiles = m.qk_pad / 16, KTQ = m.q_pad / 32;
     const int kv_tiles = m.kv_pad / 16, KTU = m.nope_pad / 32;
-    const uint16_t* wuk = L.w_uk + (long long)h * kv_tiles * KTU * 512;
-    BPre<1, KWQ> bq;  // this wave's q tile, whole K
-    bq.load(L.w_uq, h * qk_tiles + wave, wave < qk_tiles ? 1 : 0, KTQ, 0, lane);
+    BPre<kQTiles, KWQ> bq;
+    bq.load(L.w_uq, h * qk_tiles, qk_tiles, KTQ, wave, 4, lane);
     BPre<2, KWU> bu;  // this wave's two latent tiles of the absorption, whole K
-    bu.load(wuk, 2 * wave, min(2, kv_tiles - 2 * wave), KTU, 0, lane);
-    const int lda = m.q_pad + kLdsPad;
-    _Float16* a_s = reinterpret_cast<_Float16*>(smem);
-    rmsnorm_rows_to_lds(s.cq + (long long)mc * 64 * m.q_pad, m.q_pad, m.q_rank, m.q_pad, L.q_norm,
-                        m.eps, a_s, lda);
-    const int ldq = m.nope_pad + kLdsPad;  // q_h (nope columns) for the absorption
-    _Float16* q_s = a_s + 64 * lda;
-    for (int i = threadIdx.x; i < 64 * ldq; i += 256)
-        q_s[i] = (_Float16)0.0f;
+    bu.load(L.w_uk + (long long)h * kv_tiles * KTU * 512, 2 * wave, min(2, kv_tiles - 2 * wave),
+            KTU, 0, 1, lane);
+    ANorm32<KWQ> a;
+    a.load(s.cq + (long long)row0 * m.q_pad, m.q_pad, m.q_rank, KTQ, wave, 4, lane);
+    a.load_w(L.q_norm, m.q_rank, KTQ, wave, 4, lane);
+    inv_rms_to_lds(s.ss_q, m.q_pad / 16, m.q_rank, m.eps, row0, inv_s);
     __syncthreads();
-    if (wave < qk_tiles) {
-        floatx4 acc[4][1];
-        zero(acc);
-        bq.mma_all(acc, ALds16{a_s, lda}, KTQ, 0, lane);
-        const int c = wave * 16 + n;  // column inside the head's q
+    floatx4 acc[4][kQTiles];
+    zero(acc);
+    mma_steps(acc, bq, [&](int kk, int mt) {
+        const float inv = inv_s[16 * mt + n];
+        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
+    });
+    // reduce the 4 waves' partials: wave w finishes M-tile w, all of the head's tiles
+    floatx4* part = reinterpret_cast<floatx4*>(smem);  // [4 waves][4 mt][kQTiles][64]
+    float* qf = reinterpret_cast<float*>(smem);         // then q_h fp32 [64][qk_pad + 4]
+    const int ldf = m.qk_pad + 4;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * mt + 4 * g + i, row = mc * 64 + r;
-                float v = acc[mt][0][i];
-                const bool rope_col = c >= m.nope && c < m.qk;
-                const int cs = rope_col ? c - m.nope : 0;
-                const float rv = rope_lane(v, cs, m.rope, row < s.B ? s.positions[row] : 0,
-                                           m.max_seq, s.rope_tab);  // every lane joins the pair shuffle
-                if (rope_col)
-                    v = rv;
-                if (c < m.nope)
-                    q_s[r * ldq + c] = (_Float16)v;
-                else if (rope_col && row < s.B)
-                    s.q_rope[((long long)row * m.H + h) * m.rope + (c - m.nope)] =
-                        F16::from_float(v);
-            }
+        for (int j = 0; j < kQTiles; ++j)
+            part[((wave * 4 + mt) * kQTiles + j) * 64 + lane] = acc[mt][j];
+    __syncthreads();
+    floatx4 q[kQTiles];
+#pragma unroll
+    for (int j = 0; j < kQTiles; ++j) {
+        q[j] = floatx4{0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            q[j] += part[((w * 4 + wave) * kQTiles + j) * 64 + lane];
+    }
+    __syncthreads();  // partials consumed: the LDS now holds q_h in fp32
+#pragma unroll
+    for (int j = 0; j < kQTiles; ++j)
+        if (j < qk_tiles)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                qf[(16 * wave + 4 * g + i) * ldf + 16 * j + n] = q[j][i];
+    __syncthreads();
+    // RoPE + q_rope; q_nope to the fp16 A tile of the absorption
+    const int ldq = m.nope_pad + kLdsPad;
+    _Float16* q_s = reinterpret_cast<_Float16*>(smem + 64 * ldf * sizeof(float));
+    for (int e = threadIdx.x; e < 64 * m.nope_pad; e += 256) {
+        const int r = e / m.nope_pad, c = e % m.nope_pad;
+        q_s[r * ldq + c] = (_Float16)(c < m.nope ? qf[r * ldf + c] : 0.0f);
+    }
+    const int half = m.rope / 2;
+    for (int e = threadIdx.x; e < 64 * half; e += 256) {
+        const int r = e / half, jp = 2 * (e % half), row = row0 + r;
+        if (row >= s.B)
+            break;
+        const float a0 = qf[r * ldf + m.nope + jp], a1 = qf[r * ldf + m.nope + jp + 1];
+        const float2 cs = rope_cs(s, s.positions[row], jp);
+        uint16_t* qr = s.q_rope + ((long long)row * m.H + h) * m.rope;
+        qr[jp] = F16::from_float(a0 * cs.x - a1 * cs.y);
+        qr[jp + 1] = F16::from_float(a0 * cs.y + a1 * cs.x);
     }
     __syncthreads();
+    // q_latent_h = q_h[:, :nope] . W_uk_h^T  (K = nope_pad, N = kv_pad; two tiles a wave)
     if (2 * wave < kv_tiles) {
-        floatx4 acc[4][2];
-        zero(acc);
-        bu.mma_all(acc, ALds16{q_s, ldq}, KTU, 0, lane);
+        floatx4 acc2[4][2];
+        zero(acc2);
+        mma_steps(acc2, bu, [&](int kk, int mt) {  // k-steps past nope_pad: zeros, not LDS
+            return kk < KTU ? *reinterpret_cast<const V8*>(q_s + (16 * mt + n) * ldq + 32 * kk +
+                                                           8 * g)
+                            : V8{};
+        });
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int c = (2 * wave + j) * 16 + n;
@@ -379,65 +493,76 @@ __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, ui
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const int row = mc * 64 + 16 * mt + 4 * g + i;
+                        const int row = row0 + 16 * mt + 4 * g + i;
                         if (row < s.B)
                             s.q_latent[((long long)row * m.H + h) * m.kv_rank + c] =
-                                F16::from_float(acc[mt][j][i]);
+                                F16::from_float(acc2[mt][j][i]);
                     }
         }
     }
 }
 
 // ----------------------------------------------------------- g4 and g6 ----
-// out = A . W + residual for one 16-column tile per workgroup; 8 waves split K.
-constexpr int kSplitWaves = 8;
-
-template <int KW, typename A>
-__device__ __forceinline__ void splitk_residual(const A& a, const uint16_t* w, int KT, int N,
-                                                const float* residual, float* out, int ld, int mc,
-                                                int B) {
-    __shared__ __attribute__((aligned(16))) floatx4 part[kSplitWaves * 4 * 64];
+// out = A . W + residual for one 16-column tile per workgroup (8 waves split K), and
+// the per-tile sums of squares of `out` for the next RMSNorm.
+template <int KW, typename ALoad>
+__device__ __forceinline__ void splitk_residual(ALoad&& aload, const uint16_t* w, int KT, int N,
+                                                const float* residual, float* out, float* ss,
+                                                int n_tiles, int ld, int row0, int B) {
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * 64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int nt = blockIdx.x;
     BPre<1, KW> bw;
-    bw.load(w, nt, 1, KT, wave * KW, lane);
+    bw.load(w, nt, 1, KT, wave, kWaves, lane);
     floatx4 acc[4][1];
     zero(acc);
-    bw.mma_all(acc, a, KT, wave * KW, lane);
-    splitk_reduce<1, kSplitWaves>(acc, part, [&](int mt, int, floatx4 v) {
-        const int col = nt * 16 + n;
-        if (col >= N)
-            return;
+    aload(acc, bw, wave, lane);
+    int mt, j;
+    floatx4 v;
+    if (!splitk_sum<1, kWaves>(acc, part, mt, j, v))
+        return;
+    const int col = nt * 16 + n, r0 = row0 + 16 * mt;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = mc * 64 + 16 * mt + 4 * g + i;
-            if (row < B)
-                out[(long long)row * ld + col] = v[i] + residual[(long long)row * ld + col];
-        }
-    });
+    for (int i = 0; i < 4; ++i) {
+        const long long row = r0 + 4 * g + i;
+        v[i] = col < N ? v[i] + residual[row * ld + col] : 0.0f;
+        if (row < B && col < N)
+            out[row * ld + col] = v[i];
+    }
+    write_ss(v, col < N, ss, n_tiles, nt, r0, B);
 }
 
 template <int KW>
-__global__ __launch_bounds__(64 * kSplitWaves) void g4_kernel(StepArgs s, LayerWeights L) {
+__global__ __launch_bounds__(64 * kWaves) void g4_kernel(StepArgs s, LayerWeights L) {
     const ModelDims& m = s.dims;
-    const int mc = blockIdx.y, ctx_w = m.H * m.kv_rank;  // attention rows are H*kv_rank wide
-    splitk_residual<KW>(AGlb32{s.ctx + (long long)mc * 64 * ctx_w, ctx_w, ctx_w}, L.w_out,
-                        m.ctx_pad / 32, m.d_model, s.x, s.res, m.d_pad, mc, s.B);
+    const int row0 = blockIdx.y * 64, ctx_w = m.H * m.kv_rank;  // attention rows: H*kv_rank
+    const int KT = m.ctx_pad / 32;
+    splitk_residual<KW>(
+        [&](floatx4(&acc)[4][1], const BPre<1, KW>& bw, int kt0, int lane) {
+            AHalf32<KW> a;
+            a.load(s.ctx + (long long)row0 * ctx_w, ctx_w, ctx_w, KT, kt0, kWaves, lane);
+            mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
+        },
+        L.w_out, KT, m.d_model, s.x, s.res, s.ss_res, m.d_pad / 16, m.d_pad, row0, s.B);
 }
 
 template <int KW>
-__global__ __launch_bounds__(64 * kSplitWaves) void g6_kernel(StepArgs s, LayerWeights L) {
+__global__ __launch_bounds__(64 * kWaves) void g6_kernel(StepArgs s, LayerWeights L) {
     const ModelDims& m = s.dims;
-    const int mc = blockIdx.y;
-    splitk_residual<KW>(AGlb16{s.u + (long long)mc * 64 * m.ff_pad, m.ff_pad}, L.w_down,
-                        m.ff_pad / 32, m.d_model, s.res, s.x, m.d_pad, mc, s.B);
+    const int row0 = blockIdx.y * 64, KT = m.ff_pad / 32;
+    splitk_residual<KW>(
+        [&](floatx4(&acc)[4][1], const BPre<1, KW>& bw, int kt0, int lane) {
+            APre16<KW> a;
+            a.load(s.u + (long long)row0 * m.ff_pad, m.ff_pad, KT, kt0, kWaves, lane);
+            mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
+        },
+        L.w_down, KT, m.d_model, s.res, s.x, s.ss_x, m.d_pad / 16, m.d_pad, row0, s.B);
 }
 
 // --------------------------------------------------------------------- g5 ----
-// RMSNorm(res, ffn_norm) prologue; w_gate_up interleaves 16-column tiles of gate and
-// up (tile 2j = gate columns 16j.., tile 2j+1 = up columns 16j..).  One workgroup per
-// pair, 4 waves split K, and SwiGLU (ops.cpp:65-77: gate * sigmoid(gate) * up) is
-// formed after the reduction.
+// RMSNorm(res, ffn_norm) . [w_gate | w_up]: w_gate_up interleaves 16-column tiles of
+// gate and up (tile 2j = gate columns 16j.., tile 2j+1 = up columns 16j..); one pair per
+// workgroup, 8 waves split K, then SwiGLU (ops.cpp:65-77: gate * sigmoid(gate) * up).
 __device__ __forceinline__ float silu_stable(float x) {
     if (x >= 0.0f)
         return x * (1.0f / (1.0f + expf(-x)));
@@ -446,118 +571,134 @@ __device__ __forceinline__ float silu_stable(float x) {
 }
 
 template <int KW>
-__global__ __launch_bounds__(256) void g5_kernel(StepArgs s, LayerWeights L) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+__global__ __launch_bounds__(64 * kWaves) void g5_kernel(StepArgs s, LayerWeights L) {
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * 2 * 64];
+    __shared__ float inv_s[64];
     const ModelDims& m = s.dims;
-    const int mc = blockIdx.y, p = blockIdx.x;
+    const int row0 = blockIdx.y * 64, p = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32;
     BPre<2, KW> bw;
-    bw.load(L.w_gate_up, 2 * p, 2, KT, wave * KW, lane);
-    const int lda = m.d_pad + kLdsPad;
-    _Float16* a_s = reinterpret_cast<_Float16*>(smem);
-    rmsnorm_rows_to_lds(s.res + (long long)mc * 64 * m.d_pad, m.d_pad, m.d_model, m.d_pad,
-                        L.ffn_norm, m.eps, a_s, lda);
+    bw.load(L.w_gate_up, 2 * p, 2, KT, wave, kWaves, lane);
+    ANorm32<KW> a;
+    a.load(s.res + (long long)row0 * m.d_pad, m.d_pad, m.d_model, KT, wave, kWaves, lane);
+    a.load_w(L.ffn_norm, m.d_model, KT, wave, kWaves, lane);
+    inv_rms_to_lds(s.ss_res, m.d_pad / 16, m.d_model, m.eps, row0, inv_s);
     __syncthreads();
     floatx4 acc[4][2];
     zero(acc);
-    bw.mma_all(acc, ALds16{a_s, lda}, KT, wave * KW, lane);
-    __syncthreads();
-    floatx4* part = reinterpret_cast<floatx4*>(smem);
+    mma_steps(acc, bw, [&](int kk, int mt) {
+        const float inv = inv_s[16 * mt + n];
+        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
+    });
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
             part[((wave * 4 + mt) * 2 + j) * 64 + lane] = acc[mt][j];
     __syncthreads();
-    const int mt = wave, col = p * 16 + n;  // wave v finishes M-tile v (gate and up)
+    if (wave >= 4)
+        return;
+    const int mt = wave, col = p * 16 + n;  // wave v finishes M-tile v, gate and up
     floatx4 gt = {0, 0, 0, 0}, up = {0, 0, 0, 0};
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kWaves; ++w) {
         gt += part[((w * 4 + mt) * 2 + 0) * 64 + lane];
         up += part[((w * 4 + mt) * 2 + 1) * 64 + lane];
     }
     if (col < m.d_ff)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = mc * 64 + 16 * mt + 4 * g + i;
+            const int row = row0 + 16 * mt + 4 * g + i;
             if (row < s.B)
                 s.u[(long long)row * m.ff_pad + col] = F16::from_float(silu_stable(gt[i]) * up[i]);
         }
 }
 
 // --------------------------------------------------------------------- g7 ----
-// Final RMSNorm + tied logits h . E^T, kG7Tiles tiles per workgroup (4 waves split K);
-// each workgroup also leaves, per row, the greedy winner of its columns (strict >, so
-// the lowest index wins ties) and whether all of them were finite.
-constexpr int kG7Tiles = 4;
-constexpr int kG7Cols = kG7Tiles * 16;  // columns per workgroup
+// Final RMSNorm + tied logits h . E^T, two 16-column tiles per workgroup (8 waves split
+// K); each workgroup also leaves, per row, the greedy winner of its 32 columns (strict
+// >, so the lowest index wins ties) and whether all of them were finite.
+constexpr int kG7Tiles = 2;
 
 template <int KW>
-__global__ __launch_bounds__(256) void g7_kernel(StepArgs s) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+__global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * kG7Tiles * 64];
+    __shared__ float inv_s[64];
     const ModelDims& m = s.dims;
-    const int mc = blockIdx.y;
+    const int row0 = blockIdx.y * 64;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int KT = m.d_pad / 32, n_tiles = m.vocab_pad / 16, nt0 = blockIdx.x * kG7Tiles;
+    const int KT = m.d_pad / 32;
+    const int n_tiles = m.vocab_pad / 16, nt0 = blockIdx.x * kG7Tiles;
     BPre<kG7Tiles, KW> bw;
-    bw.load(s.embed, nt0, min(kG7Tiles, n_tiles - nt0), KT, wave * KW, lane);
-    const int lda = m.d_pad + kLdsPad;
-    _Float16* a_s = reinterpret_cast<_Float16*>(smem);
-    rmsnorm_rows_to_lds(s.x + (long long)mc * 64 * m.d_pad, m.d_pad, m.d_model, m.d_pad,
-                        s.final_norm, m.eps, a_s, lda);
+    bw.load(s.embed, nt0, min(kG7Tiles, n_tiles - nt0), KT, wave, kWaves, lane);
+    ANorm32<KW> a;
+    a.load(s.x + (long long)row0 * m.d_pad, m.d_pad, m.d_model, KT, wave, kWaves, lane);
+    a.load_w(s.final_norm, m.d_model, KT, wave, kWaves, lane);
+    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s);
     __syncthreads();
     floatx4 acc[4][kG7Tiles];
     zero(acc);
-    bw.mma_all(acc, ALds16{a_s, lda}, KT, wave * KW, lane);
+    mma_steps(acc, bw, [&](int kk, int mt) {
+        const float inv = inv_s[16 * mt + n];
+        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
+    });
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < kG7Tiles; ++j)
+            part[((wave * 4 + mt) * kG7Tiles + j) * 64 + lane] = acc[mt][j];
     __syncthreads();
-    __shared__ float best_v[kG7Tiles][64];
-    __shared__ int best_c[kG7Tiles][64], all_finite[kG7Tiles][64];
-    // wave v reduces tile j = v for every M-tile (4 waves, 4 tiles)
-    splitk_reduce<kG7Tiles, 4>(acc, reinterpret_cast<floatx4*>(smem), [&](int mt, int j, floatx4 v) {
+    if (wave >= 4)
+        return;
+    const int mt = wave;  // wave v finishes M-tile v over the workgroup's columns
+    float bv[4], fin[4];
+    int bc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        bv[i] = -INFINITY;
+        bc[i] = 0x7fffffff;
+        fin[i] = 1.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kG7Tiles; ++j) {  // tiles in increasing column order
+        floatx4 v = {0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            v += part[((w * 4 + mt) * kG7Tiles + j) * 64 + lane];
         const int col = (nt0 + j) * 16 + n;
         const bool valid = nt0 + j < n_tiles && col < m.vocab;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = 16 * mt + 4 * g + i, row = mc * 64 + r;
+            const int row = row0 + 16 * mt + 4 * g + i;
             if (valid && row < s.B)
                 s.logits[(long long)row * m.vocab + col] = v[i];
-            float bv = valid ? v[i] : -INFINITY;
-            int bc = valid ? col : 0x7fffffff, fin = !valid || isfinite(v[i]) ? 1 : 0;
-            // the 16 lanes of a row hold 16 columns: larger value, then lower column
-            for (int off = 8; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, 16);
-                const int oc = __shfl_xor(bc, off, 16);
-                fin &= __shfl_xor(fin, off, 16);
-                if (oc != 0x7fffffff && (bc == 0x7fffffff || ov > bv || (ov == bv && oc < bc))) {
-                    bv = ov;
-                    bc = oc;
-                }
-            }
-            if (n == 0) {
-                best_v[j][r] = bv;
-                best_c[j][r] = bc;
-                all_finite[j][r] = fin;
+            if (valid && !isfinite(v[i]))
+                fin[i] = 0.0f;
+            if (valid && (bc[i] == 0x7fffffff || v[i] > bv[i])) {  // strict >: lowest column
+                bv[i] = v[i];
+                bc[i] = col;
             }
         }
-    });
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const int r = threadIdx.x, row = mc * 64 + r;
-        float bv = -INFINITY;
-        int bc = 0x7fffffff, fin = 1;
-        for (int j = 0; j < kG7Tiles; ++j) {  // tiles in increasing column order
-            fin &= all_finite[j][r];
-            const int oc = best_c[j][r];
-            if (oc != 0x7fffffff && (bc == 0x7fffffff || best_v[j][r] > bv)) {
-                bv = best_v[j][r];
-                bc = oc;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // the 16 lanes of a row hold 16 columns each: larger value, then lower column
+        for (int off = 8; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv[i], off, 16);
+            const int oc = __shfl_xor(bc[i], off, 16);
+            fin[i] = fminf(fin[i], __shfl_xor(fin[i], off, 16));
+            if (oc != 0x7fffffff &&
+                (bc[i] == 0x7fffffff || ov > bv[i] || (ov == bv[i] && oc < bc[i]))) {
+                bv[i] = ov;
+                bc[i] = oc;
             }
         }
-        if (row < s.B) {
+        const int row = row0 + 16 * mt + 4 * g + i;
+        if (n == 0 && row < s.B) {
             const long long idx = (long long)row * gridDim.x + blockIdx.x;
-            s.arg_v[idx] = bv;
-            s.arg_c[idx] = fin ? bc : -1;
+            s.arg_v[idx] = bv[i];
+            s.arg_c[idx] = fin[i] > 0.0f ? bc[i] : -1;
         }
     }
 }
@@ -591,29 +732,18 @@ __global__ __launch_bounds__(64) void argmax_kernel(StepArgs s, int parts) {
         s.next_tokens[row] = bad || bc == 0x7fffffff ? -1 : bc;
 }
 
+// k-steps per wave, rounded up to a compiled variant
+int kw_variant(int ksteps) {
+    return ksteps <= 1 ? 1 : ksteps <= 2 ? 2 : ksteps <= 3 ? 3 : ksteps <= 4 ? 4 : ksteps <= 6 ? 6 : 8;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launches ----
-namespace {
-// k-steps per wave rounded up to a compiled variant
-int kw_variant(int ksteps) { return ksteps <= 1 ? 1 : ksteps <= 2 ? 2 : ksteps <= 4 ? 4 : 8; }
-
-template <template <int> class K>
-struct Dummy;
-}  // namespace
-
-size_t g1_lds_bytes(const ModelDims& m) {
-    const size_t a = 64 * (size_t)(m.d_pad + kLdsPad) * 2;
-    const size_t part = 4 * 4 * 64 * 16;  // split-K partials alias the A tile
-    return a > part ? a : part;
-}
 size_t g23_lds_bytes(const ModelDims& m) {
-    return 64 * (size_t)(m.q_pad + kLdsPad) * 2 + 64 * (size_t)(m.nope_pad + kLdsPad) * 2;
-}
-size_t dpad_lds_bytes(const ModelDims& m) {
-    const size_t a = 64 * (size_t)(m.d_pad + kLdsPad) * 2;
-    const size_t part = 4 * 4 * kG7Tiles * 64 * 16;  // g7 (g5: 4*4*2*64*16)
-    return a > part ? a : part;
+    const size_t part = 4 * 4 * kQTiles * 64 * sizeof(floatx4);
+    const size_t q = 64 * (size_t)(m.qk_pad + 4) * 4 + 64 * (size_t)(m.nope_pad + kLdsPad) * 2;
+    return part > q ? part : q;
 }
 
 int g7_parts(const ModelDims& m) { return (m.vocab_pad / 16 + kG7Tiles - 1) / kG7Tiles; }
@@ -622,22 +752,28 @@ int g7_parts(const ModelDims& m) { return (m.vocab_pad / 16 + kG7Tiles - 1) / kG
     switch (kw) {                                                                                \
     case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;                                   \
     case 2: hipLaunchKernelGGL(KERNEL<2>, __VA_ARGS__); break;                                   \
+    case 3: hipLaunchKernelGGL(KERNEL<3>, __VA_ARGS__); break;                                   \
     case 4: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;                                   \
+    case 6: hipLaunchKernelGGL(KERNEL<6>, __VA_ARGS__); break;                                   \
     default: hipLaunchKernelGGL(KERNEL<8>, __VA_ARGS__); break;                                  \
+    }
+// Kernels that RMSNorm their A operand on the fly (K = d_model <= 1024: 4 k-steps a wave)
+#define MLA_KW4_DISPATCH(kw, KERNEL, ...)                                                       \
+    switch (kw) {                                                                                \
+    case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;                                   \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, __VA_ARGS__); break;                                   \
+    case 3: hipLaunchKernelGGL(KERNEL<3>, __VA_ARGS__); break;                                   \
+    default: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;                                  \
     }
 
 // Kernels whose dynamic LDS can exceed 64 KB.
 hipError_t model_kernel_attributes() {
-    const int bytes = 160 * 1024 - 16 * 1024;
-    const void* ks[] = {
-        reinterpret_cast<const void*>(&g1_kernel<1>), reinterpret_cast<const void*>(&g1_kernel<2>),
-        reinterpret_cast<const void*>(&g1_kernel<4>), reinterpret_cast<const void*>(&g1_kernel<8>),
-        reinterpret_cast<const void*>(&g5_kernel<1>), reinterpret_cast<const void*>(&g5_kernel<2>),
-        reinterpret_cast<const void*>(&g5_kernel<4>), reinterpret_cast<const void*>(&g5_kernel<8>),
-        reinterpret_cast<const void*>(&g7_kernel<1>), reinterpret_cast<const void*>(&g7_kernel<2>),
-        reinterpret_cast<const void*>(&g7_kernel<4>), reinterpret_cast<const void*>(&g7_kernel<8>)};
+    const int bytes = 160 * 1024 - 32 * 1024;
+    const void* ks[] = {reinterpret_cast<const void*>(&g23_kernel<2, 2>),
+                        reinterpret_cast<const void*>(&g23_kernel<2, 4>)};
     for (const void* k : ks) {
-        const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        const hipError_t e =
+            hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (e != hipSuccess)
             return e;
     }
@@ -653,21 +789,18 @@ hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* 
                             hipStream_t st) {
     const ModelDims& m = s.dims;
     const int chunks = s.m_pad / 64;
-    const int g1_tiles = (m.q_pad + m.kvw_pad) / 16;
-    MLA_KW_DISPATCH(kw_variant((m.d_pad / 32 + 3) / 4), g1_kernel, dim3(g1_tiles, chunks),
-                    dim3(256), g1_lds_bytes(m), st, s, w);
+    MLA_KW4_DISPATCH(kw_variant((m.d_pad / 32 + kWaves - 1) / kWaves), g1_kernel,
+                    dim3((m.q_pad + m.kvw_pad) / 16, chunks), dim3(64 * kWaves), 0, st, s, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    const int kwq = kw_variant(m.q_pad / 32), kwu = kw_variant(m.nope_pad / 32);
-    const dim3 grid(m.H + 1, chunks);
+    // q_pad <= 256: at most 2 k-steps of w_uq per wave; nope_pad <= 128: 4 of w_uk
+    const dim3 grid(m.H + kKvWGs, chunks);
     const size_t lds = g23_lds_bytes(m);
-    if (kwq <= 4 && kwu <= 2)
-        hipLaunchKernelGGL((g23_kernel<4, 2>), grid, dim3(256), lds, st, s, w, pool);
-    else if (kwq <= 8 && kwu <= 2)
-        hipLaunchKernelGGL((g23_kernel<8, 2>), grid, dim3(256), lds, st, s, w, pool);
+    if (m.nope_pad / 32 <= 2)
+        hipLaunchKernelGGL((g23_kernel<2, 2>), grid, dim3(256), lds, st, s, w, pool);
     else
-        hipLaunchKernelGGL((g23_kernel<8, 4>), grid, dim3(256), lds, st, s, w, pool);
+        hipLaunchKernelGGL((g23_kernel<2, 4>), grid, dim3(256), lds, st, s, w, pool);
     return hipGetLastError();
 }
 
@@ -675,26 +808,26 @@ hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, hipStream
     const ModelDims& m = s.dims;
     const int chunks = s.m_pad / 64;
     const int d_tiles = m.d_pad / 16;
-    MLA_KW_DISPATCH(kw_variant((m.ctx_pad / 32 + kSplitWaves - 1) / kSplitWaves), g4_kernel,
-                    dim3(d_tiles, chunks), dim3(64 * kSplitWaves), 0, st, s, w);
+    MLA_KW_DISPATCH(kw_variant((m.ctx_pad / 32 + kWaves - 1) / kWaves), g4_kernel,
+                    dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    MLA_KW_DISPATCH(kw_variant((m.d_pad / 32 + 3) / 4), g5_kernel, dim3(m.ff_pad / 16, chunks),
-                    dim3(256), dpad_lds_bytes(m), st, s, w);
+    MLA_KW4_DISPATCH(kw_variant((m.d_pad / 32 + kWaves - 1) / kWaves), g5_kernel,
+                    dim3(m.ff_pad / 16, chunks), dim3(64 * kWaves), 0, st, s, w);
     e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    MLA_KW_DISPATCH(kw_variant((m.ff_pad / 32 + kSplitWaves - 1) / kSplitWaves), g6_kernel,
-                    dim3(d_tiles, chunks), dim3(64 * kSplitWaves), 0, st, s, w);
+    MLA_KW_DISPATCH(kw_variant((m.ff_pad / 32 + kWaves - 1) / kWaves), g6_kernel,
+                    dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w);
     return hipGetLastError();
 }
 
 hipError_t launch_logits(const StepArgs& s, hipStream_t st) {
     const ModelDims& m = s.dims;
     const int parts = g7_parts(m);
-    MLA_KW_DISPATCH(kw_variant((m.d_pad / 32 + 3) / 4), g7_kernel, dim3(parts, s.m_pad / 64),
-                    dim3(256), dpad_lds_bytes(m), st, s);
+    MLA_KW4_DISPATCH(kw_variant((m.d_pad / 32 + kWaves - 1) / kWaves), g7_kernel,
+                    dim3(parts, s.m_pad / 64), dim3(64 * kWaves), 0, st, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;

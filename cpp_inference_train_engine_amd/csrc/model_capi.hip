@@ -119,6 +119,7 @@ struct Model {
     const float* final_norm = nullptr;
     const float* rope_tab = nullptr;
     float *x, *res, *cq, *ctx, *kvraw, *logits, *arg_v;
+    float *ss_x, *ss_res, *ss_q, *ss_kv;
     uint16_t *u, *q_latent, *q_rope;
     int32_t* arg_c;
 
@@ -200,17 +201,16 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_create: invalid argument");
     const mla_model_config& c = *config;
     const ModelDims m = make_dims(c, page_size);
-    // Shapes the step kernels cover: the kv row of [w_dq | w_dkv] within one wave's
-    // registers (<= 256 columns), a head's q within one workgroup (<= 4 tiles) and its
-    // absorption within 4 waves x 2 tiles, rows of at most 1024 (norm prologues) and
-    // 256 k-steps per split-K wave group, attention rows a multiple of 8 floats.
-    if (c.kv_lora_rank + c.head_dim_rope > 256 || m.qk_pad / 16 > 4 || m.kv_pad / 16 > 8 ||
-        (c.n_heads * c.kv_lora_rank) % 8 || m.d_pad > 1024 || m.q_pad > 256 ||
+    // Shapes the step kernels cover: a head's q within one workgroup (<= 4 tiles) and its
+    // absorption within 4 waves x 2 tiles, at most 8 k-steps per split-K wave (d_model,
+    // q_lora_rank: 4 with their on-the-fly norms), fp32 rows read 8 columns at a time.
+    if (m.qk_pad / 16 > 4 || m.kv_pad / 16 > 8 || (c.n_heads * c.kv_lora_rank) % 8 ||
+        c.d_model % 8 || c.q_lora_rank % 8 || m.d_pad > 1024 || m.q_pad > 256 ||
         m.nope_pad > 128 || m.ctx_pad / 32 > 64 || m.ff_pad / 32 > 64)
         return fail(MLA_ERR_UNSUPPORTED,
-                    "mla_model_create: shape outside the step kernels (kv_lora_rank + "
-                    "head_dim_rope <= 256, head_dim_nope + head_dim_rope <= 64, kv_lora_rank "
-                    "<= 128, head_dim_nope <= 128, q_lora_rank <= 256, d_model <= 1024, "
+                    "mla_model_create: shape outside the step kernels (head_dim_nope + "
+                    "head_dim_rope <= 64, kv_lora_rank <= 128, head_dim_nope <= 128, "
+                    "q_lora_rank <= 256 and d_model <= 1024, both multiples of 8, "
                     "n_heads*kv_lora_rank <= 2048 and a multiple of 8, d_ff <= 2048)");
     auto* M = new (std::nothrow) Model();
     if (!M)
@@ -324,6 +324,10 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
     if (e == hipSuccess) e = M->alloc(M->logits, (size_t)max_batch * c.vocab_size);
     if (e == hipSuccess) e = M->alloc(M->arg_v, (size_t)max_batch * M->parts);
     if (e == hipSuccess) e = M->alloc(M->arg_c, (size_t)max_batch * M->parts);
+    if (e == hipSuccess) e = M->alloc(M->ss_x, rows * (m.d_pad / 16));
+    if (e == hipSuccess) e = M->alloc(M->ss_res, rows * (m.d_pad / 16));
+    if (e == hipSuccess) e = M->alloc(M->ss_q, rows * (m.q_pad / 16));
+    if (e == hipSuccess) e = M->alloc(M->ss_kv, rows * (m.kv_pad / 16));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess)
         return bail(e);
@@ -384,6 +388,10 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
     s.arg_v = M->arg_v;
     s.arg_c = M->arg_c;
     s.next_tokens = next_tokens;
+    s.ss_x = M->ss_x;
+    s.ss_res = M->ss_res;
+    s.ss_q = M->ss_q;
+    s.ss_kv = M->ss_kv;
     DecodeArgs a{};
     a.B = B;
     a.H = m.H;
