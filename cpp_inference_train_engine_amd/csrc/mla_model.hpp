@@ -54,8 +54,11 @@ struct StepArgs {
     const uint16_t* embed;     // token_embedding [V x d] tiled as the logits W (K=d, N=V)
     const float* final_norm;
     const float2* rope_tab;    // [max_seq x rope/2] (cos, sin) of pos * theta^(-j/rope)
-    // activations (rows padded to m_pad; padding rows stay zero)
-    float *x, *res, *cq, *ctx;  // [m_pad x d_pad], [m_pad x d_pad], [m_pad x q_pad], [m_pad x H*kv_rank]
+    float2* rope_rows;         // [m_pad x rope/2] the table rows of this step's positions
+    // activations (rows padded to m_pad)
+    float *x, *res, *ctx;       // [m_pad x d_pad], [m_pad x d_pad], [m_pad x H*kv_rank]
+    uint16_t *xw, *resw;        // fp16 x o (next norm weight), res o ffn_norm [m_pad x d_pad]
+    uint16_t* cqw;              // fp16 cq o q_norm [m_pad x q_pad]
     float* kvraw;               // [m_pad x kvw_pad] kv columns of [w_dq | w_dkv]
     uint16_t *u;                // [m_pad x ff_pad] fp16
     uint16_t *q_latent, *q_rope;  // [B x H x kv_rank], [B x H x rope] in the cache dtype
@@ -74,10 +77,13 @@ struct StepArgs {
 int g7_parts(const ModelDims& m);
 size_t g23_lds_bytes(const ModelDims& m);
 hipError_t model_kernel_attributes();
-hipError_t launch_embed(const StepArgs& s, hipStream_t st);
+// first_norm: attn_norm of layer 0
+hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t st);
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
                             hipStream_t st);  // g1, then g23 (which appends to `pool`)
-hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, hipStream_t st);
+// next_norm: attn_norm of the next layer, or final_norm after the last one
+hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const float* next_norm,
+                             hipStream_t st);
 hipError_t launch_logits(const StepArgs& s, hipStream_t st);
 
 }  // namespace mla

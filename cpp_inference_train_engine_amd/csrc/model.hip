@@ -15,21 +15,23 @@
 //               is the combined W_uv.W_o of prepare_projections, inference.cpp:28-46)
 //   g5_kernel   RMSNorm(ffn_norm) -> [w_gate | w_up] -> SwiGLU  (inference.cpp:157-161)
 //   g6_kernel   . w_down + residual  (inference.cpp:162-165)
-// Per step: embed_kernel (token rows), g7_kernel (final RMSNorm, tied logits
-// h.E^T, inference.cpp:166-168, with a per-workgroup greedy partial) and
-// argmax_kernel (sample_token's greedy rule, inference.cpp:345-380).
+// Per step: embed_kernel (token rows, RoPE rows), g7_kernel (final RMSNorm, tied logits
+// h.E^T, inference.cpp:166-168, with a per-workgroup greedy partial) and argmax_kernel
+// (sample_token's greedy rule, inference.cpp:345-380).
 //
-// Every projection is a skinny GEMM (M = the batch rows, 64 per chunk) on
-// v_mfma_f32_16x16x32_f16, fp16 operands, fp32 accumulation.  A workgroup owns one or
-// two 16-column output tiles and its 8 waves split K; each wave fetches its weight
-// tiles (fp16, TILED: each wave load reads 1 KB contiguously) and its slice of the
-// activation rows into registers at kernel start, so a GEMM pays about one memory
-// round trip, and the partial sums meet in LDS.
+// Every projection is a skinny GEMM on v_mfma_f32_16x16x32_f16 (fp16 operands, fp32
+// accumulation).  A workgroup owns 16 rows (64 for the logits) and one to four 16-column
+// output tiles; its 8 waves split K.  Each wave fetches its weight tiles (fp16, TILED:
+// each wave load reads 1 KB contiguously) and its slice of the activation rows into
+// registers at kernel start, so a GEMM pays about one memory round trip, and the
+// partial sums meet in LDS.  Small row blocks keep the bytes each CU must pull low:
+// the load phase, not the arithmetic, is what these kernels wait on.
 //
-// RMSNorm (ops.cpp:33-45) never re-reads a row: the kernel that writes a normalised
-// activation also writes, per row and 16-column tile, the sum of squares of its
-// columns; the consumer adds those partials (in a fixed order) into 1/rms per row
-// and scales its A operands by it and by the norm weight while rounding them to fp16.
+// RMSNorm (ops.cpp:33-45) is RMSNorm(x)_k = x_k * inv * w_k with inv = 1/rms(x) per row,
+// so RMSNorm(x).W = inv * ((x o w).W): the kernel that writes an activation x also
+// writes (x o w) in fp16 for the consumer's A operand (w = the norm weight of the next
+// consumer) and, per row and 16-column tile, the sum of squares of x; the consumer adds
+// those partials (in a fixed order) into inv and scales its output rows by it.
 #include "mla_common.hpp"
 #include "mla_internal.hpp"
 #include "mla_model.hpp"
@@ -40,7 +42,7 @@ namespace mla {
 namespace {
 
 using V8 = half8;
-constexpr int kWaves = 8;  // split-K waves per GEMM workgroup
+constexpr int kWaves = 8;  // waves per GEMM workgroup
 constexpr int kLdsPad = 8;
 
 __device__ __forceinline__ floatx4 mma(V8 a, V8 b, floatx4 c) {
@@ -61,10 +63,10 @@ __device__ __forceinline__ float sum16(float v) {
     return v;
 }
 
-template <int NT>
-__device__ __forceinline__ void zero(floatx4 (&acc)[4][NT]) {
+template <int MT, int NT>
+__device__ __forceinline__ void zero(floatx4 (&acc)[MT][NT]) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int j = 0; j < NT; ++j)
             acc[mt][j] = floatx4{0, 0, 0, 0};
@@ -72,7 +74,7 @@ __device__ __forceinline__ void zero(floatx4 (&acc)[4][NT]) {
 
 // ---- operand prefetch ----------------------------------------------------------
 // A wave's k-steps are kt0, kt0 + ks, kt0 + 2ks, ... (KW of them; kt0 = the wave's
-// index and ks = the waves splitting K, so uneven K spreads evenly); k-steps past KT
+// K group and ks = the number of K groups, so uneven K spreads evenly); k-steps past KT
 // load zeros and add nothing.
 //
 // Weight (B operand) registers of one wave: its k-steps of tiles [nt0, nt0+NT); tiles
@@ -96,12 +98,29 @@ struct BPre {
     }
 };
 
-// Activation (A operand) registers: lane (g, n) needs rows 16mt + n (mt = 0..3) and
-// columns 32kt + 8g .. +7 of each of its k-steps.  Columns past K read as zero
-// (K % 8 == 0, so an 8-column chunk is wholly in or out).
-template <int KW>
-struct APre32 {  // fp32 rows
-    floatx4 x[KW][4][2];
+// Activation (A operand) registers: lane (g, n) needs rows 16mt + n (mt < MT) and
+// columns 32kt + 8g .. +7 of each of its k-steps.
+template <int KW, int MT>
+struct APre16 {  // fp16 rows, zero-padded to KT*32 columns
+    V8 x[KW][MT];
+    __device__ __forceinline__ void load(const uint16_t* X, int ld, int KT, int kt0, int ks,
+                                         int lane) {
+        const int g = lane >> 4, n = lane & 15;
+#pragma unroll
+        for (int kk = 0; kk < KW; ++kk)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int kt = kt0 + kk * ks;
+                x[kk][mt] = V8{};
+                if (kt < KT)
+                    x[kk][mt] = *reinterpret_cast<const V8*>(X + (long long)(16 * mt + n) * ld +
+                                                             32 * kt + 8 * g);
+            }
+    }
+};
+template <int KW, int MT>
+struct AHalf32 {  // fp32 rows (K % 8 == 0; columns past K read as zero), rounded to fp16
+    V8 x[KW][MT];
     __device__ __forceinline__ void load(const float* X, int ld, int K, int KT, int kt0, int ks,
                                          int lane) {
         const int g = lane >> 4, n = lane & 15;
@@ -111,49 +130,7 @@ struct APre32 {  // fp32 rows
             const int k = 32 * kt + 8 * g;
             const bool ok = kt < KT && k < K;
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                x[kk][mt][0] = x[kk][mt][1] = floatx4{0, 0, 0, 0};
-                if (ok) {
-                    const floatx4* p =
-                        reinterpret_cast<const floatx4*>(X + (long long)(16 * mt + n) * ld + k);
-                    x[kk][mt][0] = p[0];
-                    x[kk][mt][1] = p[1];
-                }
-            }
-        }
-    }
-};
-template <int KW>
-struct ANorm32 : APre32<KW> {  // fp32 rows, RMSNorm-ed on the fly: x * inv[row] * w[col]
-    floatx4 w[KW][2];
-    __device__ __forceinline__ void load_w(const float* wn, int K, int KT, int kt0, int ks,
-                                           int lane) {
-        const int g = lane >> 4;
-#pragma unroll
-        for (int kk = 0; kk < KW; ++kk) {
-            const int kt = kt0 + kk * ks;
-            const int k = 32 * kt + 8 * g;
-            w[kk][0] = w[kk][1] = floatx4{0, 0, 0, 0};
-            if (kt < KT && k < K) {
-                w[kk][0] = *reinterpret_cast<const floatx4*>(wn + k);
-                w[kk][1] = *reinterpret_cast<const floatx4*>(wn + k + 4);
-            }
-        }
-    }
-};
-template <int KW>
-struct AHalf32 {  // fp32 rows rounded to fp16 operands as they arrive (half the registers)
-    V8 x[KW][4];
-    __device__ __forceinline__ void load(const float* X, int ld, int K, int KT, int kt0, int ks,
-                                         int lane) {
-        const int g = lane >> 4, n = lane & 15;
-#pragma unroll
-        for (int kk = 0; kk < KW; ++kk) {
-            const int kt = kt0 + kk * ks;
-            const int k = 32 * kt + 8 * g;
-            const bool ok = kt < KT && k < K;
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
+            for (int mt = 0; mt < MT; ++mt) {
                 x[kk][mt] = V8{};
                 if (ok) {
                     const floatx4* p =
@@ -164,31 +141,14 @@ struct AHalf32 {  // fp32 rows rounded to fp16 operands as they arrive (half the
         }
     }
 };
-template <int KW>
-struct APre16 {  // fp16 rows (the buffer is zero-padded to KT*32 columns)
-    V8 x[KW][4];
-    __device__ __forceinline__ void load(const uint16_t* X, int ld, int KT, int kt0, int ks,
-                                         int lane) {
-        const int g = lane >> 4, n = lane & 15;
-#pragma unroll
-        for (int kk = 0; kk < KW; ++kk)
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const int kt = kt0 + kk * ks;
-                x[kk][mt] = V8{};
-                if (kt < KT)
-                    x[kk][mt] = *reinterpret_cast<const V8*>(X + (long long)(16 * mt + n) * ld +
-                                                             32 * kt + 8 * g);
-            }
-    }
-};
 
-template <int NT, int KW, typename AOp>
-__device__ __forceinline__ void mma_steps(floatx4 (&acc)[4][NT], const BPre<NT, KW>& b, AOp aop) {
+template <int MT, int NT, int KW, typename AOp>
+__device__ __forceinline__ void mma_steps(floatx4 (&acc)[MT][NT], const BPre<NT, KW>& b,
+                                          AOp aop) {
 #pragma unroll
     for (int kk = 0; kk < KW; ++kk)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
             const V8 a = aop(kk, mt);
 #pragma unroll
             for (int j = 0; j < NT; ++j)
@@ -199,9 +159,10 @@ __device__ __forceinline__ void mma_steps(floatx4 (&acc)[4][NT], const BPre<NT, 
 // 1/rms of `rows` rows (ops.cpp:33-45: inv = 1/sqrt(mean(x^2) + eps)) from the
 // producer's per-tile partial sums of squares (n_tiles <= 64): four threads a row each
 // load every fourth tile at once (one round trip), then combine in a fixed order.
-// Threads [0, 4*rows) take part; rows is 16 or 64, so they fill whole waves.
+// Threads [0, 4*rows) take part; rows is 16 or 64, so they fill whole waves.  Visible
+// to the workgroup after its next barrier.
 __device__ __forceinline__ void inv_rms_to_lds(const float* ss, int n_tiles, int K, float eps,
-                                               int row0, float* inv_s, int rows = 64) {
+                                               int row0, float* inv_s, int rows) {
     const int t = threadIdx.x;
     if (t < 4 * rows) {
         const float* p = ss + (long long)(row0 + (t >> 2)) * n_tiles;
@@ -222,64 +183,83 @@ __device__ __forceinline__ void inv_rms_to_lds(const float* ss, int n_tiles, int
     }
 }
 
-// Split-K reduction over the W waves of a workgroup through LDS `part` (W*4*NT*64
-// floatx4): wave w < 4*NT gets the full sums of pair (mt, j) = (w % 4, w / 4) in `v`
-// (lane (g, n)'s C[16mt + 4g + i][16(nt0+j) + n]); the other waves get false.
-template <int NT, int W>
-__device__ __forceinline__ bool splitk_sum(floatx4 (&acc)[4][NT], floatx4* part, int& mt, int& j,
-                                           floatx4& v) {
+// Split-K reduction through LDS `part` (kWaves*MT*NTW*64 floatx4).  Wave w computed K
+// group w % KG of tiles [(w / KG) * NTW, +NTW); after the barrier wave mt < MT sums all
+// K groups of M-tile mt into v[t] for the workgroup's NT = NTW * kWaves / KG tiles
+// (lane (g, n): C[16mt + 4g + i][16t + n]); other waves get false.
+template <int MT, int NTW, int KG>
+__device__ __forceinline__ bool splitk_reduce(floatx4 (&acc)[MT][NTW], floatx4* part, int& mt,
+                                              floatx4 (&v)[NTW * (kWaves / KG)]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int q = 0; q < NT; ++q)
-            part[((wave * 4 + m) * NT + q) * 64 + lane] = acc[m][q];
+        for (int j = 0; j < NTW; ++j)
+            part[((wave * MT + m) * NTW + j) * 64 + lane] = acc[m][j];
     __syncthreads();
-    if (wave >= 4 * NT)
+    if (wave >= MT)
         return false;
-    mt = wave % 4;
-    j = wave / 4;
-    v = floatx4{0, 0, 0, 0};
+    mt = wave;
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-        v += part[((w * 4 + mt) * NT + j) * 64 + lane];
+    for (int ng = 0; ng < kWaves / KG; ++ng)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+            floatx4 sum = {0, 0, 0, 0};
+#pragma unroll
+            for (int kg = 0; kg < KG; ++kg)
+                sum += part[(((ng * KG + kg) * MT + mt) * NTW + j) * 64 + lane];
+            v[ng * NTW + j] = sum;
+        }
     return true;
 }
 
-// Per-row sum of squares of this lane group's 16 columns (v holds rows 4g+i of one
+// Per-row sum of squares of this lane group's 16 columns (y holds rows 4g+i of one
 // column; columns that do not count add 0), written by lane n == 0 to
 // ss[row * n_tiles + tile] for rows < B.
-__device__ __forceinline__ void write_ss(floatx4 v, bool col_counts, float* ss, int n_tiles,
+__device__ __forceinline__ void write_ss(floatx4 y, bool col_counts, float* ss, int n_tiles,
                                          int tile, int row0, int B) {
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float q = sum16(col_counts ? v[i] * v[i] : 0.0f);
+        const float q = sum16(col_counts ? y[i] * y[i] : 0.0f);
         const int row = row0 + 4 * g + i;
         if (n == 0 && row < B)
             ss[(long long)row * n_tiles + tile] = q;
     }
 }
 
+__device__ __forceinline__ float2 rope_table(const StepArgs& s, int pos, int j2) {
+    const ModelDims& m = s.dims;
+    pos = min(max(pos, 0), m.max_seq - 1);  // the caller rejects others (inference.cpp:71-75)
+    return s.rope_tab[(long long)pos * (m.rope / 2) + j2];
+}
+
 // ------------------------------------------------------------------ embed ----
-// x[b] = E[token[b]] (fp32) and its per-tile sums of squares; rows [B, m_pad) zeroed.
-// E is read from its tiled logits layout (K = d_model, N = vocab).
-__global__ __launch_bounds__(256) void embed_kernel(StepArgs s) {
+// x[b] = E[token[b]] (fp32), xw[b] = x o attn_norm of layer 0 (fp16), the per-tile sums
+// of squares of x, and the (cos, sin) row of b's position for every layer's RoPE; rows
+// [B, m_pad) are zeroed.  E is read from its tiled logits layout (K = d_model, N = vocab).
+__global__ __launch_bounds__(256) void embed_kernel(StepArgs s, const float* norm0) {
     const int b = blockIdx.x;
     const ModelDims& m = s.dims;
-    const int d_tiles = m.d_pad / 16, KT = m.d_pad / 32;
+    const int d_tiles = m.d_pad / 16, KT = m.d_pad / 32, half = m.rope / 2;
     int tok = b < s.B ? s.tokens[b] : 0;
     tok = tok < 0 || tok >= m.vocab ? 0 : tok;  // the caller validates tokens
+    if ((int)threadIdx.x < half)
+        s.rope_rows[(long long)b * half + threadIdx.x] =
+            b < s.B ? rope_table(s, s.positions[b], threadIdx.x) : float2{1.0f, 0.0f};
     for (int c0 = 0; c0 < m.d_pad; c0 += 256) {
         const int c = c0 + threadIdx.x;
-        float v = 0.0f;
+        float v = 0.0f, w = 0.0f;
         if (b < s.B && c < m.d_model) {
-            const long long w = ((long long)(tok >> 4) * KT + (c >> 5)) * 512 +
+            const long long e = ((long long)(tok >> 4) * KT + (c >> 5)) * 512 +
                                 (((c & 31) >> 3) * 16 + (tok & 15)) * 8 + (c & 7);
-            v = (float)__builtin_bit_cast(_Float16, s.embed[w]);
+            v = (float)__builtin_bit_cast(_Float16, s.embed[e]);
+            w = norm0[c];
         }
-        if (c < m.d_pad)
+        if (c < m.d_pad) {
             s.x[(long long)b * m.d_pad + c] = v;
+            s.xw[(long long)b * m.d_pad + c] = F16::from_float(v * w);
+        }
         const float q = sum16(v * v);
         if ((threadIdx.x & 15) == 0 && c < m.d_pad)
             s.ss_x[(long long)b * d_tiles + c / 16] = q;
@@ -287,66 +267,57 @@ __global__ __launch_bounds__(256) void embed_kernel(StepArgs s) {
 }
 
 // --------------------------------------------------------------------- g1 ----
-// RMSNorm(x, attn_norm) . [w_dq | w_dkv], one 16-column tile per workgroup: q columns
-// to cq (+ their sums of squares for q_norm), kv columns to kvraw (+ the sums of
-// squares of the latent columns for kv_norm).
+// RMSNorm(x, attn_norm) . [w_dq | w_dkv] for 16 rows and one 16-column tile: q columns
+// to cqw = cq o q_norm (fp16, with cq's sums of squares for q_norm's inv), kv columns
+// to kvraw (fp32, with the sums of squares of the latent columns for kv_norm).
 template <int KW>
 __global__ __launch_bounds__(64 * kWaves) void g1_kernel(StepArgs s, LayerWeights L) {
-    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * 64];
-    __shared__ float inv_s[64];
+    constexpr int MT = 1, KG = kWaves;
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * MT * 64];
+    __shared__ float inv_s[16 * MT];
     const ModelDims& m = s.dims;
-    const int mc = blockIdx.y, nt = blockIdx.x, row0 = mc * 64;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
-    const int KT = m.d_pad / 32;
+    const int nt = blockIdx.x, row0 = blockIdx.y * 16 * MT;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+    const int KT = m.d_pad / 32, col = nt * 16 + n;
+    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s, 16 * MT);
     BPre<1, KW> bw;
-    bw.load(L.w_dq_dkv, nt, 1, KT, wave, kWaves, lane);
-    ANorm32<KW> a;
-    a.load(s.x + (long long)row0 * m.d_pad, m.d_pad, m.d_model, KT, wave, kWaves, lane);
-    a.load_w(L.attn_norm, m.d_model, KT, wave, kWaves, lane);
-    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s);
-    __syncthreads();
-    floatx4 acc[4][1];
+    bw.load(L.w_dq_dkv, nt, 1, KT, wave, KG, lane);
+    APre16<KW, MT> a;
+    a.load(s.xw + (long long)row0 * m.d_pad, m.d_pad, KT, wave, KG, lane);
+    const float qn = col < m.q_rank ? L.q_norm[col] : 0.0f;
+    floatx4 acc[MT][1];
     zero(acc);
-    mma_steps(acc, bw, [&](int kk, int mt) {
-        const float inv = inv_s[16 * mt + n];
-        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
-    });
-    int mt, j;
-    floatx4 v;
-    if (!splitk_sum<1, kWaves>(acc, part, mt, j, v))
+    mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
+    int mt;
+    floatx4 v[1];
+    if (!splitk_reduce<MT, 1, KG>(acc, part, mt, v))
         return;
-    const int col = nt * 16 + n, g = lane >> 4;
-    const int q_tiles = m.q_pad / 16;
-    const int r0 = row0 + 16 * mt;
+    const int q_tiles = m.q_pad / 16, r0 = row0 + 16 * mt;
+    floatx4 y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const long long r = r0 + 4 * g + i;
+        y[i] = v[0][i] * inv_s[16 * mt + 4 * g + i];
         if (col < m.q_pad)
-            s.cq[r * m.q_pad + col] = v[i];
+            s.cqw[r * m.q_pad + col] = F16::from_float(y[i] * qn);
         else
-            s.kvraw[r * m.kvw_pad + (col - m.q_pad)] = v[i];
+            s.kvraw[r * m.kvw_pad + (col - m.q_pad)] = y[i];
     }
     if (nt < q_tiles)
-        write_ss(v, true, s.ss_q, q_tiles, nt, r0, s.B);
+        write_ss(y, true, s.ss_q, q_tiles, nt, r0, s.B);
     else if ((nt - q_tiles) * 16 < m.kv_rank)
-        write_ss(v, col - m.q_pad < m.kv_rank, s.ss_kv, m.kv_pad / 16, nt - q_tiles, r0, s.B);
+        write_ss(y, col - m.q_pad < m.kv_rank, s.ss_kv, m.kv_pad / 16, nt - q_tiles, r0, s.B);
 }
 
 // -------------------------------------------------------------------- g23 ----
-// Workgroups h < H (4 waves): q_h = q_norm(cq) . w_uq[:, head columns], the waves
-// splitting K over all of the head's tiles; RoPE of the rope columns (pairs read from
-// LDS; cos/sin from the model's table, computed on the host with ops.cpp:88-108's
-// float formula); q_rope stored in the cache dtype; q_latent_h = q_h[:, :nope] .
-// W_uk_h^T.  Workgroups H ..: kv_norm of the latent, RoPE of the key, rounding, append.
-constexpr int kQTiles = 4;  // q tiles of a head (qk <= 64)
+// Workgroups h < H (4 waves, 64 rows): q_h = q_norm(cq) . w_uq[:, head columns], the
+// waves splitting K over all of the head's tiles; RoPE of the rope columns (pairs read
+// from LDS); q_rope stored in the cache dtype; q_latent_h = q_h[:, :nope] . W_uk_h^T.
+// Workgroups H ..: kv_norm of the latent, RoPE of the key, rounding, append.
+constexpr int kQTiles = 4;                        // q tiles of a head (qk <= 64)
+constexpr int kRopeItems = 64 * 32 / 256;         // RoPE pairs a thread (rope <= 64)
 constexpr int kKvWGs = 4, kKvRows = 64 / kKvWGs;  // kv-append workgroups per 64 rows
 constexpr int kKvItems = (kKvRows * (128 + 32) + 255) / 256;  // kv_rank <= 128, rope <= 64
-
-__device__ __forceinline__ float2 rope_cs(const StepArgs& s, int pos, int j) {
-    const ModelDims& m = s.dims;
-    pos = min(max(pos, 0), m.max_seq - 1);  // the caller rejects others (inference.cpp:71-75)
-    return s.rope_tab[(long long)pos * (m.rope / 2) + (j >> 1)];
-}
 
 template <int KWQ, int KWU>
 __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, uint16_t* pool) {
@@ -354,23 +325,26 @@ __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, ui
     const ModelDims& m = s.dims;
     const int h = blockIdx.x, mc = blockIdx.y, row0 = mc * 64;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+    const int half = m.rope / 2;
     __shared__ float inv_s[64];
     if (h >= m.H) {  // ---- kv append: kKvRows rows per workgroup, elementwise ----
         const int r0 = row0 + (h - m.H) * kKvRows;
         inv_rms_to_lds(s.ss_kv, m.kv_pad / 16, m.kv_rank, m.eps, r0, inv_s, kKvRows);
         const bool tiled = page_tiled(m.page_size, m.kv_rank, m.rope);
-        const int width = m.kv_rank + m.rope, half = m.rope / 2;
+        const int width = m.kv_rank + m.rope;
         const int per_row = m.kv_rank + half;  // latent columns, then rope pairs
-        // every load in flight first (per_row <= 160: kKvItems items a thread) ...
+        // every load in flight first (per_row <= 160: kKvItems items a thread), then the
+        // rounded stores
         float va[kKvItems], vb[kKvItems], wn[kKvItems];
-        int slot[kKvItems], pos[kKvItems];
+        float2 cs[kKvItems];
+        int slot[kKvItems];
 #pragma unroll
         for (int i = 0; i < kKvItems; ++i) {
             const int e = threadIdx.x + 256 * i, r = e / per_row, c = e % per_row;
             const int row = r0 + r;
             va[i] = vb[i] = wn[i] = 0.0f;
+            cs[i] = float2{1.0f, 0.0f};
             slot[i] = -1;
-            pos[i] = 0;
             if (r < kKvRows && row < s.B) {
                 slot[i] = s.slot_mapping[row];
                 const float* kr = s.kvraw + (long long)row * m.kvw_pad;
@@ -378,22 +352,16 @@ __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, ui
                     va[i] = kr[c];
                     wn[i] = L.kv_norm[c];
                 } else {
-                    va[i] = kr[m.kv_rank + 2 * (c - m.kv_rank)];
-                    vb[i] = kr[m.kv_rank + 2 * (c - m.kv_rank) + 1];
-                    pos[i] = s.positions[row];
+                    const int j2 = c - m.kv_rank;
+                    va[i] = kr[m.kv_rank + 2 * j2];
+                    vb[i] = kr[m.kv_rank + 2 * j2 + 1];
+                    cs[i] = s.rope_rows[(long long)row * half + j2];
                 }
             }
         }
-        float2 cs[kKvItems];  // ... then the RoPE table rows of the positions ...
-#pragma unroll
-        for (int i = 0; i < kKvItems; ++i) {
-            const int c = (threadIdx.x + 256 * i) % per_row;
-            cs[i] = slot[i] >= 0 && c >= m.kv_rank ? rope_cs(s, pos[i], 2 * (c - m.kv_rank))
-                                                   : float2{1.0f, 0.0f};
-        }
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < kKvItems; ++i) {  // ... then the rounded stores
+        for (int i = 0; i < kKvItems; ++i) {
             const int e = threadIdx.x + 256 * i, r = e / per_row, c = e % per_row;
             const int page = slot[i] / m.page_size, off = slot[i] % m.page_size;
             if (slot[i] < 0 || page >= s.num_pool_pages)
@@ -415,22 +383,24 @@ __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, ui
     // ---- one head: q_h over the head's tiles, 4 waves splitting K ----
     const int qk_tiles = m.qk_pad / 16, KTQ = m.q_pad / 32;
     const int kv_tiles = m.kv_pad / 16, KTU = m.nope_pad / 32;
+    inv_rms_to_lds(s.ss_q, m.q_pad / 16, m.q_rank, m.eps, row0, inv_s, 64);
     BPre<kQTiles, KWQ> bq;
     bq.load(L.w_uq, h * qk_tiles, qk_tiles, KTQ, wave, 4, lane);
     BPre<2, KWU> bu;  // this wave's two latent tiles of the absorption, whole K
     bu.load(L.w_uk + (long long)h * kv_tiles * KTU * 512, 2 * wave, min(2, kv_tiles - 2 * wave),
             KTU, 0, 1, lane);
-    ANorm32<KWQ> a;
-    a.load(s.cq + (long long)row0 * m.q_pad, m.q_pad, m.q_rank, KTQ, wave, 4, lane);
-    a.load_w(L.q_norm, m.q_rank, KTQ, wave, 4, lane);
-    inv_rms_to_lds(s.ss_q, m.q_pad / 16, m.q_rank, m.eps, row0, inv_s);
-    __syncthreads();
+    APre16<KWQ, 4> a;
+    a.load(s.cqw + (long long)row0 * m.q_pad, m.q_pad, KTQ, wave, 4, lane);
+    float2 cs[kRopeItems];  // RoPE rows of this thread's pairs
+#pragma unroll
+    for (int i = 0; i < kRopeItems; ++i) {
+        const int e = threadIdx.x + 256 * i, r = e / max(half, 1);
+        cs[i] = e < 64 * half ? s.rope_rows[(long long)(row0 + r) * half + e % half]
+                              : float2{1.0f, 0.0f};
+    }
     floatx4 acc[4][kQTiles];
     zero(acc);
-    mma_steps(acc, bq, [&](int kk, int mt) {
-        const float inv = inv_s[16 * mt + n];
-        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
-    });
+    mma_steps(acc, bq, [&](int kk, int mt) { return a.x[kk][mt]; });
     // reduce the 4 waves' partials: wave w finishes M-tile w, all of the head's tiles
     floatx4* part = reinterpret_cast<floatx4*>(smem);  // [4 waves][4 mt][kQTiles][64]
     float* qf = reinterpret_cast<float*>(smem);         // then q_h fp32 [64][qk_pad + 4]
@@ -454,8 +424,10 @@ __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, ui
     for (int j = 0; j < kQTiles; ++j)
         if (j < qk_tiles)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                qf[(16 * wave + 4 * g + i) * ldf + 16 * j + n] = q[j][i];
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * wave + 4 * g + i;
+                qf[r * ldf + 16 * j + n] = q[j][i] * inv_s[r];
+            }
     __syncthreads();
     // RoPE + q_rope; q_nope to the fp16 A tile of the absorption
     const int ldq = m.nope_pad + kLdsPad;
@@ -464,16 +436,16 @@ __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, ui
         const int r = e / m.nope_pad, c = e % m.nope_pad;
         q_s[r * ldq + c] = (_Float16)(c < m.nope ? qf[r * ldf + c] : 0.0f);
     }
-    const int half = m.rope / 2;
-    for (int e = threadIdx.x; e < 64 * half; e += 256) {
-        const int r = e / half, jp = 2 * (e % half), row = row0 + r;
-        if (row >= s.B)
-            break;
-        const float a0 = qf[r * ldf + m.nope + jp], a1 = qf[r * ldf + m.nope + jp + 1];
-        const float2 cs = rope_cs(s, s.positions[row], jp);
-        uint16_t* qr = s.q_rope + ((long long)row * m.H + h) * m.rope;
-        qr[jp] = F16::from_float(a0 * cs.x - a1 * cs.y);
-        qr[jp + 1] = F16::from_float(a0 * cs.y + a1 * cs.x);
+#pragma unroll
+    for (int i = 0; i < kRopeItems; ++i) {
+        const int e = threadIdx.x + 256 * i, r = e / max(half, 1), jp = 2 * (e % max(half, 1));
+        const int row = row0 + r;
+        if (e < 64 * half && row < s.B) {
+            const float a0 = qf[r * ldf + m.nope + jp], a1 = qf[r * ldf + m.nope + jp + 1];
+            uint16_t* qr = s.q_rope + ((long long)row * m.H + h) * m.rope;
+            qr[jp] = F16::from_float(a0 * cs[i].x - a1 * cs[i].y);
+            qr[jp + 1] = F16::from_float(a0 * cs[i].y + a1 * cs[i].x);
+        }
     }
     __syncthreads();
     // q_latent_h = q_h[:, :nope] . W_uk_h^T  (K = nope_pad, N = kv_pad; two tiles a wave)
@@ -503,66 +475,84 @@ __global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, ui
 }
 
 // ----------------------------------------------------------- g4 and g6 ----
-// out = A . W + residual for one 16-column tile per workgroup (8 waves split K), and
-// the per-tile sums of squares of `out` for the next RMSNorm.
+// y = A . W + residual for 16 rows and one 16-column tile (8 waves split K): y to `out`
+// (fp32), y o wnorm to `outw` (fp16, the next consumer's normalised A operand), and
+// y's per-tile sums of squares.  The residual and norm columns are fetched with the
+// operands.
 template <int KW, typename ALoad>
 __device__ __forceinline__ void splitk_residual(ALoad&& aload, const uint16_t* w, int KT, int N,
-                                                const float* residual, float* out, float* ss,
+                                                const float* residual, const float* wnorm,
+                                                float* out, uint16_t* outw, float* ss,
                                                 int n_tiles, int ld, int row0, int B) {
-    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * 64];
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int nt = blockIdx.x;
+    const int nt = blockIdx.x, col = nt * 16 + n;
     BPre<1, KW> bw;
     bw.load(w, nt, 1, KT, wave, kWaves, lane);
-    floatx4 acc[4][1];
+    floatx4 res = {0, 0, 0, 0};
+    float wn = 0.0f;
+    if (wave == 0 && col < N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            res[i] = residual[(long long)(row0 + 4 * g + i) * ld + col];
+        wn = wnorm[col];
+    }
+    floatx4 acc[1][1];
     zero(acc);
     aload(acc, bw, wave, lane);
-    int mt, j;
-    floatx4 v;
-    if (!splitk_sum<1, kWaves>(acc, part, mt, j, v))
+    int mt;
+    floatx4 v[1];
+    if (!splitk_reduce<1, 1, kWaves>(acc, part, mt, v))
         return;
-    const int col = nt * 16 + n, r0 = row0 + 16 * mt;
+    floatx4 y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const long long row = r0 + 4 * g + i;
-        v[i] = col < N ? v[i] + residual[row * ld + col] : 0.0f;
-        if (row < B && col < N)
-            out[row * ld + col] = v[i];
+        const long long row = row0 + 4 * g + i;
+        y[i] = col < N ? v[0][i] + res[i] : 0.0f;
+        if (row < B && col < N) {
+            out[row * ld + col] = y[i];
+            outw[row * ld + col] = F16::from_float(y[i] * wn);
+        }
     }
-    write_ss(v, col < N, ss, n_tiles, nt, r0, B);
+    write_ss(y, col < N, ss, n_tiles, nt, row0, B);
 }
 
 template <int KW>
 __global__ __launch_bounds__(64 * kWaves) void g4_kernel(StepArgs s, LayerWeights L) {
     const ModelDims& m = s.dims;
-    const int row0 = blockIdx.y * 64, ctx_w = m.H * m.kv_rank;  // attention rows: H*kv_rank
+    const int row0 = blockIdx.y * 16, ctx_w = m.H * m.kv_rank;  // attention rows: H*kv_rank
     const int KT = m.ctx_pad / 32;
     splitk_residual<KW>(
-        [&](floatx4(&acc)[4][1], const BPre<1, KW>& bw, int kt0, int lane) {
-            AHalf32<KW> a;
+        [&](floatx4(&acc)[1][1], const BPre<1, KW>& bw, int kt0, int lane) {
+            AHalf32<KW, 1> a;
             a.load(s.ctx + (long long)row0 * ctx_w, ctx_w, ctx_w, KT, kt0, kWaves, lane);
             mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
         },
-        L.w_out, KT, m.d_model, s.x, s.res, s.ss_res, m.d_pad / 16, m.d_pad, row0, s.B);
+        L.w_out, KT, m.d_model, s.x, L.ffn_norm, s.res, s.resw, s.ss_res, m.d_pad / 16, m.d_pad,
+        row0, s.B);
 }
 
+// next_norm: the norm weight of x's next consumer (attn_norm of the next layer, or
+// final_norm after the last layer).
 template <int KW>
-__global__ __launch_bounds__(64 * kWaves) void g6_kernel(StepArgs s, LayerWeights L) {
+__global__ __launch_bounds__(64 * kWaves) void g6_kernel(StepArgs s, LayerWeights L,
+                                                         const float* next_norm) {
     const ModelDims& m = s.dims;
-    const int row0 = blockIdx.y * 64, KT = m.ff_pad / 32;
+    const int row0 = blockIdx.y * 16, KT = m.ff_pad / 32;
     splitk_residual<KW>(
-        [&](floatx4(&acc)[4][1], const BPre<1, KW>& bw, int kt0, int lane) {
-            APre16<KW> a;
+        [&](floatx4(&acc)[1][1], const BPre<1, KW>& bw, int kt0, int lane) {
+            APre16<KW, 1> a;
             a.load(s.u + (long long)row0 * m.ff_pad, m.ff_pad, KT, kt0, kWaves, lane);
             mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
         },
-        L.w_down, KT, m.d_model, s.res, s.x, s.ss_x, m.d_pad / 16, m.d_pad, row0, s.B);
+        L.w_down, KT, m.d_model, s.res, next_norm, s.x, s.xw, s.ss_x, m.d_pad / 16, m.d_pad,
+        row0, s.B);
 }
 
 // --------------------------------------------------------------------- g5 ----
-// RMSNorm(res, ffn_norm) . [w_gate | w_up]: w_gate_up interleaves 16-column tiles of
-// gate and up (tile 2j = gate columns 16j.., tile 2j+1 = up columns 16j..); one pair per
-// workgroup, 8 waves split K, then SwiGLU (ops.cpp:65-77: gate * sigmoid(gate) * up).
+// RMSNorm(res, ffn_norm) . [w_gate | w_up] for 16 rows: w_gate_up interleaves 16-column
+// tiles of gate and up (tile 2j = gate columns 16j.., tile 2j+1 = up columns 16j..); one
+// pair per workgroup, 8 waves split K, then SwiGLU (ops.cpp:65-77: gate*sigmoid(gate)*up).
 __device__ __forceinline__ float silu_stable(float x) {
     if (x >= 0.0f)
         return x * (1.0f / (1.0f + expf(-x)));
@@ -572,86 +562,65 @@ __device__ __forceinline__ float silu_stable(float x) {
 
 template <int KW>
 __global__ __launch_bounds__(64 * kWaves) void g5_kernel(StepArgs s, LayerWeights L) {
-    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * 2 * 64];
-    __shared__ float inv_s[64];
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 2 * 64];
+    __shared__ float inv_s[16];
     const ModelDims& m = s.dims;
-    const int row0 = blockIdx.y * 64, p = blockIdx.x;
+    const int row0 = blockIdx.y * 16, p = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32;
+    inv_rms_to_lds(s.ss_res, m.d_pad / 16, m.d_model, m.eps, row0, inv_s, 16);
     BPre<2, KW> bw;
     bw.load(L.w_gate_up, 2 * p, 2, KT, wave, kWaves, lane);
-    ANorm32<KW> a;
-    a.load(s.res + (long long)row0 * m.d_pad, m.d_pad, m.d_model, KT, wave, kWaves, lane);
-    a.load_w(L.ffn_norm, m.d_model, KT, wave, kWaves, lane);
-    inv_rms_to_lds(s.ss_res, m.d_pad / 16, m.d_model, m.eps, row0, inv_s);
-    __syncthreads();
-    floatx4 acc[4][2];
+    APre16<KW, 1> a;
+    a.load(s.resw + (long long)row0 * m.d_pad, m.d_pad, KT, wave, kWaves, lane);
+    floatx4 acc[1][2];
     zero(acc);
-    mma_steps(acc, bw, [&](int kk, int mt) {
-        const float inv = inv_s[16 * mt + n];
-        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
-    });
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            part[((wave * 4 + mt) * 2 + j) * 64 + lane] = acc[mt][j];
-    __syncthreads();
-    if (wave >= 4)
+    mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
+    int mt;
+    floatx4 v[2];
+    if (!splitk_reduce<1, 2, kWaves>(acc, part, mt, v))
         return;
-    const int mt = wave, col = p * 16 + n;  // wave v finishes M-tile v, gate and up
-    floatx4 gt = {0, 0, 0, 0}, up = {0, 0, 0, 0};
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        gt += part[((w * 4 + mt) * 2 + 0) * 64 + lane];
-        up += part[((w * 4 + mt) * 2 + 1) * 64 + lane];
-    }
+    const int col = p * 16 + n;
     if (col < m.d_ff)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = row0 + 16 * mt + 4 * g + i;
+            const int row = row0 + 4 * g + i;
+            const float inv = inv_s[4 * g + i];
             if (row < s.B)
-                s.u[(long long)row * m.ff_pad + col] = F16::from_float(silu_stable(gt[i]) * up[i]);
+                s.u[(long long)row * m.ff_pad + col] =
+                    F16::from_float(silu_stable(v[0][i] * inv) * (v[1][i] * inv));
         }
 }
 
 // --------------------------------------------------------------------- g7 ----
-// Final RMSNorm + tied logits h . E^T, two 16-column tiles per workgroup (8 waves split
-// K); each workgroup also leaves, per row, the greedy winner of its 32 columns (strict
-// >, so the lowest index wins ties) and whether all of them were finite.
-constexpr int kG7Tiles = 2;
+// Final RMSNorm + tied logits h . E^T for 64 rows and four 16-column tiles per
+// workgroup (the waves split K four ways and the tiles two ways); each workgroup also
+// leaves, per row, the greedy winner of its 64 columns (strict >, so the lowest index
+// wins ties) and whether all of them were finite.
+constexpr int kG7Tiles = 4, kG7KG = 4;
 
 template <int KW>
 __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
-    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * kG7Tiles * 64];
+    constexpr int NTW = kG7Tiles / (kWaves / kG7KG);
+    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 4 * NTW * 64];
     __shared__ float inv_s[64];
     const ModelDims& m = s.dims;
     const int row0 = blockIdx.y * 64;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int KT = m.d_pad / 32;
+    const int KT = m.d_pad / 32, kg = wave % kG7KG, ng = wave / kG7KG;
     const int n_tiles = m.vocab_pad / 16, nt0 = blockIdx.x * kG7Tiles;
-    BPre<kG7Tiles, KW> bw;
-    bw.load(s.embed, nt0, min(kG7Tiles, n_tiles - nt0), KT, wave, kWaves, lane);
-    ANorm32<KW> a;
-    a.load(s.x + (long long)row0 * m.d_pad, m.d_pad, m.d_model, KT, wave, kWaves, lane);
-    a.load_w(s.final_norm, m.d_model, KT, wave, kWaves, lane);
-    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s);
-    __syncthreads();
-    floatx4 acc[4][kG7Tiles];
+    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s, 64);
+    BPre<NTW, KW> bw;
+    bw.load(s.embed, nt0 + ng * NTW, min(NTW, n_tiles - nt0 - ng * NTW), KT, kg, kG7KG, lane);
+    APre16<KW, 4> a;
+    a.load(s.xw + (long long)row0 * m.d_pad, m.d_pad, KT, kg, kG7KG, lane);
+    floatx4 acc[4][NTW];
     zero(acc);
-    mma_steps(acc, bw, [&](int kk, int mt) {
-        const float inv = inv_s[16 * mt + n];
-        return to_half8(a.x[kk][mt][0] * inv * a.w[kk][0], a.x[kk][mt][1] * inv * a.w[kk][1]);
-    });
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int j = 0; j < kG7Tiles; ++j)
-            part[((wave * 4 + mt) * kG7Tiles + j) * 64 + lane] = acc[mt][j];
-    __syncthreads();
-    if (wave >= 4)
+    mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
+    int mt;
+    floatx4 v[kG7Tiles];
+    if (!splitk_reduce<4, NTW, kG7KG>(acc, part, mt, v))
         return;
-    const int mt = wave;  // wave v finishes M-tile v over the workgroup's columns
     float bv[4], fin[4];
     int bc[4];
 #pragma unroll
@@ -662,21 +631,18 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
     }
 #pragma unroll
     for (int j = 0; j < kG7Tiles; ++j) {  // tiles in increasing column order
-        floatx4 v = {0, 0, 0, 0};
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w)
-            v += part[((w * 4 + mt) * kG7Tiles + j) * 64 + lane];
         const int col = (nt0 + j) * 16 + n;
         const bool valid = nt0 + j < n_tiles && col < m.vocab;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = row0 + 16 * mt + 4 * g + i;
+            const float y = v[j][i] * inv_s[16 * mt + 4 * g + i];
             if (valid && row < s.B)
-                s.logits[(long long)row * m.vocab + col] = v[i];
-            if (valid && !isfinite(v[i]))
+                s.logits[(long long)row * m.vocab + col] = y;
+            if (valid && !isfinite(y))
                 fin[i] = 0.0f;
-            if (valid && (bc[i] == 0x7fffffff || v[i] > bv[i])) {  // strict >: lowest column
-                bv[i] = v[i];
+            if (valid && (bc[i] == 0x7fffffff || y > bv[i])) {  // strict >: lowest column
+                bv[i] = y;
                 bc[i] = col;
             }
         }
@@ -704,38 +670,72 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
 }
 
 // Greedy token per row (inference.cpp:363-373 with no penalty or bans): the lowest
-// column among the maxima; -1 when a logit is not finite (numerical_error).
-__global__ __launch_bounds__(64) void argmax_kernel(StepArgs s, int parts) {
-    const int row = blockIdx.x;
-    float bv = -INFINITY;
-    int bc = 0x7fffffff, bad = 0;
-    for (int p = threadIdx.x; p < parts; p += 64) {  // parts cover increasing columns
-        const float v = s.arg_v[(long long)row * parts + p];
-        const int c = s.arg_c[(long long)row * parts + p];
-        if (c < 0)
-            bad = 1;
-        else if (c != 0x7fffffff && (bc == 0x7fffffff || v > bv)) {
-            bv = v;
-            bc = c;
+// column among the maxima; -1 when a logit is not finite (numerical_error).  256
+// threads load up to four partials each at once (parts <= 1024).
+constexpr int kArgItems = 4;
+
+__global__ __launch_bounds__(256) void argmax_kernel(StepArgs s, int parts) {
+    __shared__ float sv[4];
+    __shared__ int sc[4], sbad[4];
+    const int row = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float pv[kArgItems];
+    int pc[kArgItems];
+#pragma unroll
+    for (int i = 0; i < kArgItems; ++i) {
+        const int p = threadIdx.x + 256 * i;
+        pv[i] = -INFINITY;
+        pc[i] = 0x7fffffff;
+        if (p < parts) {
+            pv[i] = s.arg_v[(long long)row * parts + p];
+            pc[i] = s.arg_c[(long long)row * parts + p];
         }
     }
+    float bv = -INFINITY;
+    int bc = 0x7fffffff, bad = 0;
+#pragma unroll
+    for (int i = 0; i < kArgItems; ++i) {  // increasing columns
+        if (pc[i] < 0)
+            bad = 1;
+        else if (pc[i] != 0x7fffffff && (bc == 0x7fffffff || pv[i] > bv)) {
+            bv = pv[i];
+            bc = pc[i];
+        }
+    }
+    auto better = [](float ov, int oc, float v, int c) {
+        return oc != 0x7fffffff && (c == 0x7fffffff || ov > v || (ov == v && oc < c));
+    };
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(bv, off, 64);
         const int oc = __shfl_xor(bc, off, 64);
         bad |= __shfl_xor(bad, off, 64);
-        if (oc != 0x7fffffff && (bc == 0x7fffffff || ov > bv || (ov == bv && oc < bc))) {
+        if (better(ov, oc, bv, bc)) {
             bv = ov;
             bc = oc;
         }
     }
-    if (threadIdx.x == 0)
+    if (lane == 0) {
+        sv[wave] = bv;
+        sc[wave] = bc;
+        sbad[wave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            bad |= sbad[w];
+            if (better(sv[w], sc[w], bv, bc)) {
+                bv = sv[w];
+                bc = sc[w];
+            }
+        }
         s.next_tokens[row] = bad || bc == 0x7fffffff ? -1 : bc;
+    }
 }
 
 // k-steps per wave, rounded up to a compiled variant
 int kw_variant(int ksteps) {
     return ksteps <= 1 ? 1 : ksteps <= 2 ? 2 : ksteps <= 3 ? 3 : ksteps <= 4 ? 4 : ksteps <= 6 ? 6 : 8;
 }
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace
 
@@ -746,7 +746,7 @@ size_t g23_lds_bytes(const ModelDims& m) {
     return part > q ? part : q;
 }
 
-int g7_parts(const ModelDims& m) { return (m.vocab_pad / 16 + kG7Tiles - 1) / kG7Tiles; }
+int g7_parts(const ModelDims& m) { return ceil_div(m.vocab_pad / 16, kG7Tiles); }
 
 #define MLA_KW_DISPATCH(kw, KERNEL, ...)                                                        \
     switch (kw) {                                                                                \
@@ -757,7 +757,7 @@ int g7_parts(const ModelDims& m) { return (m.vocab_pad / 16 + kG7Tiles - 1) / kG
     case 6: hipLaunchKernelGGL(KERNEL<6>, __VA_ARGS__); break;                                   \
     default: hipLaunchKernelGGL(KERNEL<8>, __VA_ARGS__); break;                                  \
     }
-// Kernels that RMSNorm their A operand on the fly (K = d_model <= 1024: 4 k-steps a wave)
+// K = d_model <= 1024 over 8 K groups: at most 4 k-steps a wave
 #define MLA_KW4_DISPATCH(kw, KERNEL, ...)                                                       \
     switch (kw) {                                                                                \
     case 1: hipLaunchKernelGGL(KERNEL<1>, __VA_ARGS__); break;                                   \
@@ -780,22 +780,22 @@ hipError_t model_kernel_attributes() {
     return hipSuccess;
 }
 
-hipError_t launch_embed(const StepArgs& s, hipStream_t st) {
-    hipLaunchKernelGGL(embed_kernel, dim3(s.m_pad), dim3(256), 0, st, s);
+hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3(s.m_pad), dim3(256), 0, st, s, first_norm);
     return hipGetLastError();
 }
 
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
                             hipStream_t st) {
     const ModelDims& m = s.dims;
-    const int chunks = s.m_pad / 64;
-    MLA_KW4_DISPATCH(kw_variant((m.d_pad / 32 + kWaves - 1) / kWaves), g1_kernel,
-                    dim3((m.q_pad + m.kvw_pad) / 16, chunks), dim3(64 * kWaves), 0, st, s, w);
+    MLA_KW4_DISPATCH(kw_variant(ceil_div(m.d_pad / 32, kWaves)), g1_kernel,
+                     dim3((m.q_pad + m.kvw_pad) / 16, ceil_div(s.B, 16)), dim3(64 * kWaves), 0,
+                     st, s, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
     // q_pad <= 256: at most 2 k-steps of w_uq per wave; nope_pad <= 128: 4 of w_uk
-    const dim3 grid(m.H + kKvWGs, chunks);
+    const dim3 grid(m.H + kKvWGs, ceil_div(s.B, 64));
     const size_t lds = g23_lds_bytes(m);
     if (m.nope_pad / 32 <= 2)
         hipLaunchKernelGGL((g23_kernel<2, 2>), grid, dim3(256), lds, st, s, w, pool);
@@ -804,35 +804,35 @@ hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* 
     return hipGetLastError();
 }
 
-hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, hipStream_t st) {
+hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const float* next_norm,
+                             hipStream_t st) {
     const ModelDims& m = s.dims;
-    const int chunks = s.m_pad / 64;
-    const int d_tiles = m.d_pad / 16;
-    MLA_KW_DISPATCH(kw_variant((m.ctx_pad / 32 + kWaves - 1) / kWaves), g4_kernel,
+    const int chunks = ceil_div(s.B, 16), d_tiles = m.d_pad / 16;
+    MLA_KW_DISPATCH(kw_variant(ceil_div(m.ctx_pad / 32, kWaves)), g4_kernel,
                     dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    MLA_KW4_DISPATCH(kw_variant((m.d_pad / 32 + kWaves - 1) / kWaves), g5_kernel,
-                    dim3(m.ff_pad / 16, chunks), dim3(64 * kWaves), 0, st, s, w);
+    MLA_KW4_DISPATCH(kw_variant(ceil_div(m.d_pad / 32, kWaves)), g5_kernel,
+                     dim3(m.ff_pad / 16, chunks), dim3(64 * kWaves), 0, st, s, w);
     e = hipGetLastError();
     if (e != hipSuccess)
         return e;
-    MLA_KW_DISPATCH(kw_variant((m.ff_pad / 32 + kWaves - 1) / kWaves), g6_kernel,
-                    dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w);
+    MLA_KW_DISPATCH(kw_variant(ceil_div(m.ff_pad / 32, kWaves)), g6_kernel,
+                    dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w, next_norm);
     return hipGetLastError();
 }
 
 hipError_t launch_logits(const StepArgs& s, hipStream_t st) {
     const ModelDims& m = s.dims;
     const int parts = g7_parts(m);
-    MLA_KW4_DISPATCH(kw_variant((m.d_pad / 32 + kWaves - 1) / kWaves), g7_kernel,
-                    dim3(parts, s.m_pad / 64), dim3(64 * kWaves), 0, st, s);
+    MLA_KW_DISPATCH(kw_variant(ceil_div(m.d_pad / 32, kG7KG)), g7_kernel,
+                    dim3(parts, ceil_div(s.B, 64)), dim3(64 * kWaves), 0, st, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return e;
     if (s.B > 0)
-        hipLaunchKernelGGL(argmax_kernel, dim3(s.B), dim3(64), 0, st, s, parts);
+        hipLaunchKernelGGL(argmax_kernel, dim3(s.B), dim3(256), 0, st, s, parts);
     return hipGetLastError();
 }
 

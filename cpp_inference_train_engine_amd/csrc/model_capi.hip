@@ -118,9 +118,10 @@ struct Model {
     const uint16_t* embed = nullptr;
     const float* final_norm = nullptr;
     const float* rope_tab = nullptr;
-    float *x, *res, *cq, *ctx, *kvraw, *logits, *arg_v;
+    float *x, *res, *ctx, *kvraw, *logits, *arg_v;
     float *ss_x, *ss_res, *ss_q, *ss_kv;
-    uint16_t *u, *q_latent, *q_rope;
+    float2* rope_rows;
+    uint16_t *xw, *resw, *cqw, *u, *q_latent, *q_rope;
     int32_t* arg_c;
 
     ~Model() {
@@ -315,7 +316,10 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
     const size_t rows = M->m_pad_max;
     if (e == hipSuccess) e = M->alloc(M->x, rows * m.d_pad);
     if (e == hipSuccess) e = M->alloc(M->res, rows * m.d_pad);
-    if (e == hipSuccess) e = M->alloc(M->cq, rows * m.q_pad);
+    if (e == hipSuccess) e = M->alloc(M->xw, rows * m.d_pad);
+    if (e == hipSuccess) e = M->alloc(M->resw, rows * m.d_pad);
+    if (e == hipSuccess) e = M->alloc(M->cqw, rows * m.q_pad);
+    if (e == hipSuccess) e = M->alloc(M->rope_rows, rows * (size_t)(c.head_dim_rope / 2));
     if (e == hipSuccess) e = M->alloc(M->ctx, rows * (size_t)H * kv);
     if (e == hipSuccess) e = M->alloc(M->kvraw, rows * m.kvw_pad);
     if (e == hipSuccess) e = M->alloc(M->u, rows * m.ff_pad);
@@ -378,7 +382,10 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
     s.rope_tab = reinterpret_cast<const float2*>(M->rope_tab);
     s.x = M->x;
     s.res = M->res;
-    s.cq = M->cq;
+    s.xw = M->xw;
+    s.resw = M->resw;
+    s.cqw = M->cqw;
+    s.rope_rows = M->rope_rows;
     s.ctx = M->ctx;
     s.kvraw = M->kvraw;
     s.u = M->u;
@@ -416,8 +423,9 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
     a.part_o = static_cast<float*>(workspace);
     a.part_ml = a.part_o + (size_t)max_work * m.H * m.kv_rank;
     const bool generic = (reinterpret_cast<uintptr_t>(workspace) & 15) != 0;
-    hipError_t e = launch_embed(s, st);
+    hipError_t e = launch_embed(s, M->layers[0].attn_norm, st);
     for (int l = 0; l < m.n_layers && e == hipSuccess; ++l) {
+        const float* next_norm = l + 1 < m.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
         uint16_t* pool = static_cast<uint16_t*>(pages[l]);
         e = launch_layer_pre(s, M->layers[l], pool, st);
         if (e != hipSuccess)
@@ -427,7 +435,7 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
         if (e == hipSuccess)
             e = launch_merge(a, st);
         if (e == hipSuccess)
-            e = launch_layer_post(s, M->layers[l], st);
+            e = launch_layer_post(s, M->layers[l], next_norm, st);
     }
     if (e == hipSuccess)
         e = launch_logits(s, st);
