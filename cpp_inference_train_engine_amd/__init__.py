@@ -52,6 +52,9 @@ _SIGNATURES = {
                              C.c_int]),
     "mla_decode_merge": (C.c_int, [C.c_void_p] + [C.c_int] * 3 + [C.c_void_p] * 4 +
                          [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    "mla_prefill_attention": (C.c_int, [C.c_void_p] + [C.c_int] * 6 + [C.c_float] +
+                              [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_void_p] * 4 +
+                              [C.c_int, C.c_void_p, C.c_void_p, C.c_int]),
     "mla_config_validate": (C.c_int, [C.c_void_p]),
     "mla_config_parameter_count": (C.c_size_t, [C.c_void_p]),
     "mla_model_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_int,
@@ -106,12 +109,12 @@ def stream_handle(stream=None) -> int | None:
 
 from .ops import (  # noqa: E402  (re-exported operator interface)
     PagedLatentCache, RaggedBatch, append_latent, build_metadata, decode_attention,
-    decode_merge, decode_partials, decode_workspace, decode_workspace_bytes)
+    decode_merge, decode_partials, decode_workspace, decode_workspace_bytes, prefill_attention)
 
 from .model import HipModel, ModelConfig, config_parameter_count, config_validate  # noqa: E402
 
 __all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
-           "decode_partials", "decode_merge", "HipModel", "ModelConfig", "config_validate",
+           "decode_partials", "decode_merge", "prefill_attention", "HipModel", "ModelConfig", "config_validate",
            "config_parameter_count",
            "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",
            "DTYPE_BF16"]

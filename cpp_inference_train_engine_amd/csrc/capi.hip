@@ -238,4 +238,49 @@ int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_
     return gpu_status(launch_merge(a, static_cast<hipStream_t>(stream)), "mla_decode_merge");
 }
 
+int mla_prefill_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
+                          int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
+                          const int32_t* cu_seqlens_k, const int32_t* page_table, int max_pages,
+                          int num_pool_pages, const void* pages, const void* q_latent,
+                          const void* q_rope, const int32_t* info, int max_q_len, float* out,
+                          float* lse, int flags) {
+    if (B < 0 || B > 65535 || n_heads < 1 || n_heads > 65535 || kv_rank < 1 || kv_rank > 1024 ||
+        rope_dim < 0 || rope_dim > 1024 || page_size < 1 || max_pages < 0 ||
+        num_pool_pages < 0 || max_q_len < 0 ||
+        (dtype != MLA_DTYPE_F16 && dtype != MLA_DTYPE_BF16) || !(scale > 0.0f))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_prefill_attention: invalid argument");
+    if (B == 0 || max_q_len < 2)
+        return MLA_OK;
+    if (!cu_seqlens_q || !cu_seqlens_k || !page_table || !pages || !q_latent ||
+        (rope_dim > 0 && !q_rope) || !info || !out)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_prefill_attention: null buffer");
+    PrefillArgs a{};
+    a.B = B;
+    a.H = n_heads;
+    a.kv_rank = kv_rank;
+    a.rope_dim = rope_dim;
+    a.page_size = page_size;
+    a.max_pages = max_pages;
+    a.num_pool_pages = num_pool_pages;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.cu_q = cu_seqlens_q;
+    a.cu_k = cu_seqlens_k;
+    a.page_table = page_table;
+    a.info = info;
+    a.pages = static_cast<const uint16_t*>(pages);
+    a.q_latent = static_cast<const uint16_t*>(q_latent);
+    a.q_rope = static_cast<const uint16_t*>(q_rope);
+    a.out = out;
+    a.lse = lse;
+    // The MFMA kernel issues 16-byte loads of q and cache chunks and 16-byte stores.
+    const bool aligned =
+        ((reinterpret_cast<uintptr_t>(pages) | reinterpret_cast<uintptr_t>(q_latent) |
+          reinterpret_cast<uintptr_t>(q_rope) | reinterpret_cast<uintptr_t>(out)) &
+         15) == 0;
+    return gpu_status(launch_prefill(a, max_q_len, dtype,
+                                     (flags & MLA_DECODE_FORCE_GENERIC) || !aligned,
+                                     static_cast<hipStream_t>(stream)),
+                      "mla_prefill_attention");
+}
+
 }  // extern "C"

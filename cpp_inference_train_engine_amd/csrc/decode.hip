@@ -218,7 +218,7 @@ void decode_page_kernel(DecodeArgs a) {
                 acc[r] *= alpha;
             m_run = m_new;
         }
-        V8 pb[UPP];
+        V8 pb[UPP], pl[UPP];  // P^T operands (pl: the low part, bf16 only)
         float psum = 0.0f;
 #pragma unroll
         for (int t = 0; t < TT; ++t)
@@ -226,7 +226,11 @@ void decode_page_kernel(DecodeArgs a) {
             for (int i = 0; i < 4; ++i) {
                 const float e = exp2_fast(sc[t][i] - m_run);
                 psum += e;
-                pb[t / 2][4 * (t % 2) + i] = static_cast<typename T::scalar>(e);
+                const auto hi = static_cast<typename T::scalar>(e);
+                pb[t / 2][4 * (t % 2) + i] = hi;
+                if constexpr (T::split_p)
+                    pl[t / 2][4 * (t % 2) + i] =
+                        static_cast<typename T::scalar>(e - static_cast<float>(hi));
             }
         l_run += psum;
 #pragma unroll
@@ -245,8 +249,10 @@ void decode_page_kernel(DecodeArgs a) {
             for (int rt = 0; rt < RT; ++rt) {
                 const u32x2 lo = lds_read_tr16(src + 16 * rt);
                 const u32x2 hi = lds_read_tr16(src + 16 * UP + 16 * rt);
-                acc[rt] = T::mma32(__builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb[u],
-                                   acc[rt]);
+                const V8 ca = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                acc[rt] = T::mma32(ca, pb[u], acc[rt]);
+                if constexpr (T::split_p)
+                    acc[rt] = T::mma32(ca, pl[u], acc[rt]);
             }
             wave_lds_fence();
         }

@@ -26,6 +26,8 @@ struct F16 {
     using vec8 = half8;
     using vec4 = half4;
     static constexpr int code = 0;
+    // Softmax probabilities enter the P.C MFMA as one fp16 operand (2^-11 relative).
+    static constexpr bool split_p = false;
     __device__ static float to_float(uint16_t bits) {
         return static_cast<float>(__builtin_bit_cast(_Float16, bits));
     }
@@ -45,6 +47,9 @@ struct BF16 {
     using vec8 = bf8;
     using vec4 = bf4;
     static constexpr int code = 1;
+    // bf16 keeps 8 mantissa bits: probabilities enter the P.C MFMA as hi + lo bf16
+    // parts (two MFMAs, about 16 bits), so the output stays within the fp32 tolerance.
+    static constexpr bool split_p = true;
     __device__ static float to_float(uint16_t bits) {
         return __builtin_bit_cast(float, static_cast<uint32_t>(bits) << 16);
     }

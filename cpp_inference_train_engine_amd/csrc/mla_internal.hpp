@@ -43,6 +43,15 @@ struct DecodeArgs {
     float *out, *lse, *part_o, *part_ml;
 };
 
+// Chunked-prefill attention (sessions with q_len > 1, causal within the chunk).
+struct PrefillArgs {
+    int B, H, kv_rank, rope_dim, page_size, max_pages, num_pool_pages;
+    float scale_log2;  // softmax scale * log2(e)
+    const int32_t *cu_q, *cu_k, *page_table, *info;
+    const uint16_t *pages, *q_latent, *q_rope;
+    float *out, *lse;
+};
+
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
 hipError_t launch_append(const AppendArgs& a, int dtype, hipStream_t stream);
 // Decode kernel only (MFMA page kernel, or the generic one when force_generic or the
@@ -52,5 +61,9 @@ hipError_t launch_decode_partials(const DecodeArgs& a, int dtype, bool force_gen
 // Log-sum-exp merge of the partials into the rows of split sessions.
 hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream);
 bool decode_mfma_supported(int H, int kv_rank, int rope_dim, int page_size);
+// Prefill attention for the sessions with q_len > 1 (max_q_len >= their q_len).
+hipError_t launch_prefill(const PrefillArgs& a, int max_q_len, int dtype, bool force_generic,
+                          hipStream_t stream);
+bool prefill_mfma_supported(int H, int kv_rank, int rope_dim, int page_size);
 
 }  // namespace mla

@@ -178,9 +178,29 @@ def decode_merge(batch: RaggedBatch, n_heads: int, kv_rank: int, out, workspace,
     return out
 
 
+def prefill_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
+                      kv_rank: int, rope_dim: int, max_q_len: int, dtype: int = DTYPE_F16,
+                      out=None, lse=None, flags: int = 0, stream=None):
+    """(c) Absorbed MLA chunked-prefill attention for every session with q_len > 1: query
+    row i of a session attends causally to its keys [0, ctx + i].  The chunk's latent
+    rows must already be in ``pages``.  q_latent [rows, H, kv_rank], q_rope
+    [rows, H, rope_dim] in the cache dtype; returns out [rows, H, kv_rank] fp32 (rows of
+    sessions with q_len <= 1 are left as they were)."""
+    torch = _torch()
+    rows, H = int(q_latent.shape[0]), int(q_latent.shape[1])
+    if out is None:
+        out = torch.zeros((rows, H, kv_rank), dtype=torch.float32, device=q_latent.device)
+    check(lib().mla_prefill_attention(
+        stream_handle(stream), batch.B, H, kv_rank, rope_dim, batch.page_size, dtype,
+        float(scale), ptr(batch.cu_seqlens_q), ptr(batch.cu_seqlens_k), ptr(batch.page_table),
+        batch.max_pages, batch.num_pool_pages, ptr(pages), ptr(q_latent), ptr(q_rope),
+        ptr(batch.info), int(max_q_len), ptr(out), ptr(lse), flags))
+    return out
+
+
 __all__ = ["RaggedBatch", "build_metadata", "PagedLatentCache", "append_latent",
            "decode_workspace_bytes", "decode_workspace", "decode_attention", "decode_partials",
-           "decode_merge", "DTYPE_F16", "DTYPE_BF16"]
+           "decode_merge", "prefill_attention", "DTYPE_F16", "DTYPE_BF16"]
 
 
 # ---------------------------------------------------------------- page layout ----

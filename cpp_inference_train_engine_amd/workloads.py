@@ -54,7 +54,9 @@ def to_bits(x: np.ndarray, dtype: int) -> np.ndarray:
 
 @dataclass
 class DecodeBatch:
-    """One ragged decode step: every session appends one token (q_len = 1)."""
+    """One ragged step: session b has ctx_len[b] cached tokens and appends q_len[b]
+    (1 for a decode session, a chunk for a prefill session); query rows are packed in
+    session order (rows = q_len.sum())."""
 
     ctx_len: np.ndarray   # int32 [B] tokens already cached
     q_len: np.ndarray     # int32 [B]
@@ -63,8 +65,8 @@ class DecodeBatch:
     num_pages: int        # pool size
     max_pages: int
     pages: np.ndarray     # uint16 [L, num_pages, page_size*(kv+rope)]
-    q_latent: np.ndarray  # uint16 [B, H, kv]
-    q_rope: np.ndarray    # uint16 [B, H, rope]
+    q_latent: np.ndarray  # uint16 [rows, H, kv]
+    q_rope: np.ndarray    # uint16 [rows, H, rope]
     page_size: int
     kv_rank: int
     rope_dim: int
@@ -112,6 +114,66 @@ def ragged_decode_batch(B=64, min_len=128, max_len=4096, page_size=64, n_heads=8
     return DecodeBatch(ctx_len=(k_len - 1).astype(np.int32), q_len=np.ones(B, np.int32),
                        cu_pages=cu_pages, page_ids=page_ids, num_pages=P,
                        max_pages=int(counts.max()), pages=pages, q_latent=q_latent,
+                       q_rope=q_rope, page_size=page_size, kv_rank=kv_rank, rope_dim=rope_dim,
+                       n_heads=n_heads, dtype=dtype)
+
+
+def mixed_prefill_batch(n_prefill=8, chunk=512, max_prefill_ctx=2048, n_decode=120,
+                        median_len=2048, sigma=1.0, max_len=16384, prefix_tokens=256,
+                        n_share=None, page_size=64, n_heads=8, kv_rank=128, rope_dim=16,
+                        n_layers=1, dtype=0, seed=0) -> DecodeBatch:
+    """Config-4-style mixed batch: ``n_prefill`` chunks of ``chunk`` tokens appended
+    (causal within the chunk) to contexts uniform in [0, max_prefill_ctx], then
+    ``n_decode`` decode sessions whose lengths (after the append) are log-normal with
+    median ``median_len`` and shape ``sigma``, capped at ``max_len``.  Half of the
+    sessions (``n_share``) share the first ``prefix_tokens`` tokens through aliased
+    page ids: the first sessions, in order, whose cached context covers the whole
+    prefix (a session never appends into a shared page).  Page ids are a Fisher-Yates
+    permutation of the pool (reference Rng); contents N(0, 1) rounded once."""
+    rng = SplitMix64(seed)
+    gen = np.random.default_rng(seed)
+    B = n_prefill + n_decode
+    ctx = np.zeros(B, np.int64)
+    q = np.ones(B, np.int64)
+    for b in range(n_prefill):
+        ctx[b] = rng.bounded(max_prefill_ctx + 1)
+        q[b] = chunk
+    lens = np.minimum(np.maximum(np.rint(gen.lognormal(np.log(median_len), sigma, n_decode)), 1),
+                      max_len).astype(np.int64)
+    ctx[n_prefill:] = lens - 1
+    k_len = ctx + q
+    share_pages = prefix_tokens // page_size
+    if n_share is None:
+        n_share = B // 2
+    sharers = [b for b in range(B) if ctx[b] >= share_pages * page_size][:n_share]
+    shared = np.zeros(B, bool)
+    shared[sharers] = share_pages > 0
+    need = (k_len + page_size - 1) // page_size
+    own = need - np.where(shared, share_pages, 0)
+    P = int(own.sum()) + (share_pages if shared.any() else 0)
+    perm = list(range(P))
+    for i in range(P - 1, 0, -1):  # Fisher-Yates with the reference Rng
+        j = rng.bounded(i + 1)
+        perm[i], perm[j] = perm[j], perm[i]
+    pool = iter(perm)
+    prefix_ids = [next(pool) for _ in range(share_pages)] if shared.any() else []
+    lists = []
+    for b in range(B):
+        lst = list(prefix_ids) if shared[b] else []
+        lst += [next(pool) for _ in range(int(own[b]))]
+        lists.append(lst)
+    page_ids = np.array([p for lst in lists for p in lst], np.int32)
+    cu_pages = np.concatenate([[0], np.cumsum([len(x) for x in lists])]).astype(np.int32)
+    rec = page_size * (kv_rank + rope_dim)
+    pages = np.empty((n_layers, P, rec), np.uint16)
+    for l in range(n_layers):
+        pages[l] = to_bits(gen.standard_normal((P, rec), dtype=np.float32), dtype)
+    rows = int(q.sum())
+    q_latent = to_bits(gen.standard_normal((rows, n_heads, kv_rank), dtype=np.float32), dtype)
+    q_rope = to_bits(gen.standard_normal((rows, n_heads, rope_dim), dtype=np.float32), dtype)
+    return DecodeBatch(ctx_len=ctx.astype(np.int32), q_len=q.astype(np.int32),
+                       cu_pages=cu_pages, page_ids=page_ids, num_pages=P,
+                       max_pages=int(need.max()) if B else 0, pages=pages, q_latent=q_latent,
                        q_rope=q_rope, page_size=page_size, kv_rank=kv_rank, rope_dim=rope_dim,
                        n_heads=n_heads, dtype=dtype)
 

@@ -179,6 +179,32 @@ int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_
                      int max_work, float* out, float* lse, const void* workspace,
                      size_t workspace_bytes);
 
+/* ------------------------------------------------------------------ (c)
+ * Absorbed MLA chunked-prefill attention over the paged cache, for every session
+ * with q_len > 1 in the batch.  Session b appended q_len tokens at positions
+ * ctx .. ctx+q_len-1 (ctx = k_len - q_len, k_len = cu_seqlens_k[b+1] -
+ * cu_seqlens_k[b]); its query row i attends causally to keys [0, ctx + i]:
+ *     s_j = (q_latent[i,h] . c_j + q_rope[i,h] . k_j) * scale,  j <= ctx + i
+ *     out[i,h] = sum_j softmax(s)_j c_j,   lse[i,h] = ln(sum_j exp(s_j))
+ * i.e. the causal attention of the reference's full forward (src/model/ops.cpp:
+ * 109-142, via Model::forward, src/model/model.cpp:76-155, which is what
+ * CpuDecoder::prefill runs, src/infer/inference.cpp:47-68) in the absorbed form
+ * of inference.cpp:116-153, restricted to rows ctx.. of the sequence: the
+ * reference has no chunked prefill onto an existing context; causality
+ * (tests/test_model.cpp:65-77) makes those rows equal.  The chunk's own latent
+ * rows must already be appended (mla_append_latent with the metadata's
+ * slot_mapping).  Arguments as for mla_decode_attention, plus cu_seqlens_k from
+ * the same mla_build_metadata call and max_q_len >= every session's q_len (rows
+ * of a longer session past max_q_len are not written).  Rows of sessions with
+ * q_len <= 1 are not written (mla_decode_attention covers them).  flags:
+ * MLA_DECODE_FORCE_GENERIC selects the portable VALU kernel.  No workspace. */
+int mla_prefill_attention(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
+                          int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
+                          const int32_t* cu_seqlens_k, const int32_t* page_table, int max_pages,
+                          int num_pool_pages, const void* pages, const void* q_latent,
+                          const void* q_rope, const int32_t* info, int max_q_len, float* out,
+                          float* lse, int flags);
+
 /* ------------------------------------------------------------------ model
  * The batched decode step around the attention: everything of
  * CpuDecoder::decode (src/infer/inference.cpp:76-173) for B sessions at once,
