@@ -64,6 +64,21 @@ _SIGNATURES = {
                        [C.c_int, C.c_int] + [C.c_void_p] * 6 + [C.c_int] +
                        [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
     "mla_model_logits": (C.c_void_p, [C.c_void_p]),
+    "mla_model_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
+                                    C.c_int, C.c_int] + [C.c_void_p] * 3 + [C.c_int, C.c_int] +
+                          [C.c_void_p] * 6 + [C.c_int] +
+                          [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "mla_engine_create": (C.c_int, [C.c_void_p, C.c_void_p] + [C.c_int] * 4 +
+                          [C.POINTER(C.c_void_p)]),
+    "mla_engine_destroy": (C.c_int, [C.c_void_p]),
+    "mla_engine_info": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "mla_session_create": (C.c_int, [C.c_void_p, C.POINTER(C.c_int)]),
+    "mla_session_fork": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
+    "mla_session_release": (C.c_int, [C.c_void_p, C.c_int]),
+    "mla_session_length": (C.c_int, [C.c_void_p, C.c_int, C.POINTER(C.c_int)]),
+    "mla_session_prefill": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
+    "mla_session_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_uint16, C.c_void_p]),
+    "mla_engine_step": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 5),
 }
 
 
@@ -112,9 +127,10 @@ from .ops import (  # noqa: E402  (re-exported operator interface)
     decode_merge, decode_partials, decode_workspace, decode_workspace_bytes, prefill_attention)
 
 from .model import HipModel, ModelConfig, config_parameter_count, config_validate  # noqa: E402
+from .engine import HipEngine, HipExecution, generate_tokens  # noqa: E402
 
 __all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
-           "decode_partials", "decode_merge", "prefill_attention", "HipModel", "ModelConfig", "config_validate",
+           "decode_partials", "decode_merge", "prefill_attention", "HipModel", "HipEngine", "HipExecution", "generate_tokens", "ModelConfig", "config_validate",
            "config_parameter_count",
            "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",
            "DTYPE_BF16"]

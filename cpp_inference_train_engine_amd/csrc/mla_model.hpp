@@ -11,6 +11,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "mla_hip.h"
+
 #include <cstddef>
 #include <cstdint>
 
@@ -85,5 +87,29 @@ hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* 
 hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const float* next_norm,
                              hipStream_t st);
 hipError_t launch_logits(const StepArgs& s, hipStream_t st);
+// Row b < B of (xw_out, ss_out) = row cu_q[b+1]-1 of (s.xw, s.ss_x) for the B sessions
+// of cu_q; rows [B, round_up(B, 64)) are zeroed.  s describes the forward's rows.
+hipError_t launch_gather_last(const StepArgs& s, int B, const int32_t* cu_q, uint16_t* xw_out,
+                              float* ss_out, hipStream_t st);
+
+// Device metadata of one mla_build_metadata call.
+struct MetaPtrs {
+    const int32_t *cu_seqlens_q, *cu_seqlens_k, *page_table, *slot_mapping, *num_splits,
+        *cu_splits, *work_desc, *work_pages, *info;
+    int max_pages, num_pool_pages, max_work;
+};
+struct Model;  // model_capi.hip
+// One forward of `rows` new tokens belonging to B sessions (row order = session order,
+// q_len = cu_q[b+1] - cu_q[b] >= 1, max_q_len the largest): per layer the projections,
+// the paged append, decode attention for q_len == 1 sessions and chunked-prefill
+// attention for the others, the FFN; then logits and the greedy token of each
+// session's LAST row into logits [B x vocab] / next_tokens [B].  When every session
+// has q_len == 1 (rows == B) the rows are the sessions.  Returns an MLA status.
+int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
+                  const int32_t* positions, int B, int max_q_len, const MetaPtrs& md,
+                  void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
+                  int32_t* next_tokens);
+int model_max_rows(const Model* M);
+const mla_model_config& model_config(const Model* M);
 
 }  // namespace mla

@@ -669,6 +669,21 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
     }
 }
 
+// Last row of each session (cu_q[b+1] - 1) to row b of the logits operands: the
+// normalised activation xw (fp16) and its per-tile sums of squares.  The reference
+// returns the logits of a prefill's last position only (inference.cpp:64-66).  Rows
+// [B, m_pad) are zeroed.
+__global__ __launch_bounds__(256) void gather_last_kernel(StepArgs s, int B, const int32_t* cu_q,
+                                                          uint16_t* xw_out, float* ss_out) {
+    const ModelDims& m = s.dims;
+    const int b = blockIdx.x, d_tiles = m.d_pad / 16;
+    const int src = b < B ? cu_q[b + 1] - 1 : -1;
+    for (int c = threadIdx.x; c < m.d_pad; c += 256)
+        xw_out[(long long)b * m.d_pad + c] = src >= 0 ? s.xw[(long long)src * m.d_pad + c] : 0;
+    for (int c = threadIdx.x; c < d_tiles; c += 256)
+        ss_out[(long long)b * d_tiles + c] = src >= 0 ? s.ss_x[(long long)src * d_tiles + c] : 0.0f;
+}
+
 // Greedy token per row (inference.cpp:363-373 with no penalty or bans): the lowest
 // column among the maxima; -1 when a logit is not finite (numerical_error).  256
 // threads load up to four partials each at once (parts <= 1024).
@@ -820,6 +835,13 @@ hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const flo
         return e;
     MLA_KW_DISPATCH(kw_variant(ceil_div(m.ff_pad / 32, kWaves)), g6_kernel,
                     dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w, next_norm);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_last(const StepArgs& s, int B, const int32_t* cu_q, uint16_t* xw_out,
+                              float* ss_out, hipStream_t st) {
+    hipLaunchKernelGGL(gather_last_kernel, dim3((B + 63) / 64 * 64), dim3(256), 0, st, s, B, cu_q,
+                       xw_out, ss_out);
     return hipGetLastError();
 }
 

@@ -109,6 +109,8 @@ Registry view(const mla_model_config& c, const float* p) {
     return r;
 }
 
+}  // namespace
+
 struct Model {
     mla_model_config cfg;
     ModelDims dims;
@@ -149,6 +151,8 @@ struct Model {
     }
 };
 
+namespace {
+
 ModelDims make_dims(const mla_model_config& c, int page_size) {
     ModelDims m{};
     m.vocab = c.vocab_size;
@@ -179,6 +183,137 @@ ModelDims make_dims(const mla_model_config& c, int page_size) {
 }
 
 }  // namespace
+
+int model_max_rows(const Model* M) { return M->max_batch; }
+const mla_model_config& model_config(const Model* M) { return M->cfg; }
+
+int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
+                  const int32_t* positions, int B, int max_q_len, const MetaPtrs& md,
+                  void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
+                  int32_t* next_tokens) {
+    if (!M || rows < 0 || rows > M->max_batch || B < 0 || B > rows || max_q_len < 1 ||
+        max_q_len > rows + (rows == 0) || md.max_work < 0 || md.max_work > kMaxWork ||
+        md.max_pages < 0 || md.num_pool_pages < 0 || (rows == B) != (max_q_len == 1))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "model forward: invalid argument");
+    if (rows == 0)
+        return MLA_OK;
+    if (!tokens || !positions || !md.cu_seqlens_q || !md.page_table || !md.slot_mapping ||
+        !md.num_splits || !md.cu_splits || !md.work_desc || !md.work_pages || !md.info ||
+        !pages || !next_tokens || (max_q_len > 1 && !md.cu_seqlens_k))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "model forward: null buffer");
+    for (int l = 0; l < M->cfg.n_layers; ++l)
+        if (!pages[l])
+            return fail(MLA_ERR_INVALID_ARGUMENT, "model forward: null page pool");
+    const ModelDims& m = M->dims;
+    const size_t need = mla_decode_workspace_bytes(md.max_work, B, m.H, m.kv_rank);
+    if (!workspace || workspace_bytes < need)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "model forward: workspace needs " + std::to_string(need) + " bytes");
+    StepArgs s{};
+    s.dims = m;
+    s.B = rows;
+    s.m_pad = round_up(rows, 64);
+    s.tokens = tokens;
+    s.positions = positions;
+    s.slot_mapping = md.slot_mapping;
+    s.num_pool_pages = md.num_pool_pages;
+    s.embed = M->embed;
+    s.final_norm = M->final_norm;
+    s.rope_tab = reinterpret_cast<const float2*>(M->rope_tab);
+    s.x = M->x;
+    s.res = M->res;
+    s.xw = M->xw;
+    s.resw = M->resw;
+    s.cqw = M->cqw;
+    s.rope_rows = M->rope_rows;
+    s.ctx = M->ctx;
+    s.kvraw = M->kvraw;
+    s.u = M->u;
+    s.q_latent = M->q_latent;
+    s.q_rope = M->q_rope;
+    s.logits = logits ? logits : M->logits;
+    s.arg_v = M->arg_v;
+    s.arg_c = M->arg_c;
+    s.next_tokens = next_tokens;
+    s.ss_x = M->ss_x;
+    s.ss_res = M->ss_res;
+    s.ss_q = M->ss_q;
+    s.ss_kv = M->ss_kv;
+    DecodeArgs a{};
+    a.B = B;
+    a.H = m.H;
+    a.kv_rank = m.kv_rank;
+    a.rope_dim = m.rope;
+    a.page_size = m.page_size;
+    a.max_pages = md.max_pages;
+    a.num_pool_pages = md.num_pool_pages;
+    a.max_work = md.max_work;
+    a.scale_log2 = 1.4426950408889634f / std::sqrt((float)m.qk);  // inference.cpp:133
+    a.cu_q = md.cu_seqlens_q;
+    a.page_table = md.page_table;
+    a.num_splits = md.num_splits;
+    a.cu_splits = md.cu_splits;
+    a.work_desc = md.work_desc;
+    a.work_pages = md.work_pages;
+    a.info = md.info;
+    a.q_latent = M->q_latent;
+    a.q_rope = M->q_rope;
+    a.out = M->ctx;
+    a.lse = nullptr;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_ml = a.part_o + (size_t)md.max_work * m.H * m.kv_rank;
+    PrefillArgs pa{};
+    pa.B = B;
+    pa.H = m.H;
+    pa.kv_rank = m.kv_rank;
+    pa.rope_dim = m.rope;
+    pa.page_size = m.page_size;
+    pa.max_pages = md.max_pages;
+    pa.num_pool_pages = md.num_pool_pages;
+    pa.scale_log2 = a.scale_log2;
+    pa.cu_q = md.cu_seqlens_q;
+    pa.cu_k = md.cu_seqlens_k;
+    pa.page_table = md.page_table;
+    pa.info = md.info;
+    pa.q_latent = M->q_latent;
+    pa.q_rope = M->q_rope;
+    pa.out = M->ctx;
+    pa.lse = nullptr;
+    const bool generic = (reinterpret_cast<uintptr_t>(workspace) & 15) != 0;
+    hipError_t e = launch_embed(s, M->layers[0].attn_norm, st);
+    for (int l = 0; l < m.n_layers && e == hipSuccess; ++l) {
+        const float* next_norm = l + 1 < m.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
+        uint16_t* pool = static_cast<uint16_t*>(pages[l]);
+        e = launch_layer_pre(s, M->layers[l], pool, st);
+        if (e != hipSuccess)
+            break;
+        a.pages = pool;
+        pa.pages = pool;
+        // decode attention for the q_len == 1 sessions (its work items of longer sessions
+        // exit at once), then chunked-prefill attention for the others
+        e = launch_decode_partials(a, MLA_DTYPE_F16, generic, st);
+        if (e == hipSuccess)
+            e = launch_merge(a, st);
+        if (e == hipSuccess && max_q_len > 1)
+            e = launch_prefill(pa, max_q_len, MLA_DTYPE_F16, false, st);
+        if (e == hipSuccess)
+            e = launch_layer_post(s, M->layers[l], next_norm, st);
+    }
+    if (e == hipSuccess && rows != B) {  // logits of each session's last row only
+        StepArgs t = s;
+        t.B = B;
+        t.m_pad = round_up(B, 64);
+        t.xw = M->resw;  // free after the last layer's FFN
+        t.ss_x = M->ss_res;
+        e = launch_gather_last(s, B, md.cu_seqlens_q, t.xw, t.ss_x, st);  // from s.xw, s.ss_x
+        if (e == hipSuccess)
+            e = launch_logits(t, st);
+    } else if (e == hipSuccess) {
+        e = launch_logits(s, st);
+    }
+    return gpu_status(e, "model forward");
+}
+
 }  // namespace mla
 
 using namespace mla;
@@ -351,95 +486,31 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
                    const int32_t* cu_splits, const int32_t* work_desc, const int32_t* work_pages,
                    const int32_t* info, int max_work, void* const* pages, void* workspace,
                    size_t workspace_bytes, float* logits, int32_t* next_tokens) {
-    auto* M = static_cast<Model*>(model);
-    if (!M || B < 0 || B > (M ? M->max_batch : 0) || max_work < 0 || max_work > kMaxWork ||
-        max_pages < 0 || num_pool_pages < 0)
-        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_step: invalid argument");
-    if (B == 0)
-        return MLA_OK;
-    if (!tokens || !positions || !cu_seqlens_q || !page_table || !slot_mapping || !num_splits ||
-        !cu_splits || !work_desc || !work_pages || !info || !pages || !next_tokens)
-        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_step: null buffer");
-    for (int l = 0; l < M->cfg.n_layers; ++l)
-        if (!pages[l])
-            return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_step: null page pool");
-    const ModelDims& m = M->dims;
-    const size_t need = mla_decode_workspace_bytes(max_work, B, m.H, m.kv_rank);
-    if (!workspace || workspace_bytes < need)
-        return fail(MLA_ERR_INVALID_ARGUMENT,
-                    "mla_model_step: workspace needs " + std::to_string(need) + " bytes");
-    const auto st = static_cast<hipStream_t>(stream);
-    StepArgs s{};
-    s.dims = m;
-    s.B = B;
-    s.m_pad = round_up(B, 64);
-    s.tokens = tokens;
-    s.positions = positions;
-    s.slot_mapping = slot_mapping;
-    s.num_pool_pages = num_pool_pages;
-    s.embed = M->embed;
-    s.final_norm = M->final_norm;
-    s.rope_tab = reinterpret_cast<const float2*>(M->rope_tab);
-    s.x = M->x;
-    s.res = M->res;
-    s.xw = M->xw;
-    s.resw = M->resw;
-    s.cqw = M->cqw;
-    s.rope_rows = M->rope_rows;
-    s.ctx = M->ctx;
-    s.kvraw = M->kvraw;
-    s.u = M->u;
-    s.q_latent = M->q_latent;
-    s.q_rope = M->q_rope;
-    s.logits = logits ? logits : M->logits;
-    s.arg_v = M->arg_v;
-    s.arg_c = M->arg_c;
-    s.next_tokens = next_tokens;
-    s.ss_x = M->ss_x;
-    s.ss_res = M->ss_res;
-    s.ss_q = M->ss_q;
-    s.ss_kv = M->ss_kv;
-    DecodeArgs a{};
-    a.B = B;
-    a.H = m.H;
-    a.kv_rank = m.kv_rank;
-    a.rope_dim = m.rope;
-    a.page_size = m.page_size;
-    a.max_pages = max_pages;
-    a.num_pool_pages = num_pool_pages;
-    a.max_work = max_work;
-    a.scale_log2 = 1.4426950408889634f / std::sqrt((float)m.qk);  // inference.cpp:133
-    a.cu_q = cu_seqlens_q;
-    a.page_table = page_table;
-    a.num_splits = num_splits;
-    a.cu_splits = cu_splits;
-    a.work_desc = work_desc;
-    a.work_pages = work_pages;
-    a.info = info;
-    a.q_latent = M->q_latent;
-    a.q_rope = M->q_rope;
-    a.out = M->ctx;
-    a.lse = nullptr;
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = a.part_o + (size_t)max_work * m.H * m.kv_rank;
-    const bool generic = (reinterpret_cast<uintptr_t>(workspace) & 15) != 0;
-    hipError_t e = launch_embed(s, M->layers[0].attn_norm, st);
-    for (int l = 0; l < m.n_layers && e == hipSuccess; ++l) {
-        const float* next_norm = l + 1 < m.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
-        uint16_t* pool = static_cast<uint16_t*>(pages[l]);
-        e = launch_layer_pre(s, M->layers[l], pool, st);
-        if (e != hipSuccess)
-            break;
-        a.pages = pool;
-        e = launch_decode_partials(a, MLA_DTYPE_F16, generic, st);
-        if (e == hipSuccess)
-            e = launch_merge(a, st);
-        if (e == hipSuccess)
-            e = launch_layer_post(s, M->layers[l], next_norm, st);
-    }
-    if (e == hipSuccess)
-        e = launch_logits(s, st);
-    return gpu_status(e, "mla_model_step");
+    // Every session appends one token: rows are sessions and no prefill attention runs,
+    // so cu_seqlens_k is not read.
+    const MetaPtrs md{cu_seqlens_q, nullptr, page_table, slot_mapping, num_splits, cu_splits,
+                      work_desc, work_pages, info, max_pages, num_pool_pages, max_work};
+    return model_forward(static_cast<Model*>(model), static_cast<hipStream_t>(stream), B, tokens,
+                         positions, B, 1, md, pages, workspace, workspace_bytes, logits,
+                         next_tokens);
+}
+
+int mla_model_forward(void* model, void* stream, int rows, const int32_t* tokens,
+                      const int32_t* positions, int B, int max_q_len,
+                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                      const int32_t* page_table, int max_pages, int num_pool_pages,
+                      const int32_t* slot_mapping, const int32_t* num_splits,
+                      const int32_t* cu_splits, const int32_t* work_desc,
+                      const int32_t* work_pages, const int32_t* info, int max_work,
+                      void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
+                      int32_t* next_tokens) {
+    if (!cu_seqlens_k && max_q_len > 1)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_forward: null cu_seqlens_k");
+    const MetaPtrs md{cu_seqlens_q, cu_seqlens_k, page_table, slot_mapping, num_splits, cu_splits,
+                      work_desc, work_pages, info, max_pages, num_pool_pages, max_work};
+    return model_forward(static_cast<Model*>(model), static_cast<hipStream_t>(stream), rows,
+                         tokens, positions, B, max_q_len, md, pages, workspace, workspace_bytes,
+                         logits, next_tokens);
 }
 
 const float* mla_model_logits(void* model) {

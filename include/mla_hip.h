@@ -259,8 +259,86 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
                    const int32_t* cu_splits, const int32_t* work_desc, const int32_t* work_pages,
                    const int32_t* info, int max_work, void* const* pages, void* workspace,
                    size_t workspace_bytes, float* logits, int32_t* next_tokens);
+/* One forward of `rows` new tokens of B sessions in one batch (continuous batching with
+ * chunked prefill): session b appends q_len = cu_seqlens_q[b+1] - cu_seqlens_q[b] >= 1
+ * tokens (rows in session order; rows <= max_batch), token r at positions[r].  Per
+ * layer: the projections and the paged append of every row, decode attention for the
+ * q_len == 1 sessions (mla_decode_attention) and causal chunked-prefill attention for
+ * the others (mla_prefill_attention), the FFN.  Then the final norm, tied logits and
+ * greedy token of each session's LAST row, as the reference's prefill returns the
+ * logits of the last prompt position (src/infer/inference.cpp:64-66): logits
+ * [B x vocab], next_tokens [B].  max_q_len is the largest q_len (1 when rows == B).
+ * The metadata arguments come from one mla_build_metadata call (ctx_len = tokens
+ * already cached, q_len as above).  A prompt of n tokens prefilled in chunks through
+ * successive calls gives the same rows as one call (causality, tests/test_model.cpp:
+ * 65-77). */
+int mla_model_forward(void* model, void* stream, int rows, const int32_t* tokens,
+                      const int32_t* positions, int B, int max_q_len,
+                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                      const int32_t* page_table, int max_pages, int num_pool_pages,
+                      const int32_t* slot_mapping, const int32_t* num_splits,
+                      const int32_t* cu_splits, const int32_t* work_desc,
+                      const int32_t* work_pages, const int32_t* info, int max_work,
+                      void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
+                      int32_t* next_tokens);
 /* The model's own logits buffer [max_batch x vocab] (device). */
 const float* mla_model_logits(void* model);
+
+/* ------------------------------------------------------------------ sessions
+ * The reference's per-session inference contract -- Execution::prefill, decode and
+ * fork_inference (include/mini_mla/execution.hpp:34-37,56-58), implemented by
+ * CpuDecoder (src/infer/inference.cpp:47-174) and MpsExecution
+ * (src/backends/mps_backend.mm:872-977) -- for many sessions that share one uploaded
+ * model and one paged latent cache, plus a batched step over them (continuous
+ * batching with chunked prefill, modelled on the Gemma engine's session API
+ * prefill_batch / decode(sessions, tokens) / release, include/mini_mla/gemma.hpp:16-20).
+ * The engine owns its HIP stream, device buffers and pinned staging; logits are
+ * returned in caller-owned HOST buffers (the reference returns a host span,
+ * inference.cpp:67).  Calls on one engine are serialised by an internal mutex, so
+ * sessions may be driven from different threads (the reference's fork-per-thread
+ * use, tests/inference_sessions.hpp:191-217); concurrent sessions are served best
+ * through mla_engine_step.  Weights are immutable after creation, so the reference's
+ * stale-weight error (inference.cpp:72) cannot arise. */
+
+/* An engine for up to max_sessions sessions: model upload as mla_model_create,
+ * num_pages pages of page_size tokens per layer (fp16, the mla_append_latent format),
+ * at most max_rows new tokens per step (longer prompts are prefilled in chunks). */
+int mla_engine_create(const mla_model_config* config, const float* params, int max_sessions,
+                      int max_rows, int num_pages, int page_size, void** engine);
+int mla_engine_destroy(void* engine);
+/* info[8] = {active sessions, free pages, pages, page_size, max_rows, max_sessions,
+ *            steps run, page-pool bytes}. */
+int mla_engine_info(void* engine, int64_t* info);
+
+/* A new, empty session sharing the engine's weights: Execution::fork_inference
+ * (inference.cpp:182-188; mps_backend.mm:670-676 shares weights and programs, the
+ * cache is private).  MLA_ERR_OUT_OF_MEMORY when every slot is in use. */
+int mla_session_create(void* engine, int* session);
+/* A new session holding `source`'s cached tokens: it shares source's pages (reference
+ * counts) until either session appends into a shared page, which is then copied. */
+int mla_session_fork(void* engine, int source, int* session);
+/* Frees the session and its pages. */
+int mla_session_release(void* engine, int session);
+/* Tokens cached by the session (the reference's position_). */
+int mla_session_length(void* engine, int session, int* length);
+/* CpuDecoder::prefill (inference.cpp:47-68): restarts the session at position 0 and
+ * runs the n prompt tokens (n in [1, max_sequence_length], else
+ * MLA_ERR_INVALID_ARGUMENT "Prompt exceeds context or is empty"); logits (host
+ * [vocab], may be NULL) receives the last position's logits. */
+int mla_session_prefill(void* engine, int session, const uint16_t* ids, int n, float* logits);
+/* CpuDecoder::decode (inference.cpp:69-174): appends `token` at the session's position
+ * and returns the new logits.  MLA_ERR_INVALID_ARGUMENT unless 1 <= position <
+ * max_sequence_length and token < vocab (inference.cpp:71-75); MLA_ERR_NUMERICAL when
+ * a logit is not finite (inference.cpp:170-172; the token is appended). */
+int mla_session_decode(void* engine, int session, uint16_t token, float* logits);
+/* One batched step: sessions[i] (distinct) appends counts[i] >= 1 tokens taken in
+ * order from `tokens` (a count > 1 is a chunked prefill on top of the session's
+ * cached context; an empty session may start this way).  logits (host [n x vocab],
+ * may be NULL) and next_tokens (host [n], may be NULL: the greedy token of
+ * sample_token, inference.cpp:345-380) are those of each session's last new token.
+ * On an error no session advances. */
+int mla_engine_step(void* engine, int n, const int* sessions, const int* counts,
+                    const uint16_t* tokens, float* logits, int32_t* next_tokens);
 
 #ifdef __cplusplus
 }
