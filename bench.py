@@ -56,6 +56,8 @@ def parse():
                     help="graph replays of 20 back-to-back attention calls")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the config-2 and config-4 legs")
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="seconds of CPU work per baseline leg (all threads, then 1 thread)")
     ap.add_argument("--flags", type=int, default=0)
@@ -120,6 +122,93 @@ def cpu_baseline(batch, params, seconds: float):
                       f"sessions spread over the batch's lengths (mean context {mean_ctx:.0f}): "
                       f"{n_many} tokens on {cores} threads, one session per thread; "
                       f"{n_single} tokens on 1 thread"}
+
+
+def config2_leg(mla, params, steps: int = 64, prompt_len: int = 1024):
+    """Config 2: the mla36m model, one session, a 1024-token prompt (reference Rng seed 0,
+    ids uniform in [0, vocab)), then 64 greedy decode steps through the session engine
+    (mla_session_prefill / mla_session_decode: the reference's Execution::prefill and
+    decode, logits returned to the host every step).  Times each decode call on the host
+    clock like apps/bench_main.cpp:12-30 (median, p95)."""
+    from cpp_inference_train_engine_amd.workloads import MLA36M, SplitMix64
+    cfg = mla.ModelConfig.from_dict(MLA36M)
+    rng = SplitMix64(0)
+    prompt = [rng.bounded(MLA36M["vocab_size"]) for _ in range(prompt_len)]
+    eng = mla.HipEngine(cfg, params, max_sessions=1, max_rows=prompt_len, num_pages=32)
+    ex = eng.session()
+    ex.prefill(prompt)  # warm
+    t0 = time.perf_counter()
+    logits = ex.prefill(prompt)
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+    times = []
+    for _ in range(steps):
+        tok = int(np.argmax(logits))
+        t0 = time.perf_counter()
+        logits = ex.decode(tok)
+        times.append((time.perf_counter() - t0) * 1e3)
+    eng.close()
+    med = float(np.median(times))
+    return {"workload": "config 2: mla36m, one session, 1024-token prompt, 64 greedy decode "
+                        "steps through the session engine (host-timed decode calls, logits "
+                        "to host each step)",
+            "prefill_ms": round(prefill_ms, 3), "decode_ms_median": round(med, 4),
+            "decode_ms_p95": round(float(np.percentile(times, 95)), 4),
+            "tok_per_s": round(1e3 / med, 1),
+            "reference_mps_fp16_ms": 3.583,
+            "vs_reference_mps": round(3.583 / med, 2)}
+
+
+def config4_leg(mla, torch, reps: int = 20):
+    """Config 4 (one layer, kernels only): 8 prefill chunks of 512 tokens on contexts
+    U[0, 2048] + 120 decode sessions with log-normal lengths (median 2048, sigma 1, cap
+    16384), half of the sessions aliasing a 256-token prefix.  Times the chunked-prefill
+    kernel (MFMA-bound: flops = 544 per visible (query row, head, key)) and the decode
+    attention call (HBM-bound: 288 B per cached token) with HIP events."""
+    from cpp_inference_train_engine_amd.workloads import mixed_prefill_batch
+    b = mixed_prefill_batch(seed=0)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    need = (b.k_len + 63) // 64
+    mw = int(((need + 3) // 4).sum())
+    rows = int(b.q_len.sum())
+    rb = mla.build_metadata(dev(b.ctx_len), dev(b.q_len), dev(b.cu_pages), dev(b.page_ids), 64,
+                            b.max_pages, b.num_pages, split_pages=4, max_work=mw, max_rows=rows)
+    pages = dev(b.pages[0].view(np.int16)).view(torch.float16)
+    ql = dev(b.q_latent.view(np.int16)).view(torch.float16)
+    qr = dev(b.q_rope.view(np.int16)).view(torch.float16)
+    out = torch.empty((rows, 8, 128), dtype=torch.float32, device="cuda")
+    ws = mla.decode_workspace(mw, len(b.q_len), 8, 128)
+    flops = sum(8 * 544 * (int(c) + i + 1) for c, q in zip(b.ctx_len, b.q_len) if q > 1
+                for i in range(int(q)))
+    dec_tokens = int(b.k_len[b.q_len == 1].sum())
+    res = {}
+    for kind in ("prefill", "decode"):
+        def run(n):
+            for _ in range(n):
+                if kind == "prefill":
+                    mla.prefill_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16,
+                                          max_q_len=512, out=out)
+                else:
+                    mla.decode_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16,
+                                         out=out, workspace=ws)
+        run(3)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        run(reps)
+        e1.record()
+        torch.cuda.synchronize()
+        res[kind] = e0.elapsed_time(e1) * 1e3 / reps
+    rb.read_info()
+    tf = flops / res["prefill"] / 1e6
+    gbs = dec_tokens * 288 / res["decode"] / 1e3
+    return {"workload": "config 4 (one layer): 8 x 512-token chunks on contexts U[0,2048] + "
+                        "120 log-normal decode sessions (median 2048, sigma 1, cap 16384), "
+                        "4-page prefix shared by 64 sessions, fp16",
+            "prefill_kernel": {"us": round(res["prefill"], 2), "gflop": round(flops / 1e9, 3),
+                               "tflops": round(tf, 1), "mfma_peak_tflops": 2500.0,
+                               "frac": round(tf / 2500.0, 4)},
+            "decode_call": {"us": round(res["decode"], 2), "cached_tokens": dec_tokens,
+                            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
 
 def copy_probe(torch, mib: int):
@@ -283,6 +372,9 @@ def main():
                            "frac": round(attn_gbs / HBM_PEAK_GBS, 4)},
     }
     model.close()
+    if not args.no_secondary:
+        result["config2"] = config2_leg(mla, params)
+        result["config4"] = config4_leg(mla, torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(batch, params, args.cpu_seconds)
     print(json.dumps(result), flush=True)
