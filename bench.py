@@ -57,7 +57,7 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the config-2 and config-4 legs")
+                    help="skip the config-2, config-4 and config-5 legs")
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="seconds of CPU work per baseline leg (all threads, then 1 thread)")
     ap.add_argument("--flags", type=int, default=0)
@@ -209,6 +209,53 @@ def config4_leg(mla, torch, reps: int = 20):
                                "frac": round(tf / 2500.0, 4)},
             "decode_call": {"us": round(res["decode"], 2), "cached_tokens": dec_tokens,
                             "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
+def config5_leg(mla, torch, reps: int = 5, split: int = 128):
+    """Config 5 (kernel only): decode attention at the DeepSeek-like latent shape (128
+    heads, kv_rank 512, rope 64, nope 128: scale 1/sqrt(192)), bf16 64-token pages, 256
+    sessions with lengths U[8192, 32768] and the page permutation from the reference Rng
+    (seed 0); cache and queries N(0, 1) drawn on the device (torch generator, seed 0).
+    HBM bytes = 1152 per cached token; flops = 128 x (576 + 512) x 2 per cached token."""
+    from cpp_inference_train_engine_amd.workloads import deepseek_decode_shape
+    shape = deepseek_decode_shape(seed=0)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    pages = torch.randn((shape.num_pages, 64 * 576), generator=gen, device="cuda").to(
+        torch.bfloat16)
+    B = len(shape.k_len)
+    ql = torch.randn((B, 128, 512), generator=gen, device="cuda").to(torch.bfloat16)
+    qr = torch.randn((B, 128, 64), generator=gen, device="cuda").to(torch.bfloat16)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    need = (shape.k_len + 63) // 64
+    mw = int(((need + split - 1) // split).sum())
+    rb = mla.build_metadata(dev(shape.ctx_len), dev(shape.q_len), dev(shape.cu_pages),
+                            dev(shape.page_ids), 64, shape.max_pages, shape.num_pages,
+                            split_pages=split, max_work=mw)
+    ws = mla.decode_workspace(mw, B, 128, 512)
+    out = torch.empty((B, 128, 512), dtype=torch.float32, device="cuda")
+    scale = 1.0 / np.sqrt(192.0)
+    call = lambda: mla.decode_attention(rb, pages, ql, qr, scale, kv_rank=512, rope_dim=64,
+                                        dtype=mla.DTYPE_BF16, out=out, workspace=ws)
+    call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    rb.read_info()
+    tokens = int(shape.k_len.sum())
+    gbs = tokens * 1152 / us / 1e3
+    tf = tokens * 128 * 1088 * 2 / us / 1e6
+    del pages, ws
+    return {"workload": "config 5 (kernel only): H=128, kv_rank 512, rope 64, bf16 64-token "
+                        "pages, 256 sessions, len U[8192,32768], N(0,1) contents",
+            "kernels": "decode_wide_kernel + merge_kernel (mla_decode_attention)",
+            "split_pages": split, "work_items": mw, "cached_tokens": tokens,
+            "us": round(us, 1), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "tflops": round(tf, 1), "mfma_frac": round(tf / 2500.0, 4)}
 
 
 def copy_probe(torch, mib: int):
@@ -375,6 +422,7 @@ def main():
     if not args.no_secondary:
         result["config2"] = config2_leg(mla, params)
         result["config4"] = config4_leg(mla, torch)
+        result["config5"] = config5_leg(mla, torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(batch, params, args.cpu_seconds)
     print(json.dumps(result), flush=True)

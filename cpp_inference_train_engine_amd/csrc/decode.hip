@@ -538,6 +538,8 @@ hipError_t launch_decode_partials(const DecodeArgs& a, int dtype, bool force_gen
     const int grid = a.max_work;  // <= kMaxWork
     if (!force_generic && decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size))
         return dtype == 0 ? launch_page<F16>(a, grid, stream) : launch_page<BF16>(a, grid, stream);
+    if (!force_generic && decode_wide_supported(a.H, a.kv_rank, a.rope_dim, a.page_size))
+        return launch_decode_wide(a, dtype, stream);
     const size_t shmem = (a.kv_rank + a.rope_dim + kGenChunk + 8) * sizeof(float);
     const dim3 g(grid, a.H);
     if (dtype == 0)

@@ -1,0 +1,290 @@
+// (c) Absorbed MLA decode attention at the DeepSeek-like latent shape, gfx950:
+// 128 heads, kv_rank 512, rope 64, 64-token tiled pages (bf16 or fp16).
+//
+// Same math as decode_page_kernel (src/infer/inference.cpp:116-153), but the shape
+// turns it MFMA-heavy: per cached token 128 heads x (576 + 512) MACs against 1152
+// bytes, ~242 flop per byte, close to the bf16 MFMA ridge (2.5 PFLOP/s / 8 TB/s).
+//
+// decode_wide_kernel -- one workgroup of WAVES waves per work item (session, page
+//   range); wave v owns HT 16-head tiles (heads 16*HT*v ..), so the waves never
+//   exchange softmax state.  Each wave keeps its Q^T operands (HT x 18 k-steps) in
+//   registers and its O^T accumulators (kv_rank x 16*HT fp32) in AGPRs.  The item's
+//   pages stream through two LDS page buffers (2 x 72 KB) filled by gfx950 direct
+//   global->LDS loads (global_load_lds_dwordx4: each wave instruction copies 1 KB of
+//   the tiled record, no VGPR staging), so page p+1 is in flight while page p is
+//   consumed.  Per 32-token unit of a page:
+//     S^T = K . Q^T      v_mfma_f32_16x16x32: token tiles read from LDS as stored
+//                        (1 KB per wave read), 16 latent + 2 rope k-steps
+//     online softmax     log2 domain; the accumulators are rescaled only when a
+//                        head's running maximum rises
+//     O^T += C^T . P^T   C^T through the transpose read ds_read_b64_tr_b16 straight
+//                        from the tiled record; the S^T accumulators are P^T's B
+//                        operand as they stand (bf16: hi + lo parts)
+//   Slots past the session's end in its last page are zeroed in LDS before use.
+#include "mla_common.hpp"
+#include "mla_internal.hpp"
+
+#include <cmath>
+
+namespace mla {
+namespace {
+
+constexpr int kWideMaxItemPages = 512;  // page ids of an item staged in LDS
+
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    const auto v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (s4 __attribute__((address_space(3)))*)((__attribute__((address_space(3))) char*)p));
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// One wave copies 1 KB (64 lanes x 16 bytes, lane l: bytes 16l..) from global to LDS.
+__device__ __forceinline__ void copy_block_to_lds(const uint16_t* src, uint16_t* dst, int lane) {
+    __builtin_amdgcn_global_load_lds(
+        (const void*)(src + lane * 8),
+        (__attribute__((address_space(3))) void*)((__attribute__((address_space(3))) char*)dst),
+        16, 0, 0);
+}
+
+template <typename T, int KV, int RP, int PS, int HT, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
+    static_assert(KV % 32 == 0 && RP % 32 == 0 && PS % 32 == 0, "tile shape");
+    constexpr int KS = KV / 32;          // latent k-steps
+    constexpr int RS = RP / 32;          // rope k-steps
+    constexpr int UPP = PS / 32;         // 32-token units per page
+    constexpr int RT = KV / 16;          // latent row tiles of O^T
+    constexpr int REC = PS * (KV + RP);  // words of a page record
+    constexpr int BLOCKS = REC / 512;    // 1 KB blocks of a record
+    constexpr int CHUNKS = REC / 8;      // 16-byte chunks of a record
+    constexpr int THREADS = 64 * WAVES;
+    static_assert(REC % 512 == 0, "record blocks");
+    using V8 = typename T::vec8;
+    __shared__ __attribute__((aligned(16))) uint16_t buf0[REC];
+    __shared__ __attribute__((aligned(16))) uint16_t buf1[REC];
+    __shared__ int32_t pids[kWideMaxItemPages];  // the item's page ids
+
+    const int w = blockIdx.x;
+    const int32_t* d = a.work_desc + (long long)w * kWorkDescInts;
+    const int s = d[0];
+    if (s < 0 || d[7] != 1)
+        return;  // past the last item (or a failed build), or not a decode row
+    const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
+    const int H = a.H;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = tid >> 6;
+    const int32_t* ptab = a.page_table + (long long)s * a.max_pages;
+
+    auto issue_page_id = [&](int page, uint16_t* dst) {
+        const uint16_t* base =
+            a.pages + (long long)((unsigned)page < (unsigned)a.num_pool_pages ? page : 0) * REC;
+        for (int bk = wave; bk < BLOCKS; bk += WAVES)
+            copy_block_to_lds(base + bk * 512, dst + bk * 512, lane);
+    };
+    // Page ids come from LDS (staged below), so issuing a page never waits on memory.
+    auto issue_page = [&](int p, uint16_t* dst) {
+        const int i = p - p_begin;
+        issue_page_id(i < kWideMaxItemPages ? pids[i] : ptab[p], dst);
+    };
+    issue_page_id(ptab[p_begin], buf0);  // first page in flight while q and the ids load
+    for (int i = tid; i < min(p_end - p_begin, kWideMaxItemPages); i += THREADS)
+        pids[i] = ptab[p_begin + i];
+
+    // ---- Q^T operands: head 16*(HT*wave + ht) + n, dims 32j + 8g .. +7 ----
+    V8 qv[HT][KS + RS];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+        const int head = 16 * (HT * wave + ht) + n;
+        const bool ok = head < H;
+        const long long q = (long long)row * H + head;
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+            qv[ht][j] = ok ? *reinterpret_cast<const V8*>(a.q_latent + q * KV + 32 * j + 8 * g)
+                           : V8{};
+#pragma unroll
+        for (int j = 0; j < RS; ++j)
+            qv[ht][KS + j] =
+                ok ? *reinterpret_cast<const V8*>(a.q_rope + q * RP + 32 * j + 8 * g) : V8{};
+    }
+    const int tr_lane = (((n & 3) >> 1) * 128) + (4 * g + (n >> 2)) * 8 + 4 * (n & 1);
+
+    float m_run[HT], l_run[HT];
+    floatx4 acc[RT][HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+        m_run[ht] = -INFINITY;
+        l_run[ht] = 0.0f;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            acc[rt][ht] = floatx4{0, 0, 0, 0};
+    }
+
+    auto compute_page = [&](const uint16_t* pg, int p) {
+        const int valid = min(PS, kl - p * PS);  // >= 1 inside [p_begin, p_end)
+        if (valid < PS) {
+            // the session's last page: zero the slots past its end (they may hold any bits)
+            uint16_t* wpg = const_cast<uint16_t*>(pg);
+            for (int c = tid; c < CHUNKS; c += THREADS) {
+                const int slot = c < PS * KV / 8 ? (c / (16 * 4 * KS)) * 16 + (c & 15)
+                                                 : ((c - PS * KV / 8) / (16 * (RP / 8))) * 16 +
+                                                       (c & 15);
+                if (slot >= valid)
+                    *reinterpret_cast<u32x4*>(wpg + c * 8) = u32x4{0, 0, 0, 0};
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < UPP; ++u) {
+            floatx4 sc[2][HT];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int t = 2 * u + tt;
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht)
+                    sc[tt][ht] = floatx4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < KS; ++j) {
+                    const V8 ka = *reinterpret_cast<const V8*>(pg + (t * KS + j) * 512 + lane * 8);
+#pragma unroll
+                    for (int ht = 0; ht < HT; ++ht)
+                        sc[tt][ht] = T::mma32(ka, qv[ht][j], sc[tt][ht]);
+                }
+#pragma unroll
+                for (int j = 0; j < RS; ++j) {
+                    const V8 kr = *reinterpret_cast<const V8*>(
+                        pg + PS * KV + (t * (RP / 8) + 4 * j) * 128 + lane * 8);
+#pragma unroll
+                    for (int ht = 0; ht < HT; ++ht)
+                        sc[tt][ht] = T::mma32(kr, qv[ht][KS + j], sc[tt][ht]);
+                }
+            }
+            V8 pb[HT], pl[HT];
+#pragma unroll
+            for (int ht = 0; ht < HT; ++ht) {
+                float mp = -INFINITY;
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int slot = 32 * u + 16 * tt + 4 * g + i;
+                        const float x = slot < valid ? sc[tt][ht][i] * a.scale_log2 : -INFINITY;
+                        sc[tt][ht][i] = x;
+                        mp = fmaxf(mp, x);
+                    }
+                mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
+                mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+                const float m_new = fmaxf(m_run[ht], mp);
+                if (__ballot(m_new > m_run[ht])) {  // some head's maximum rose
+                    const float alpha =
+                        m_run[ht] == -INFINITY ? 0.0f : exp2_fast(m_run[ht] - m_new);
+                    l_run[ht] *= alpha;
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        acc[rt][ht] *= alpha;
+                    m_run[ht] = m_new;
+                }
+                float psum = 0.0f;
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float e =
+                            m_run[ht] == -INFINITY ? 0.0f : exp2_fast(sc[tt][ht][i] - m_run[ht]);
+                        psum += e;
+                        const auto hi = static_cast<typename T::scalar>(e);
+                        pb[ht][4 * tt + i] = hi;
+                        if constexpr (T::split_p)
+                            pl[ht][4 * tt + i] =
+                                static_cast<typename T::scalar>(e - static_cast<float>(hi));
+                    }
+                l_run[ht] += psum;
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int blk = ((rt >> 1) * 4 + 2 * (rt & 1)) * 128;
+                const u32x2 lo = lds_read_tr16(pg + (2 * u) * KS * 512 + blk + tr_lane);
+                const u32x2 hi = lds_read_tr16(pg + (2 * u + 1) * KS * 512 + blk + tr_lane);
+                const V8 ca = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+                for (int ht = 0; ht < HT; ++ht) {
+                    acc[rt][ht] = T::mma32(ca, pb[ht], acc[rt][ht]);
+                    if constexpr (T::split_p)
+                        acc[rt][ht] = T::mma32(ca, pl[ht], acc[rt][ht]);
+                }
+            }
+        }
+    };
+
+    // Page p of the item lives in buf0 when (p - p_begin) is even, buf1 when odd.  Each
+    // round: wait for this page's loads, barrier, issue the next page into the other
+    // buffer (its readers finished before the previous barrier), consume, barrier.
+    for (int p = p_begin; p < p_end; p += 2) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of page p landed
+        __syncthreads();
+        if (p + 1 < p_end)
+            issue_page(p + 1, buf1);
+        compute_page(buf0, p);
+        __syncthreads();
+        if (p + 1 >= p_end)
+            break;
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        if (p + 2 < p_end)
+            issue_page(p + 2, buf0);
+        compute_page(buf1, p + 1);
+        __syncthreads();
+    }
+
+    // ---- this wave's heads: final rows (one-item sessions) or split partials ----
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+        float l = l_run[ht];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const int head = 16 * (HT * wave + ht) + n;
+        if (head >= H)
+            continue;
+        if (ns == 1) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            float* o = a.out + ((long long)row * H + head) * KV;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt][ht] * inv;
+            if (a.lse && g == 0)
+                a.lse[(long long)row * H + head] = (m_run[ht] + __log2f(l)) * kLn2;
+        } else {
+            float* o = a.part_o + ((long long)w * H + head) * KV;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt][ht];
+            if (g == 0) {
+                a.part_ml[((long long)w * H + head) * 2] = m_run[ht];
+                a.part_ml[((long long)w * H + head) * 2 + 1] = l;
+            }
+        }
+    }
+}
+
+constexpr int kWideHT = 1, kWideWaves = 8;
+
+template <typename T>
+hipError_t launch_wide_t(const DecodeArgs& a, int grid, hipStream_t stream) {
+    hipLaunchKernelGGL((decode_wide_kernel<T, 512, 64, 64, kWideHT, kWideWaves>), dim3(grid),
+                       dim3(64 * kWideWaves), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool decode_wide_supported(int H, int kv_rank, int rope_dim, int page_size) {
+    return H > 16 && H <= 16 * kWideHT * kWideWaves && kv_rank == 512 && rope_dim == 64 &&
+           page_size == 64;
+}
+
+hipError_t launch_decode_wide(const DecodeArgs& a, int dtype, hipStream_t stream) {
+    return dtype == 0 ? launch_wide_t<F16>(a, a.max_work, stream)
+                      : launch_wide_t<BF16>(a, a.max_work, stream);
+}
+
+}  // namespace mla

@@ -61,6 +61,9 @@ hipError_t launch_decode_partials(const DecodeArgs& a, int dtype, bool force_gen
 // Log-sum-exp merge of the partials into the rows of split sessions.
 hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream);
 bool decode_mfma_supported(int H, int kv_rank, int rope_dim, int page_size);
+// The DeepSeek-like shape (16 < H <= 128, kv_rank 512, rope 64, 64-token pages).
+bool decode_wide_supported(int H, int kv_rank, int rope_dim, int page_size);
+hipError_t launch_decode_wide(const DecodeArgs& a, int dtype, hipStream_t stream);
 // Prefill attention for the sessions with q_len > 1 (max_q_len >= their q_len).
 hipError_t launch_prefill(const PrefillArgs& a, int max_q_len, int dtype, bool force_generic,
                           hipStream_t stream);

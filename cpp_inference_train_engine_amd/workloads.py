@@ -84,7 +84,7 @@ class DecodeBatch:
 
 def ragged_decode_batch(B=64, min_len=128, max_len=4096, page_size=64, n_heads=8, kv_rank=128,
                         rope_dim=16, n_layers=1, dtype=0, seed=0, spare_pages=0,
-                        lengths=None) -> DecodeBatch:
+                        lengths=None, q_rows=None) -> DecodeBatch:
     """Config-3-style batch: context lengths (after the append) uniform in
     [min_len, max_len], pages of ``page_size`` tokens at a random permutation of the
     pool, N(0,1) cache and query contents."""
@@ -109,8 +109,9 @@ def ragged_decode_batch(B=64, min_len=128, max_len=4096, page_size=64, n_heads=8
     pages = np.empty((n_layers, P, rec), np.uint16)
     for l in range(n_layers):
         pages[l] = to_bits(gen.standard_normal((P, rec), dtype=np.float32), dtype)
-    q_latent = to_bits(gen.standard_normal((B, n_heads, kv_rank), dtype=np.float32), dtype)
-    q_rope = to_bits(gen.standard_normal((B, n_heads, rope_dim), dtype=np.float32), dtype)
+    rows = B if q_rows is None else q_rows
+    q_latent = to_bits(gen.standard_normal((rows, n_heads, kv_rank), dtype=np.float32), dtype)
+    q_rope = to_bits(gen.standard_normal((rows, n_heads, rope_dim), dtype=np.float32), dtype)
     return DecodeBatch(ctx_len=(k_len - 1).astype(np.int32), q_len=np.ones(B, np.int32),
                        cu_pages=cu_pages, page_ids=page_ids, num_pages=P,
                        max_pages=int(counts.max()), pages=pages, q_latent=q_latent,
@@ -176,6 +177,16 @@ def mixed_prefill_batch(n_prefill=8, chunk=512, max_prefill_ctx=2048, n_decode=1
                        max_pages=int(need.max()) if B else 0, pages=pages, q_latent=q_latent,
                        q_rope=q_rope, page_size=page_size, kv_rank=kv_rank, rope_dim=rope_dim,
                        n_heads=n_heads, dtype=dtype)
+
+
+def deepseek_decode_shape(B=256, min_len=8192, max_len=32768, seed=0) -> DecodeBatch:
+    """Config 5's batch SHAPE (kernel-only decode at the DeepSeek-like latent shape: 128
+    heads, kv_rank 512, rope 64, bf16, 64-token pages): lengths uniform in [8192, 32768]
+    and the page permutation from the reference Rng; no contents (6 GB: callers draw
+    them on the device)."""
+    return ragged_decode_batch(B=B, min_len=min_len, max_len=max_len, n_heads=128,
+                               kv_rank=512, rope_dim=64, n_layers=0, dtype=1, seed=seed,
+                               q_rows=0)
 
 
 # mla36m-v1 (config/mla36m-v1.json of the reference), max_sequence_length raised so a

@@ -150,7 +150,8 @@ def test_append_generic_shape_and_skips_bad_slots(gpu, orc):
 
 
 # ------------------------------------------------------ decode attention ----
-def _run_decode(gpu, batch, layer=0, split=0, target=1024, flags=0, want_lse=True):
+def _run_decode(gpu, batch, layer=0, split=0, target=1024, flags=0, want_lse=True,
+                scale=1.0 / 8.0):
     import torch
     rb = gpu.build_metadata(_dev(batch.ctx_len), _dev(batch.q_len), _dev(batch.cu_pages),
                             _dev(batch.page_ids), batch.page_size, batch.max_pages,
@@ -161,7 +162,7 @@ def _run_decode(gpu, batch, layer=0, split=0, target=1024, flags=0, want_lse=Tru
     qr = _dev(batch.q_rope.view(np.int16)).view(tdt)
     B, H = batch.q_latent.shape[:2]
     lse = torch.zeros((B, H), dtype=torch.float32, device="cuda") if want_lse else None
-    out = gpu.decode_attention(rb, pages, ql, qr, 1.0 / np.sqrt(64.0), kv_rank=batch.kv_rank,
+    out = gpu.decode_attention(rb, pages, ql, qr, scale, kv_rank=batch.kv_rank,
                                rope_dim=batch.rope_dim, dtype=batch.dtype, lse=lse, flags=flags)
     torch.cuda.synchronize()
     info = rb.read_info()
@@ -358,3 +359,73 @@ def test_decode_partials_then_merge_equals_attention(gpu, orc, flags):
     assert torch.equal(out, ref) and torch.equal(lse_a, lse_b)
     want, _ = _oracle_decode(orc, batch)
     _check(out.cpu().numpy(), want, f"flags={flags}")
+
+
+# --------------------------------------------- DeepSeek-like shape (config 5) ----
+def _wide_batch(lengths, dtype, seed):
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    return ragged_decode_batch(lengths=lengths, n_heads=128, kv_rank=512, rope_dim=64,
+                               dtype=dtype, seed=seed, spare_pages=1)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("split", [2, 1000])
+def test_decode_wide_shape_edges(gpu, orc, dtype, split):
+    """H=128, kv_rank=512, rope=64 (config 5's latent shape): lengths at page boundaries,
+    NaN bit patterns past every session's end, split partials and single items."""
+    from cpp_inference_train_engine_amd.ops import latent_word, rope_word
+    batch = _wide_batch([1, 2, 63, 64, 65, 130, 700, 1500], dtype, seed=20 + dtype)
+    nan = 0x7E00 if dtype == 0 else 0x7FC0
+    for b, L in enumerate(batch.k_len):
+        lst = batch.page_ids[batch.cu_pages[b]:batch.cu_pages[b + 1]]
+        for t in range(int(L), len(lst) * 64):
+            rec = batch.pages[0, lst[t // 64]]
+            rec[latent_word(t % 64, np.arange(512), 64, 512, 64)] = nan
+            rec[rope_word(t % 64, np.arange(64), 64, 512, 64)] = nan
+    _say(f"decode wide dtype={dtype} split={split}")
+    scale = 1.0 / np.sqrt(192.0)
+    want, want_lse = _oracle_decode(orc, batch, scale=scale)
+    got, lse, _ = _run_decode(gpu, batch, split=split, scale=scale)
+    _check(got, want, "out")
+    np.testing.assert_allclose(lse, want_lse, rtol=1e-4, atol=1e-3)
+
+
+def test_decode_config5_full_size(gpu, orc):
+    """Config 5 at full size: 256 sessions, len U[8192, 32768] (reference Rng, seed 0), bf16
+    64-token pages in a random permutation, N(0,1) cache and queries drawn on the GPU
+    (torch generator, seed 0).  Three sessions (shortest, longest, one more) are read back
+    and checked against the oracle; every output is finite."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import deepseek_decode_shape
+    shape = deepseek_decode_shape(seed=0)
+    _say(f"decode config5 tokens={int(shape.k_len.sum())} pages={shape.num_pages}")
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    rec = 64 * 576
+    pages = torch.randn((shape.num_pages, rec), generator=gen, device="cuda").to(torch.bfloat16)
+    B = len(shape.k_len)
+    ql = torch.randn((B, 128, 512), generator=gen, device="cuda").to(torch.bfloat16)
+    qr = torch.randn((B, 128, 64), generator=gen, device="cuda").to(torch.bfloat16)
+    need = (shape.k_len + 63) // 64
+    split = 64
+    max_work = int(((need + split - 1) // split).sum())
+    rb = gpu.build_metadata(_dev(shape.ctx_len), _dev(shape.q_len), _dev(shape.cu_pages),
+                            _dev(shape.page_ids), 64, shape.max_pages, shape.num_pages,
+                            split_pages=split, max_work=max_work)
+    scale = 1.0 / np.sqrt(192.0)
+    out = gpu.decode_attention(rb, pages, ql, qr, scale, kv_rank=512, rope_dim=64,
+                               dtype=gpu.DTYPE_BF16)
+    torch.cuda.synchronize()
+    rb.read_info()
+    assert torch.isfinite(out).all()
+    order = np.argsort(shape.k_len)
+    for b in (int(order[0]), int(order[-1]), 17):
+        ids = shape.page_ids[shape.cu_pages[b]:shape.cu_pages[b + 1]]
+        sub = pages[torch.from_numpy(ids.astype(np.int64)).cuda()].view(torch.int16)
+        sub = sub.cpu().numpy().view(np.uint16)
+        table = np.arange(len(ids), dtype=np.int32)[None, :]
+        bits = lambda t: t[b:b + 1].view(torch.int16).cpu().numpy().view(np.uint16)
+        want = orc.attention_paged(128, 512, 64, 64, 1, np.array([0, 1], np.int32),
+                                   shape.k_len[b:b + 1].astype(np.int32), table, sub,
+                                   orc.bits_to_f32(bits(ql), 1), orc.bits_to_f32(bits(qr), 1),
+                                   scale, threads=8)
+        _check(out[b:b + 1].cpu().numpy(), want, f"session {b} (len {int(shape.k_len[b])})")
