@@ -88,11 +88,11 @@ __device__ __forceinline__ void wave_lds_fence() {
 // device-scope partial stores and loads because the items run on different XCDs,
 // whose L2s do not see each other's writes; measured on config 3 that tail costs
 // 4-8 us against 2-3 us for the separate merge launch.)
-template <typename T, int KV, int RP, int PS, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(3, 8)))
+template <typename T, int KV, int RP, int PS, int WAVES, int PPW>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(PPW == 1 ? 3 : PPW == 2 ? 2 : 1, 8)))
 void decode_page_kernel(DecodeArgs a) {
     static_assert(KV % 32 == 0 && RP % 8 == 0 && RP <= 32 && PS % 32 == 0, "tile shape");
-    static_assert(WAVES <= kWorkPages, "a wave's first page id comes from work_pages");
+    static_assert(WAVES * PPW <= kWorkPages, "a wave's first page ids come from work_pages");
     constexpr int KS = KV / 32;       // latent K-steps of the score MFMAs
     constexpr int TT = PS / 16;       // 16-token tiles per page
     constexpr int UPP = PS / 32;      // 32-token units per page (PV K-steps)
@@ -114,12 +114,15 @@ void decode_page_kernel(DecodeArgs a) {
     // the item is real).
     typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
     const i32x8 d = *reinterpret_cast<const i32x8*>(a.work_desc + (long long)w * kWorkDescInts);
-    const int pid_first = a.work_pages[(long long)w * kWorkPages + wave];
+    int pid[PPW];  // ids of this wave's first PPW pages (item pages wave, wave + WAVES, ..)
+#pragma unroll
+    for (int k = 0; k < PPW; ++k)
+        pid[k] = a.work_pages[(long long)w * kWorkPages + wave + k * WAVES];
     // Kernel arguments used below, fetched with the descriptor (one wait, not one per use).
     const int H = a.H, npool = a.num_pool_pages;
     const uint16_t* const pool = a.pages;
     const float scale_log2 = a.scale_log2;
-    asm volatile("" ::"s"(pid_first), "s"(H), "s"(npool), "s"(pool), "s"(scale_log2));
+    asm volatile("" ::"s"(pid[0]), "s"(H), "s"(npool), "s"(pool), "s"(scale_log2));
     const int s = d[0];
     if (s < 0 || d[7] != 1)
         return;  // past the last item (or a failed build), or not a decode row
@@ -157,11 +160,11 @@ void decode_page_kernel(DecodeArgs a) {
     const int wchunk = g ^ lds_swz(n);  // swizzled 8-column chunk of this lane's LDS row writes
     const uint16_t* src = myl + (4 * g + (n >> 2)) * UP + 4 * ((n & 3) ^ (2 * lds_swz(4 * g)));
 
-    u32x4 lat[TT][KS], rop[TT];
+    u32x4 lats[PPW][TT][KS], rops[PPW][TT];
     // Every load of one page, issued back to back.  The cache is read once per step,
     // so the loads are non-temporal (measured: a plain read of one layer's pages takes
     // 9.2 us, a non-temporal one 8.2 us).
-    auto load_page = [&](int page) {
+    auto load_page = [&](u32x4 (&lat)[TT][KS], u32x4 (&rop)[TT], int page) {
         const uint16_t* base = pool + page * rec;
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
@@ -174,7 +177,7 @@ void decode_page_kernel(DecodeArgs a) {
         }
     };
     // Scores, softmax update and PV of the loaded page (`valid` tokens of it count).
-    auto compute_page = [&](int valid) {
+    auto compute_page = [&](u32x4 (&lat)[TT][KS], u32x4 (&rop)[TT], int valid) {
         if (valid < PS) {  // the session's last page: zero the slots past its end
 #pragma unroll
             for (int t = 0; t < TT; ++t)
@@ -258,26 +261,34 @@ void decode_page_kernel(DecodeArgs a) {
         }
     };
 
-    // The wave's first page: its loads go out first, then the query's.  Further pages
-    // (items longer than WAVES pages) follow one at a time.
+    // The query's loads go out first (vmcnt completes in order, so each score MFMA then
+    // waits only for its own tile), then ALL loads of the wave's first PPW pages, page
+    // by page: the first page lands early and is consumed while the later ones stream.
+    // Further pages (items longer than WAVES * PPW pages) follow one at a time.
     const int p0 = p_begin + wave;
     if (p0 < p_end) {
-        const int page0 = __builtin_amdgcn_readfirstlane(pid_first);
-        const bool ok0 = (unsigned)page0 < (unsigned)npool;  // defensive: ids are validated
-        if (ok0)
-            load_page(page0);
         load_q();
-        if (ok0)
-            compute_page(min(PS, kl - p0 * PS));  // >= 1 inside [p_begin, p_end)
-        for (int p = p0 + WAVES; p < p_end; p += WAVES) {
+        bool ok[PPW];
+#pragma unroll
+        for (int k = 0; k < PPW; ++k) {
+            const int page = __builtin_amdgcn_readfirstlane(pid[k]);
+            ok[k] = p0 + k * WAVES < p_end && (unsigned)page < (unsigned)npool;
+            if (ok[k])
+                load_page(lats[k], rops[k], page);
+        }
+#pragma unroll
+        for (int k = 0; k < PPW; ++k)
+            if (ok[k])
+                compute_page(lats[k], rops[k], min(PS, kl - (p0 + k * WAVES) * PS));
+        for (int p = p0 + PPW * WAVES; p < p_end; p += WAVES) {
             const int rel = p - p_begin;
             const int page = __builtin_amdgcn_readfirstlane(
                 rel < kWorkPages ? a.work_pages[(long long)w * kWorkPages + rel]
                                  : a.page_table[(long long)s * a.max_pages + p]);
             if ((unsigned)page >= (unsigned)npool)
                 continue;
-            load_page(page);
-            compute_page(min(PS, kl - p * PS));
+            load_page(lats[0], rops[0], page);
+            compute_page(lats[0], rops[0], min(PS, kl - p * PS));
         }
     }
     l_run += __shfl_xor(l_run, 16, 64);
@@ -513,12 +524,17 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
 #ifndef MLA_DECODE_WAVES
 #define MLA_DECODE_WAVES 4
 #endif
+#ifndef MLA_DECODE_PPW
+#define MLA_DECODE_PPW 1
+#endif
 constexpr int kPageWaves = MLA_DECODE_WAVES;
+constexpr int kPagesPerWave = MLA_DECODE_PPW;
 
 template <typename T>
 hipError_t launch_page(const DecodeArgs& a, int grid, hipStream_t stream) {
     if (a.kv_rank == 128 && a.rope_dim == 16 && a.page_size == 64)
-        hipLaunchKernelGGL((decode_page_kernel<T, 128, 16, 64, kPageWaves>), dim3(grid),
+        hipLaunchKernelGGL((decode_page_kernel<T, 128, 16, 64, kPageWaves, kPagesPerWave>),
+                           dim3(grid),
                            dim3(64 * kPageWaves), 0, stream, a);
     else
         return hipErrorInvalidValue;

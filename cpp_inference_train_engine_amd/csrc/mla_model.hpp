@@ -60,8 +60,6 @@ struct StepArgs {
     // activations (rows padded to m_pad)
     float *x, *res, *ctx;       // [m_pad x d_pad], [m_pad x d_pad], [m_pad x H*kv_rank]
     uint16_t *xw, *resw;        // fp16 x o (next norm weight), res o ffn_norm [m_pad x d_pad]
-    uint16_t* cqw;              // fp16 cq o q_norm [m_pad x q_pad]
-    float* kvraw;               // [m_pad x kvw_pad] kv columns of [w_dq | w_dkv]
     uint16_t *u;                // [m_pad x ff_pad] fp16
     uint16_t *q_latent, *q_rope;  // [B x H x kv_rank], [B x H x rope] in the cache dtype
     float* logits;              // [B x vocab]
@@ -70,19 +68,17 @@ struct StepArgs {
     int32_t* next_tokens;       // [B]
     // Per-row sums of squares of each 16-column tile of an activation, written by its
     // producer and summed (in tile order) into 1/rms by the RMSNorm-ing consumer.
-    float* ss_x;    // [m_pad x d_pad/16] of x (embed, g6) -> attn_norm (g1), final_norm (g7)
+    float* ss_x;    // [m_pad x d_pad/16] of x (embed, g6) -> attn_norm (qkv), final_norm (g7)
     float* ss_res;  // [m_pad x d_pad/16] of res (g4) -> ffn_norm (g5)
-    float* ss_q;    // [m_pad x q_pad/16] of cq (g1) -> q_norm (g23)
-    float* ss_kv;   // [m_pad x kv_pad/16] of the latent columns of kvraw (g1) -> kv_norm
 };
 
 int g7_parts(const ModelDims& m);
-size_t g23_lds_bytes(const ModelDims& m);
-hipError_t model_kernel_attributes();
+size_t qkv_lds_bytes(const ModelDims& m);
+hipError_t model_kernel_attributes(const ModelDims& m);
 // first_norm: attn_norm of layer 0
 hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t st);
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
-                            hipStream_t st);  // g1, then g23 (which appends to `pool`)
+                            hipStream_t st);  // qkv_kernel (which appends to `pool`)
 // next_norm: attn_norm of the next layer, or final_norm after the last one
 hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const float* next_norm,
                              hipStream_t st);

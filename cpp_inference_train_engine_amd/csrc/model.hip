@@ -3,13 +3,12 @@
 // each.
 //
 // Per layer, in launch order (y = x.W for every projection, as in ops.cpp:8-18):
-//   g1_kernel   RMSNorm(x, attn_norm) . [w_dq | w_dkv] -> q part (cq) and kv part (kvraw)
-//   g23_kernel  per head: q_norm -> w_uq -> RoPE of the rope columns (q_rope, stored in
-//               the cache dtype) -> absorption q_latent = W_uk_h^T q_nope
-//               (inference.cpp:85-90,121-124; the MPS graph keeps q_latent in the
-//               storage dtype, mps_backend.mm:561); four more workgroups kv_norm the
-//               latent, RoPE the key, round both and append them to the paged cache
-//               (inference.cpp:91-103)
+//   qkv_kernel  per 16 rows: RMSNorm(x, attn_norm) . [w_dq | w_dkv], then per head q_norm
+//               -> w_uq -> RoPE of the rope columns (q_rope, stored in the cache dtype)
+//               -> absorption q_latent = W_uk_h^T q_nope (inference.cpp:85-90,121-124;
+//               the MPS graph keeps q_latent in the storage dtype, mps_backend.mm:561);
+//               one more workgroup kv_norms the latent, RoPEs the key, rounds both and
+//               appends them to the paged cache (inference.cpp:91-103)
 //   (decode attention partials + merge: decode.hip)
 //   g4_kernel   latent_ctx [H*kv_rank] . out_proj + x  (inference.cpp:154-156; out_proj
 //               is the combined W_uv.W_o of prepare_projections, inference.cpp:28-46)
@@ -266,211 +265,238 @@ __global__ __launch_bounds__(256) void embed_kernel(StepArgs s, const float* nor
     }
 }
 
-// --------------------------------------------------------------------- g1 ----
-// RMSNorm(x, attn_norm) . [w_dq | w_dkv] for 16 rows and one 16-column tile: q columns
-// to cqw = cq o q_norm (fp16, with cq's sums of squares for q_norm's inv), kv columns
-// to kvraw (fp32, with the sums of squares of the latent columns for kv_norm).
-template <int KW>
-__global__ __launch_bounds__(64 * kWaves) void g1_kernel(StepArgs s, LayerWeights L) {
-    constexpr int MT = 1, KG = kWaves;
-    __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * MT * 64];
-    __shared__ float inv_s[16 * MT];
-    const ModelDims& m = s.dims;
-    const int nt = blockIdx.x, row0 = blockIdx.y * 16 * MT;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int KT = m.d_pad / 32, col = nt * 16 + n;
-    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s, 16 * MT);
-    BPre<1, KW> bw;
-    bw.load(L.w_dq_dkv, nt, 1, KT, wave, KG, lane);
-    APre16<KW, MT> a;
-    a.load(s.xw + (long long)row0 * m.d_pad, m.d_pad, KT, wave, KG, lane);
-    const float qn = col < m.q_rank ? L.q_norm[col] : 0.0f;
-    floatx4 acc[MT][1];
-    zero(acc);
-    mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
-    int mt;
-    floatx4 v[1];
-    if (!splitk_reduce<MT, 1, KG>(acc, part, mt, v))
-        return;
-    const int q_tiles = m.q_pad / 16, r0 = row0 + 16 * mt;
-    floatx4 y;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const long long r = r0 + 4 * g + i;
-        y[i] = v[0][i] * inv_s[16 * mt + 4 * g + i];
-        if (col < m.q_pad)
-            s.cqw[r * m.q_pad + col] = F16::from_float(y[i] * qn);
-        else
-            s.kvraw[r * m.kvw_pad + (col - m.q_pad)] = y[i];
-    }
-    if (nt < q_tiles)
-        write_ss(y, true, s.ss_q, q_tiles, nt, r0, s.B);
-    else if ((nt - q_tiles) * 16 < m.kv_rank)
-        write_ss(y, col - m.q_pad < m.kv_rank, s.ss_kv, m.kv_pad / 16, nt - q_tiles, r0, s.B);
+// -------------------------------------------------------------------- qkv ----
+// Everything between the residual stream x and the attention, for 16 rows per
+// workgroup (inference.cpp:85-103): workgroup h < H computes head h's queries,
+// workgroup H the cache append.  Both start with the same split-K GEMM
+//     y = RMSNorm(x, attn_norm) . [w_dq | w_dkv]        (their column ranges)
+// (8 waves, wave w taking k-steps w, w+8, ..; the partial tiles meet in LDS), so no
+// other workgroup's output is waited for: each head workgroup recomputes the whole cq
+// row it needs for q_norm (w_dq is L2-resident, read once per workgroup).  Then
+//   head h:  q_norm(cq) -> . w_uq[:, head h] -> RoPE of the rope columns (q_rope in the
+//            cache dtype) -> q_latent = q_nope . W_uk_h^T (the MPS graph keeps q_latent
+//            in the storage dtype, mps_backend.mm:561)
+//   kv:      kv_norm of the latent columns, RoPE of the key, rounding, paged append
+constexpr int kQkvWaves = 8;
+constexpr int kQkvRows = 16;
+constexpr int kQkvMaxTiles = 16;  // q_pad <= 256, kvw_pad <= 192: at most 16 column tiles
+constexpr int kQkvPad = 8;        // fp16 pad of the LDS A-operand rows
+
+// LDS layout of qkv_kernel (bytes), from the model dims.
+struct QkvLds {
+    int part, y, ya, qf, qn, inv, total;
+};
+__host__ __device__ inline QkvLds qkv_lds(const ModelDims& m) {
+    const int nt = max(m.q_pad, m.kvw_pad) / 16;
+    const int ncol = max(m.q_pad, m.kvw_pad);
+    // The split-K partials are dead once y is summed, so ya / qf / qn / inv reuse them.
+    QkvLds l;
+    l.part = 0;                                             // [8 waves][nt][64] floatx4
+    l.ya = 0;                                               // [16][q_pad + pad] fp16
+    l.qf = l.ya + kQkvRows * (m.q_pad + kQkvPad) * 2;       // [16][qk_pad + 4] fp32
+    l.qn = l.qf + kQkvRows * (m.qk_pad + 4) * 4;            // [16][nope_pad + pad] fp16
+    l.inv = l.qn + kQkvRows * (m.nope_pad + kQkvPad) * 2;   // [16] fp32
+    l.y = max(kQkvWaves * nt * 64 * 16, l.inv + kQkvRows * 4);  // [16][ncol] fp32
+    l.total = l.y + kQkvRows * ncol * 4;
+    return l;
 }
 
-// -------------------------------------------------------------------- g23 ----
-// Workgroups h < H (4 waves, 64 rows): q_h = q_norm(cq) . w_uq[:, head columns], the
-// waves splitting K over all of the head's tiles; RoPE of the rope columns (pairs read
-// from LDS); q_rope stored in the cache dtype; q_latent_h = q_h[:, :nope] . W_uk_h^T.
-// Workgroups H ..: kv_norm of the latent, RoPE of the key, rounding, append.
-constexpr int kQTiles = 4;                        // q tiles of a head (qk <= 64)
-constexpr int kRopeItems = 64 * 32 / 256;         // RoPE pairs a thread (rope <= 64)
-constexpr int kKvWGs = 4, kKvRows = 64 / kKvWGs;  // kv-append workgroups per 64 rows
-constexpr int kKvItems = (kKvRows * (128 + 32) + 255) / 256;  // kv_rank <= 128, rope <= 64
+// Sum over the 32 lanes of a half wave.
+__device__ __forceinline__ float sum32(float v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1)
+        v += __shfl_xor(v, off, 32);
+    return v;
+}
 
-template <int KWQ, int KWU>
-__global__ __launch_bounds__(256) void g23_kernel(StepArgs s, LayerWeights L, uint16_t* pool) {
+// KC: chunks of two k-steps per wave (KT <= 16 * KC); NT >= the workgroup's column tiles.
+template <int KC, int NT>
+__global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWeights L,
+                                                             uint16_t* pool) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const ModelDims& m = s.dims;
-    const int h = blockIdx.x, mc = blockIdx.y, row0 = mc * 64;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int half = m.rope / 2;
-    __shared__ float inv_s[64];
-    if (h >= m.H) {  // ---- kv append: kKvRows rows per workgroup, elementwise ----
-        const int r0 = row0 + (h - m.H) * kKvRows;
-        inv_rms_to_lds(s.ss_kv, m.kv_pad / 16, m.kv_rank, m.eps, r0, inv_s, kKvRows);
-        const bool tiled = page_tiled(m.page_size, m.kv_rank, m.rope);
-        const int width = m.kv_rank + m.rope;
-        const int per_row = m.kv_rank + half;  // latent columns, then rope pairs
-        // every load in flight first (per_row <= 160: kKvItems items a thread), then the
-        // rounded stores
-        float va[kKvItems], vb[kKvItems], wn[kKvItems];
-        float2 cs[kKvItems];
-        int slot[kKvItems];
+    const QkvLds lay = qkv_lds(m);
+    floatx4* part = reinterpret_cast<floatx4*>(smem + lay.part);
+    float* y = reinterpret_cast<float*>(smem + lay.y);
+    _Float16* ya = reinterpret_cast<_Float16*>(smem + lay.ya);
+    float* qf = reinterpret_cast<float*>(smem + lay.qf);
+    _Float16* qn = reinterpret_cast<_Float16*>(smem + lay.qn);
+    float* inv_s = reinterpret_cast<float*>(smem + lay.inv);
+    __shared__ float inv_x[kQkvRows];
+
+    const int h = blockIdx.x, row0 = blockIdx.y * kQkvRows;
+    const bool kv = h == m.H;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int KT = m.d_pad / 32, q_tiles = m.q_pad / 16;
+    const int nt0 = kv ? q_tiles : 0, ntv = kv ? m.kvw_pad / 16 : q_tiles;
+    const int ncol = 16 * ntv, ldy = max(m.q_pad, m.kvw_pad);
+    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_x, kQkvRows);
+
+    // ---- GEMM 1: every operand of this wave in flight at once, chunk by chunk ----
+    floatx4 acc[NT];
 #pragma unroll
-        for (int i = 0; i < kKvItems; ++i) {
-            const int e = threadIdx.x + 256 * i, r = e / per_row, c = e % per_row;
-            const int row = r0 + r;
-            va[i] = vb[i] = wn[i] = 0.0f;
-            cs[i] = float2{1.0f, 0.0f};
-            slot[i] = -1;
-            if (r < kKvRows && row < s.B) {
-                slot[i] = s.slot_mapping[row];
-                const float* kr = s.kvraw + (long long)row * m.kvw_pad;
-                if (c < m.kv_rank) {
-                    va[i] = kr[c];
-                    wn[i] = L.kv_norm[c];
-                } else {
-                    const int j2 = c - m.kv_rank;
-                    va[i] = kr[m.kv_rank + 2 * j2];
-                    vb[i] = kr[m.kv_rank + 2 * j2 + 1];
-                    cs[i] = s.rope_rows[(long long)row * half + j2];
-                }
-            }
+    for (int j = 0; j < NT; ++j)
+        acc[j] = floatx4{0, 0, 0, 0};
+    const uint16_t* xw = s.xw + (long long)(row0 + n) * m.d_pad;
+    // head workgroups also prefetch their w_uq / W_uk tiles (used after the reduction)
+    const int qk_tiles = m.qk_pad / 16, KTQ = m.q_pad / 32;
+    const int kv_tiles = m.kv_pad / 16, KTU = m.nope_pad / 32;
+    V8 bq[8], bu[4];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        V8 a[2], b[2][NT];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int kt = wave + kQkvWaves * (2 * c + kk);
+            a[kk] = kt < KT ? *reinterpret_cast<const V8*>(xw + 32 * kt + 8 * g) : V8{};
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                b[kk][j] = kt < KT && j < ntv
+                               ? *reinterpret_cast<const V8*>(
+                                     L.w_dq_dkv + ((long long)(nt0 + j) * KT + kt) * 512 + lane * 8)
+                               : V8{};
         }
-        __syncthreads();
+        if (c == 0 && !kv) {
 #pragma unroll
-        for (int i = 0; i < kKvItems; ++i) {
-            const int e = threadIdx.x + 256 * i, r = e / per_row, c = e % per_row;
-            const int page = slot[i] / m.page_size, off = slot[i] % m.page_size;
-            if (slot[i] < 0 || page >= s.num_pool_pages)
+            for (int k = 0; k < 8; ++k)
+                bq[k] = wave < qk_tiles && k < KTQ
+                            ? *reinterpret_cast<const V8*>(
+                                  L.w_uq + ((long long)(h * qk_tiles + wave) * KTQ + k) * 512 +
+                                  lane * 8)
+                            : V8{};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                bu[k] = wave < kv_tiles && k < KTU
+                            ? *reinterpret_cast<const V8*>(
+                                  L.w_uk + (long long)h * kv_tiles * KTU * 512 +
+                                  ((long long)wave * KTU + k) * 512 + lane * 8)
+                            : V8{};
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+                acc[j] = mma(a[kk], b[kk][j], acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+        if (j < ntv)
+            part[(wave * ntv + j) * 64 + lane] = acc[j];
+    __syncthreads();
+    // y[r][c] = inv_x[r] * sum over the waves (rows 4g+i, column 16j+n of lane group e)
+    for (int e = tid; e < ntv * 64; e += 64 * kQkvWaves) {
+        const int j = e >> 6, l = e & 63;
+        floatx4 v = {0, 0, 0, 0};
+#pragma unroll
+        for (int w = 0; w < kQkvWaves; ++w)
+            v += part[(w * ntv + j) * 64 + l];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * (l >> 4) + i;
+            y[r * ldy + 16 * j + (l & 15)] = v[i] * inv_x[r];
+        }
+    }
+    __syncthreads();
+
+    // ---- row norms: q_norm over q_rank columns, or kv_norm over kv_rank ----
+    {
+        const int r = tid >> 5, sub = tid & 31;  // 32 threads a row (512 threads, 16 rows)
+        const int cols = kv ? m.kv_rank : m.q_rank;
+        float ss = 0.0f;
+        for (int c = sub; c < cols; c += 32) {
+            const float v = y[r * ldy + c];
+            ss += v * v;
+        }
+        ss = sum32(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)cols + m.eps);  // ops.cpp:37-44
+        if (kv) {
+            if (sub == 0)
+                inv_s[r] = inv;
+        } else {
+            for (int c = sub; c < m.q_pad; c += 32)
+                ya[r * (m.q_pad + kQkvPad) + c] =
+                    (_Float16)(c < m.q_rank ? y[r * ldy + c] * inv * L.q_norm[c] : 0.0f);
+        }
+    }
+    __syncthreads();
+
+    if (kv) {  // ---- kv_norm, RoPE of the key, rounding, append ----
+        const bool tiled = page_tiled(m.page_size, m.kv_rank, m.rope);
+        const int half = m.rope / 2, width = m.kv_rank + m.rope, per_row = m.kv_rank + half;
+        for (int e = tid; e < kQkvRows * per_row; e += 64 * kQkvWaves) {
+            const int r = e / per_row, c = e % per_row, row = row0 + r;
+            if (row >= s.B)
+                continue;
+            const int slot = s.slot_mapping[row];
+            const int page = slot / m.page_size, off = slot % m.page_size;
+            if (slot < 0 || page >= s.num_pool_pages)
                 continue;
             uint16_t* base = pool + (long long)page * m.page_size * width;
             if (c < m.kv_rank) {
                 base[latent_word(tiled, off, c, m.page_size, m.kv_rank)] =
-                    F16::from_float(va[i] * inv_s[r] * wn[i]);
+                    F16::from_float(y[r * ldy + c] * inv_s[r] * L.kv_norm[c]);
             } else {
-                const int jp = 2 * (c - m.kv_rank);
+                const int j2 = c - m.kv_rank, jp = 2 * j2;
+                const float2 cs = s.rope_rows[(long long)row * half + j2];
+                const float a0 = y[r * ldy + m.kv_rank + jp], a1 = y[r * ldy + m.kv_rank + jp + 1];
                 base[rope_word(tiled, off, jp, m.page_size, m.kv_rank, m.rope)] =
-                    F16::from_float(va[i] * cs[i].x - vb[i] * cs[i].y);
+                    F16::from_float(a0 * cs.x - a1 * cs.y);
                 base[rope_word(tiled, off, jp + 1, m.page_size, m.kv_rank, m.rope)] =
-                    F16::from_float(va[i] * cs[i].y + vb[i] * cs[i].x);
+                    F16::from_float(a0 * cs.y + a1 * cs.x);
             }
         }
         return;
     }
-    // ---- one head: q_h over the head's tiles, 4 waves splitting K ----
-    const int qk_tiles = m.qk_pad / 16, KTQ = m.q_pad / 32;
-    const int kv_tiles = m.kv_pad / 16, KTU = m.nope_pad / 32;
-    inv_rms_to_lds(s.ss_q, m.q_pad / 16, m.q_rank, m.eps, row0, inv_s, 64);
-    BPre<kQTiles, KWQ> bq;
-    bq.load(L.w_uq, h * qk_tiles, qk_tiles, KTQ, wave, 4, lane);
-    BPre<2, KWU> bu;  // this wave's two latent tiles of the absorption, whole K
-    bu.load(L.w_uk + (long long)h * kv_tiles * KTU * 512, 2 * wave, min(2, kv_tiles - 2 * wave),
-            KTU, 0, 1, lane);
-    APre16<KWQ, 4> a;
-    a.load(s.cqw + (long long)row0 * m.q_pad, m.q_pad, KTQ, wave, 4, lane);
-    float2 cs[kRopeItems];  // RoPE rows of this thread's pairs
+    (void)ncol;
+
+    // ---- q_h = q_norm(cq) . w_uq[:, head h]: wave w < qk_tiles owns column tile w ----
+    if (wave < qk_tiles) {
+        floatx4 q = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < kRopeItems; ++i) {
-        const int e = threadIdx.x + 256 * i, r = e / max(half, 1);
-        cs[i] = e < 64 * half ? s.rope_rows[(long long)(row0 + r) * half + e % half]
-                              : float2{1.0f, 0.0f};
+        for (int k = 0; k < 8; ++k)
+            if (k < KTQ)
+                q = mma(*reinterpret_cast<const V8*>(ya + n * (m.q_pad + kQkvPad) + 32 * k + 8 * g),
+                        bq[k], q);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            qf[(4 * g + i) * (m.qk_pad + 4) + 16 * wave + n] = q[i];
     }
-    floatx4 acc[4][kQTiles];
-    zero(acc);
-    mma_steps(acc, bq, [&](int kk, int mt) { return a.x[kk][mt]; });
-    // reduce the 4 waves' partials: wave w finishes M-tile w, all of the head's tiles
-    floatx4* part = reinterpret_cast<floatx4*>(smem);  // [4 waves][4 mt][kQTiles][64]
-    float* qf = reinterpret_cast<float*>(smem);         // then q_h fp32 [64][qk_pad + 4]
-    const int ldf = m.qk_pad + 4;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int j = 0; j < kQTiles; ++j)
-            part[((wave * 4 + mt) * kQTiles + j) * 64 + lane] = acc[mt][j];
     __syncthreads();
-    floatx4 q[kQTiles];
-#pragma unroll
-    for (int j = 0; j < kQTiles; ++j) {
-        q[j] = floatx4{0, 0, 0, 0};
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-            q[j] += part[((w * 4 + wave) * kQTiles + j) * 64 + lane];
+    {   // RoPE of the rope columns (pairs adjacent, ops.cpp:88-108) -> q_rope; q_nope -> fp16
+        const int half = m.rope / 2, ldq = m.nope_pad + kQkvPad;
+        for (int e = tid; e < kQkvRows * half; e += 64 * kQkvWaves) {
+            const int r = e / half, j2 = e % half, jp = 2 * j2, row = row0 + r;
+            if (row >= s.B)
+                continue;
+            const float2 cs = s.rope_rows[(long long)row * half + j2];
+            const float a0 = qf[r * (m.qk_pad + 4) + m.nope + jp];
+            const float a1 = qf[r * (m.qk_pad + 4) + m.nope + jp + 1];
+            uint16_t* qr = s.q_rope + ((long long)row * m.H + h) * m.rope;
+            qr[jp] = F16::from_float(a0 * cs.x - a1 * cs.y);
+            qr[jp + 1] = F16::from_float(a0 * cs.y + a1 * cs.x);
+        }
+        for (int e = tid; e < kQkvRows * m.nope_pad; e += 64 * kQkvWaves) {
+            const int r = e / m.nope_pad, c = e % m.nope_pad;
+            qn[r * ldq + c] = (_Float16)(c < m.nope ? qf[r * (m.qk_pad + 4) + c] : 0.0f);
+        }
     }
-    __syncthreads();  // partials consumed: the LDS now holds q_h in fp32
+    __syncthreads();
+    // ---- q_latent_h = q_nope . W_uk_h^T: wave w < kv_tiles owns latent tile w ----
+    if (wave < kv_tiles) {
+        const int ldq = m.nope_pad + kQkvPad;
+        floatx4 ql = {0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < kQTiles; ++j)
-        if (j < qk_tiles)
+        for (int k = 0; k < 4; ++k)
+            if (k < KTU)
+                ql = mma(*reinterpret_cast<const V8*>(qn + n * ldq + 32 * k + 8 * g), bu[k], ql);
+        const int c = 16 * wave + n;
+        if (c < m.kv_rank)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int r = 16 * wave + 4 * g + i;
-                qf[r * ldf + 16 * j + n] = q[j][i] * inv_s[r];
+                const int row = row0 + 4 * g + i;
+                if (row < s.B)
+                    s.q_latent[((long long)row * m.H + h) * m.kv_rank + c] = F16::from_float(ql[i]);
             }
-    __syncthreads();
-    // RoPE + q_rope; q_nope to the fp16 A tile of the absorption
-    const int ldq = m.nope_pad + kLdsPad;
-    _Float16* q_s = reinterpret_cast<_Float16*>(smem + 64 * ldf * sizeof(float));
-    for (int e = threadIdx.x; e < 64 * m.nope_pad; e += 256) {
-        const int r = e / m.nope_pad, c = e % m.nope_pad;
-        q_s[r * ldq + c] = (_Float16)(c < m.nope ? qf[r * ldf + c] : 0.0f);
-    }
-#pragma unroll
-    for (int i = 0; i < kRopeItems; ++i) {
-        const int e = threadIdx.x + 256 * i, r = e / max(half, 1), jp = 2 * (e % max(half, 1));
-        const int row = row0 + r;
-        if (e < 64 * half && row < s.B) {
-            const float a0 = qf[r * ldf + m.nope + jp], a1 = qf[r * ldf + m.nope + jp + 1];
-            uint16_t* qr = s.q_rope + ((long long)row * m.H + h) * m.rope;
-            qr[jp] = F16::from_float(a0 * cs[i].x - a1 * cs[i].y);
-            qr[jp + 1] = F16::from_float(a0 * cs[i].y + a1 * cs[i].x);
-        }
-    }
-    __syncthreads();
-    // q_latent_h = q_h[:, :nope] . W_uk_h^T  (K = nope_pad, N = kv_pad; two tiles a wave)
-    if (2 * wave < kv_tiles) {
-        floatx4 acc2[4][2];
-        zero(acc2);
-        mma_steps(acc2, bu, [&](int kk, int mt) {  // k-steps past nope_pad: zeros, not LDS
-            return kk < KTU ? *reinterpret_cast<const V8*>(q_s + (16 * mt + n) * ldq + 32 * kk +
-                                                           8 * g)
-                            : V8{};
-        });
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int c = (2 * wave + j) * 16 + n;
-            if (c < m.kv_rank)
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int row = row0 + 16 * mt + 4 * g + i;
-                        if (row < s.B)
-                            s.q_latent[((long long)row * m.H + h) * m.kv_rank + c] =
-                                F16::from_float(acc2[mt][j][i]);
-                    }
-        }
     }
 }
 
@@ -755,12 +781,6 @@ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 }  // namespace
 
 // ------------------------------------------------------------------ launches ----
-size_t g23_lds_bytes(const ModelDims& m) {
-    const size_t part = 4 * 4 * kQTiles * 64 * sizeof(floatx4);
-    const size_t q = 64 * (size_t)(m.qk_pad + 4) * 4 + 64 * (size_t)(m.nope_pad + kLdsPad) * 2;
-    return part > q ? part : q;
-}
-
 int g7_parts(const ModelDims& m) { return ceil_div(m.vocab_pad / 16, kG7Tiles); }
 
 #define MLA_KW_DISPATCH(kw, KERNEL, ...)                                                        \
@@ -781,11 +801,16 @@ int g7_parts(const ModelDims& m) { return ceil_div(m.vocab_pad / 16, kG7Tiles); 
     default: hipLaunchKernelGGL(KERNEL<4>, __VA_ARGS__); break;                                  \
     }
 
-// Kernels whose dynamic LDS can exceed 64 KB.
-hipError_t model_kernel_attributes() {
-    const int bytes = 160 * 1024 - 32 * 1024;
-    const void* ks[] = {reinterpret_cast<const void*>(&g23_kernel<2, 2>),
-                        reinterpret_cast<const void*>(&g23_kernel<2, 4>)};
+size_t qkv_lds_bytes(const ModelDims& m) { return (size_t)qkv_lds(m).total; }
+
+// Kernels whose dynamic LDS can exceed 64 KB: allow what this model's shape needs.
+hipError_t model_kernel_attributes(const ModelDims& m) {
+    const int bytes = (int)qkv_lds_bytes(m);
+    const void* ks[] = {
+        reinterpret_cast<const void*>(&qkv_kernel<1, 4>), reinterpret_cast<const void*>(&qkv_kernel<1, 8>),
+        reinterpret_cast<const void*>(&qkv_kernel<1, 12>), reinterpret_cast<const void*>(&qkv_kernel<1, 16>),
+        reinterpret_cast<const void*>(&qkv_kernel<2, 4>), reinterpret_cast<const void*>(&qkv_kernel<2, 8>),
+        reinterpret_cast<const void*>(&qkv_kernel<2, 12>), reinterpret_cast<const void*>(&qkv_kernel<2, 16>)};
     for (const void* k : ks) {
         const hipError_t e =
             hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -803,19 +828,22 @@ hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t 
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
                             hipStream_t st) {
     const ModelDims& m = s.dims;
-    MLA_KW4_DISPATCH(kw_variant(ceil_div(m.d_pad / 32, kWaves)), g1_kernel,
-                     dim3((m.q_pad + m.kvw_pad) / 16, ceil_div(s.B, 16)), dim3(64 * kWaves), 0,
-                     st, s, w);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess)
-        return e;
-    // q_pad <= 256: at most 2 k-steps of w_uq per wave; nope_pad <= 128: 4 of w_uk
-    const dim3 grid(m.H + kKvWGs, ceil_div(s.B, 64));
-    const size_t lds = g23_lds_bytes(m);
-    if (m.nope_pad / 32 <= 2)
-        hipLaunchKernelGGL((g23_kernel<2, 2>), grid, dim3(256), lds, st, s, w, pool);
-    else
-        hipLaunchKernelGGL((g23_kernel<2, 4>), grid, dim3(256), lds, st, s, w, pool);
+    const dim3 grid(m.H + 1, ceil_div(s.B, kQkvRows));
+    const size_t lds = qkv_lds_bytes(m);
+    const int nt = max(m.q_pad, m.kvw_pad) / 16;  // <= 16 (mla_model_create checks)
+    const int tiles = nt <= 4 ? 4 : nt <= 8 ? 8 : nt <= 12 ? 12 : 16;
+    // d_pad <= 512: one chunk of two k-steps per wave; <= 1024: two
+    const int kc = m.d_pad / 32 <= 2 * kQkvWaves ? 1 : 2;
+#define MLA_QKV(KC, NT)                                                                         \
+    hipLaunchKernelGGL((qkv_kernel<KC, NT>), grid, dim3(64 * kQkvWaves), lds, st, s, w, pool)
+    if (kc == 1) {
+        if (tiles == 4) MLA_QKV(1, 4); else if (tiles == 8) MLA_QKV(1, 8);
+        else if (tiles == 12) MLA_QKV(1, 12); else MLA_QKV(1, 16);
+    } else {
+        if (tiles == 4) MLA_QKV(2, 4); else if (tiles == 8) MLA_QKV(2, 8);
+        else if (tiles == 12) MLA_QKV(2, 12); else MLA_QKV(2, 16);
+    }
+#undef MLA_QKV
     return hipGetLastError();
 }
 

@@ -120,10 +120,10 @@ struct Model {
     const uint16_t* embed = nullptr;
     const float* final_norm = nullptr;
     const float* rope_tab = nullptr;
-    float *x, *res, *ctx, *kvraw, *logits, *arg_v;
-    float *ss_x, *ss_res, *ss_q, *ss_kv;
+    float *x, *res, *ctx, *logits, *arg_v;
+    float *ss_x, *ss_res;
     float2* rope_rows;
-    uint16_t *xw, *resw, *cqw, *u, *q_latent, *q_rope;
+    uint16_t *xw, *resw, *u, *q_latent, *q_rope;
     int32_t* arg_c;
 
     ~Model() {
@@ -224,10 +224,8 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     s.res = M->res;
     s.xw = M->xw;
     s.resw = M->resw;
-    s.cqw = M->cqw;
     s.rope_rows = M->rope_rows;
     s.ctx = M->ctx;
-    s.kvraw = M->kvraw;
     s.u = M->u;
     s.q_latent = M->q_latent;
     s.q_rope = M->q_rope;
@@ -237,8 +235,6 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     s.next_tokens = next_tokens;
     s.ss_x = M->ss_x;
     s.ss_res = M->ss_res;
-    s.ss_q = M->ss_q;
-    s.ss_kv = M->ss_kv;
     DecodeArgs a{};
     a.B = B;
     a.H = m.H;
@@ -360,7 +356,11 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
     const int d = c.d_model, q = c.q_lora_rank, H = c.n_heads, nope = c.head_dim_nope;
     const int qk = m.qk, kv = c.kv_lora_rank, kvw = kv + c.head_dim_rope, dv = c.head_dim_value;
     const int ff = c.d_ff;
-    hipError_t e = model_kernel_attributes();
+    if (qkv_lds_bytes(m) > 150 * 1024) {  // the gfx950 workgroup LDS is 160 KB
+        delete M;
+        return fail(MLA_ERR_UNSUPPORTED, "mla_model_create: projection tiles exceed the LDS");
+    }
+    hipError_t e = model_kernel_attributes(m);
     auto bail = [&](hipError_t err) {
         delete M;
         return gpu_status(err, "mla_model_create");
@@ -453,10 +453,8 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
     if (e == hipSuccess) e = M->alloc(M->res, rows * m.d_pad);
     if (e == hipSuccess) e = M->alloc(M->xw, rows * m.d_pad);
     if (e == hipSuccess) e = M->alloc(M->resw, rows * m.d_pad);
-    if (e == hipSuccess) e = M->alloc(M->cqw, rows * m.q_pad);
     if (e == hipSuccess) e = M->alloc(M->rope_rows, rows * (size_t)(c.head_dim_rope / 2));
     if (e == hipSuccess) e = M->alloc(M->ctx, rows * (size_t)H * kv);
-    if (e == hipSuccess) e = M->alloc(M->kvraw, rows * m.kvw_pad);
     if (e == hipSuccess) e = M->alloc(M->u, rows * m.ff_pad);
     if (e == hipSuccess) e = M->alloc(M->q_latent, (size_t)max_batch * H * kv);
     if (e == hipSuccess) e = M->alloc(M->q_rope, (size_t)max_batch * H * c.head_dim_rope);
@@ -465,8 +463,6 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
     if (e == hipSuccess) e = M->alloc(M->arg_c, (size_t)max_batch * M->parts);
     if (e == hipSuccess) e = M->alloc(M->ss_x, rows * (m.d_pad / 16));
     if (e == hipSuccess) e = M->alloc(M->ss_res, rows * (m.d_pad / 16));
-    if (e == hipSuccess) e = M->alloc(M->ss_q, rows * (m.q_pad / 16));
-    if (e == hipSuccess) e = M->alloc(M->ss_kv, rows * (m.kv_pad / 16));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess)
         return bail(e);
