@@ -40,10 +40,11 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-// One wave copies 1 KB (64 lanes x 16 bytes, lane l: bytes 16l..) from global to LDS.
-__device__ __forceinline__ void copy_block_to_lds(const uint16_t* src, uint16_t* dst, int lane) {
+// One wave copies 1 KB from global to LDS: lane l's 16 bytes (from its own `src`)
+// land at dst + 16 l bytes.
+__device__ __forceinline__ void copy_block_to_lds(const uint16_t* src, uint16_t* dst) {
     __builtin_amdgcn_global_load_lds(
-        (const void*)(src + lane * 8),
+        (const void*)src,
         (__attribute__((address_space(3))) void*)((__attribute__((address_space(3))) char*)dst),
         16, 0, 0);
 }
@@ -58,6 +59,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     constexpr int REC = PS * (KV + RP);  // words of a page record
     constexpr int BLOCKS = REC / 512;    // 1 KB blocks of a record
     constexpr int CHUNKS = REC / 8;      // 16-byte chunks of a record
+    constexpr int LAT_BLOCKS = PS * KV / 512;  // latent 1 KB blocks (the rest is rope)
     constexpr int THREADS = 64 * WAVES;
     static_assert(REC % 512 == 0, "record blocks");
     using V8 = typename T::vec8;
@@ -76,11 +78,17 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     const int wave = tid >> 6;
     const int32_t* ptab = a.page_table + (long long)s * a.max_pages;
 
+    // Latent blocks land in LDS with odd 256-byte sub-chunks rotated by 8 token rows
+    // (lane l of the copy fetches the chunk that belongs at LDS slot l): the transpose
+    // reads of two adjacent sub-chunks then hit disjoint banks.  Rope blocks are copied
+    // as stored.
+    const int lat_src = (lane >> 4) * 128 + ((lane & 15) ^ (((lane >> 4) & 1) << 3)) * 8;
     auto issue_page_id = [&](int page, uint16_t* dst) {
         const uint16_t* base =
             a.pages + (long long)((unsigned)page < (unsigned)a.num_pool_pages ? page : 0) * REC;
         for (int bk = wave; bk < BLOCKS; bk += WAVES)
-            copy_block_to_lds(base + bk * 512, dst + bk * 512, lane);
+            copy_block_to_lds(base + bk * 512 + (bk < LAT_BLOCKS ? lat_src : lane * 8),
+                              dst + bk * 512);
     };
     // Page ids come from LDS (staged below), so issuing a page never waits on memory.
     auto issue_page = [&](int p, uint16_t* dst) {
@@ -107,7 +115,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
             qv[ht][KS + j] =
                 ok ? *reinterpret_cast<const V8*>(a.q_rope + q * RP + 32 * j + 8 * g) : V8{};
     }
-    const int tr_lane = (((n & 3) >> 1) * 128) + (4 * g + (n >> 2)) * 8 + 4 * (n & 1);
+    // transpose-read address of lane (g, n) in a 16-token tile: sub-chunk parity
+    // (n & 3) >> 1 (odd sub-chunks rotated by 8 rows), token 4g + n/4, half n & 1
+    const int tr_par = (n & 3) >> 1;
+    const int tr_lane = tr_par * 128 + ((4 * g + (n >> 2)) ^ (tr_par << 3)) * 8 + 4 * (n & 1);
+    // score A-operand read of lane (g, n): sub-chunk g, token n
+    const int s_lane = g * 128 + (n ^ ((g & 1) << 3)) * 8;
 
     float m_run[HT], l_run[HT];
     floatx4 acc[RT][HT];
@@ -126,9 +139,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
             // the session's last page: zero the slots past its end (they may hold any bits)
             uint16_t* wpg = const_cast<uint16_t*>(pg);
             for (int c = tid; c < CHUNKS; c += THREADS) {
-                const int slot = c < PS * KV / 8 ? (c / (16 * 4 * KS)) * 16 + (c & 15)
-                                                 : ((c - PS * KV / 8) / (16 * (RP / 8))) * 16 +
-                                                       (c & 15);
+                const int slot =
+                    c < PS * KV / 8
+                        ? (c / (16 * 4 * KS)) * 16 + ((c & 15) ^ ((((c >> 4) & 1)) << 3))
+                        : ((c - PS * KV / 8) / (16 * (RP / 8))) * 16 + (c & 15);
                 if (slot >= valid)
                     *reinterpret_cast<u32x4*>(wpg + c * 8) = u32x4{0, 0, 0, 0};
             }
@@ -136,27 +150,32 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < UPP; ++u) {
+            // S^T of the unit's two token tiles, k-step by k-step (two independent MFMA
+            // chains), the next k-step's operands read while this one's MFMAs run.
             floatx4 sc[2][HT];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const int t = 2 * u + tt;
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int ht = 0; ht < HT; ++ht)
                     sc[tt][ht] = floatx4{0, 0, 0, 0};
+            auto k_operand = [&](int tt, int j) {
+                const int t = 2 * u + tt;
+                return j < KS ? *reinterpret_cast<const V8*>(pg + (t * KS + j) * 512 + s_lane)
+                              : *reinterpret_cast<const V8*>(
+                                    pg + PS * KV + (t * (RP / 8) + 4 * (j - KS)) * 128 + lane * 8);
+            };
+            V8 kn[2] = {k_operand(0, 0), k_operand(1, 0)};
 #pragma unroll
-                for (int j = 0; j < KS; ++j) {
-                    const V8 ka = *reinterpret_cast<const V8*>(pg + (t * KS + j) * 512 + lane * 8);
-#pragma unroll
-                    for (int ht = 0; ht < HT; ++ht)
-                        sc[tt][ht] = T::mma32(ka, qv[ht][j], sc[tt][ht]);
+            for (int j = 0; j < KS + RS; ++j) {
+                const V8 k0 = kn[0], k1 = kn[1];
+                if (j + 1 < KS + RS) {
+                    kn[0] = k_operand(0, j + 1);
+                    kn[1] = k_operand(1, j + 1);
                 }
 #pragma unroll
-                for (int j = 0; j < RS; ++j) {
-                    const V8 kr = *reinterpret_cast<const V8*>(
-                        pg + PS * KV + (t * (RP / 8) + 4 * j) * 128 + lane * 8);
-#pragma unroll
-                    for (int ht = 0; ht < HT; ++ht)
-                        sc[tt][ht] = T::mma32(kr, qv[ht][KS + j], sc[tt][ht]);
+                for (int ht = 0; ht < HT; ++ht) {
+                    sc[0][ht] = T::mma32(k0, qv[ht][j], sc[0][ht]);
+                    sc[1][ht] = T::mma32(k1, qv[ht][j], sc[1][ht]);
                 }
             }
             V8 pb[HT], pl[HT];
@@ -200,17 +219,38 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
                     }
                 l_run[ht] += psum;
             }
+            // O^T += C^T . P^T, two latent tiles at a time: the transpose reads of the
+            // next pair are issued before this pair's MFMAs, and the hi / lo MFMAs of the
+            // two tiles alternate so no MFMA waits on the one just issued.
+            const uint16_t* c0 = pg + (2 * u) * KS * 512 + tr_lane;
+            const uint16_t* c1 = pg + (2 * u + 1) * KS * 512 + tr_lane;
+            auto tile_off = [](int rt) { return ((rt >> 1) * 4 + 2 * (rt & 1)) * 128; };
+            V8 ca[2], cn[2];
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const int blk = ((rt >> 1) * 4 + 2 * (rt & 1)) * 128;
-                const u32x2 lo = lds_read_tr16(pg + (2 * u) * KS * 512 + blk + tr_lane);
-                const u32x2 hi = lds_read_tr16(pg + (2 * u + 1) * KS * 512 + blk + tr_lane);
-                const V8 ca = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            for (int k = 0; k < 2; ++k) {
+                const u32x2 lo = lds_read_tr16(c0 + tile_off(k)), hi = lds_read_tr16(c1 + tile_off(k));
+                cn[k] = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; rt += 2) {
+                ca[0] = cn[0];
+                ca[1] = cn[1];
+                if (rt + 2 < RT) {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const u32x2 lo = lds_read_tr16(c0 + tile_off(rt + 2 + k));
+                        const u32x2 hi = lds_read_tr16(c1 + tile_off(rt + 2 + k));
+                        cn[k] = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                    }
+                }
 #pragma unroll
                 for (int ht = 0; ht < HT; ++ht) {
-                    acc[rt][ht] = T::mma32(ca, pb[ht], acc[rt][ht]);
-                    if constexpr (T::split_p)
-                        acc[rt][ht] = T::mma32(ca, pl[ht], acc[rt][ht]);
+                    acc[rt][ht] = T::mma32(ca[0], pb[ht], acc[rt][ht]);
+                    acc[rt + 1][ht] = T::mma32(ca[1], pb[ht], acc[rt + 1][ht]);
+                    if constexpr (T::split_p) {
+                        acc[rt][ht] = T::mma32(ca[0], pl[ht], acc[rt][ht]);
+                        acc[rt + 1][ht] = T::mma32(ca[1], pl[ht], acc[rt + 1][ht]);
+                    }
                 }
             }
         }
@@ -219,20 +259,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     // Page p of the item lives in buf0 when (p - p_begin) is even, buf1 when odd.  Each
     // round: wait for this page's loads, barrier, issue the next page into the other
     // buffer (its readers finished before the previous barrier), consume, barrier.
-    for (int p = p_begin; p < p_end; p += 2) {
+    for (int p = p_begin; p < p_end; ++p) {
+        const bool odd = (p - p_begin) & 1;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of page p landed
         __syncthreads();
         if (p + 1 < p_end)
-            issue_page(p + 1, buf1);
-        compute_page(buf0, p);
-        __syncthreads();
-        if (p + 1 >= p_end)
-            break;
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-        __syncthreads();
-        if (p + 2 < p_end)
-            issue_page(p + 2, buf0);
-        compute_page(buf1, p + 1);
+            issue_page(p + 1, odd ? buf0 : buf1);
+        compute_page(odd ? buf1 : buf0, p);
         __syncthreads();
     }
 
