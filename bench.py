@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="seconds of CPU work per baseline leg (all threads, then 1 thread)")
     ap.add_argument("--flags", type=int, default=0)
+    ap.add_argument("--only", choices=["config2", "config4", "config5"], default=None,
+                    help="run only this secondary leg and print its JSON (for profiling)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
     return ap.parse_args()
@@ -288,6 +290,12 @@ def main():
     if args.copy_probe_mib > 0:
         copy_probe(torch, args.copy_probe_mib)
     from cpp_inference_train_engine_amd.workloads import MLA36M, model_params
+    if args.only:
+        legs = {"config2": lambda: config2_leg(mla, model_params(MLA36M, seed=0)),
+                "config4": lambda: config4_leg(mla, torch),
+                "config5": lambda: config5_leg(mla, torch)}
+        print(json.dumps({args.only: legs[args.only]()}), flush=True)
+        return
     t_gen = time.perf_counter()
     batch = ragged_decode_batch(B=args.sessions, n_layers=N_LAYERS, seed=0)
     params = model_params(MLA36M, seed=0)

@@ -63,9 +63,13 @@ __device__ int upper_index(const int32_t* a, int n, long long x) {
     return lo;
 }
 
-// Prefix arrays are mirrored in LDS for batches up to kMetaLdsCap sessions so the
-// per-entry lookups and binary searches below never wait on global memory.
+// For batches up to kMetaLdsCap sessions the per-session inputs and prefix arrays live
+// in LDS, and so does the padded page table when it has at most kMetaPtCap entries, so
+// the build waits on global memory twice (the session inputs, then the page ids) and
+// every later lookup and binary search reads LDS.
 constexpr int kMetaLdsCap = 4096;
+constexpr int kMetaPtCap = 16384;
+constexpr int kMetaUnroll = 4;  // page-table entries whose loads a thread issues together
 
 __device__ void write_error(const MetadataArgs& a, int session) {
     for (int w = threadIdx.x; w < a.max_work; w += kMetaThreads)
@@ -78,41 +82,105 @@ __device__ void write_error(const MetadataArgs& a, int session) {
     }
 }
 
+// ceil(x / d) for x >= 0 and d >= 1, in 32-bit arithmetic when both are below 2^31.
+__device__ __forceinline__ long long ceil_div_nn(long long x, long long d) {
+    if (x < 0x80000000LL && d < 0x80000000LL)
+        return (long long)(((uint32_t)x + (uint32_t)(d - 1)) / (uint32_t)d);
+    return (x + d - 1) / d;
+}
+
+// L: the batch fits the LDS mirrors (B <= kMetaLdsCap); the compiler then reads them
+// with LDS instructions rather than flat loads.
+template <bool L>
 __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataArgs a) {
+    constexpr int CAP = L ? kMetaLdsCap : 1, PT = L ? kMetaPtCap : 1;
     __shared__ long long lds[3 * kMetaWaves];
     __shared__ long long carry[3];
     __shared__ int err;
-    __shared__ int32_t s_cup[kMetaLdsCap + 1], s_cuq[kMetaLdsCap + 1], s_cus[kMetaLdsCap + 1];
+    __shared__ int32_t s_cup[CAP + 1], s_cuq[CAP + 1], s_cus[CAP + 1];
+    __shared__ int32_t s_q[CAP], s_ctx[CAP], s_pt[PT];
     const int tid = threadIdx.x;
-    const bool in_lds = a.B <= kMetaLdsCap;
-    const int32_t* cup = in_lds ? s_cup : a.cu_pages;
-    const int32_t* cuq = in_lds ? s_cuq : a.cu_seqlens_q;
-    const int32_t* cus = in_lds ? s_cus : a.cu_splits;
+    constexpr bool in_lds = L;
+    const long long entries = (long long)a.B * a.max_pages;
+    const bool pt_lds = L && entries <= kMetaPtCap;
+    const int32_t* __restrict__ qlen = L ? s_q : a.q_len;
+    const int32_t* __restrict__ ctxl = L ? s_ctx : a.ctx_len;
+    const int32_t* cup = L ? s_cup : a.cu_pages;
+    const int32_t* cuq = L ? s_cuq : a.cu_seqlens_q;
+    const int32_t* cus = L ? s_cus : a.cu_splits;
     if (tid == 0) {
         carry[0] = carry[1] = carry[2] = 0;
         err = INT_MAX;
         a.cu_seqlens_q[0] = 0;
         a.cu_seqlens_k[0] = 0;
         a.cu_splits[0] = 0;
-        if (in_lds) {
+        if (L) {
             s_cuq[0] = 0;
             s_cus[0] = 0;
         }
     }
     if (in_lds)
-        for (int b = tid; b <= a.B; b += kMetaThreads)
-            s_cup[b] = a.cu_pages[b];
+        for (int b = tid; b <= a.B; b += kMetaThreads) {
+            const int32_t cp = a.cu_pages[b];
+            const int32_t q = b < a.B ? a.q_len[b] : 0, c = b < a.B ? a.ctx_len[b] : 0;
+            s_cup[b] = cp;
+            if (b < a.B) {
+                s_q[b] = q;
+                s_ctx[b] = c;
+            }
+        }
     __syncthreads();
-    // Phase 1: cu_seqlens_q/k, validation, total pages of sessions with queries.
+    // Phase 1: padded page table and page-id validation (a session listing more than
+    // max_pages pages is invalid anyway and only its first max_pages ids are read), then
+    // cu_seqlens_q/k, validation and the total pages of sessions with queries.
+    const bool small = entries <= INT_MAX;  // 32-bit index arithmetic
+    for (long long e0 = tid; e0 < entries; e0 += (long long)kMetaThreads * kMetaUnroll) {
+        int32_t pid[kMetaUnroll];
+        int bs[kMetaUnroll], js[kMetaUnroll];
+#pragma unroll
+        for (int k = 0; k < kMetaUnroll; ++k) {
+            const long long e = e0 + (long long)k * kMetaThreads;
+            pid[k] = -1;
+            bs[k] = -1;
+            js[k] = 0;
+            if (e < entries) {
+                if (small) {
+                    bs[k] = (int)e / a.max_pages;
+                    js[k] = (int)e - bs[k] * a.max_pages;
+                } else {
+                    bs[k] = (int)(e / a.max_pages);
+                    js[k] = (int)(e % a.max_pages);
+                }
+                if (js[k] < cup[bs[k] + 1] - cup[bs[k]])
+                    pid[k] = a.page_ids[cup[bs[k]] + js[k]];
+                else
+                    bs[k] = -2;  // padding entry
+            }
+        }
+        int bad_b = INT_MAX;
+#pragma unroll
+        for (int k = 0; k < kMetaUnroll; ++k) {
+            const long long e = e0 + (long long)k * kMetaThreads;
+            if (bs[k] == -1)
+                continue;  // past the table
+            if (bs[k] >= 0 && (pid[k] < 0 || pid[k] >= a.num_pool_pages))
+                bad_b = min(bad_b, bs[k]);
+            a.page_table[e] = pid[k];
+            if (pt_lds)
+                s_pt[e] = pid[k];
+        }
+        if (bad_b != INT_MAX)
+            atomicMin(&err, bad_b);
+    }
     for (int base = 0; base < a.B; base += kMetaThreads) {
         const int b = base + tid;
         long long v[3] = {0, 0, 0}, tot[3];
         int bad = 0;
         if (b < a.B) {
-            const long long q = a.q_len[b], ctx = a.ctx_len[b];
+            const long long q = qlen[b], ctx = ctxl[b];
             const long long npages = (long long)cup[b + 1] - cup[b];
             const long long kl = ctx + q;
-            const long long need = (kl + a.page_size - 1) / a.page_size;
+            const long long need = kl < 0 ? 0 : ceil_div_nn(kl, a.page_size);
             bad = q < 0 || ctx < 0 || npages < 0 || npages > a.max_pages || need > npages;
             v[0] = q;
             v[1] = kl;
@@ -134,22 +202,6 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
                 carry[k] += tot[k];
         __syncthreads();
     }
-    // Phase 1b: padded page table and page-id validation, one entry per thread
-    // (a session listing more than max_pages pages is already invalid and only its
-    // first max_pages ids are read).
-    const long long entries = (long long)a.B * a.max_pages;
-    for (long long e = tid; e < entries; e += kMetaThreads) {
-        const int b = (int)(e / a.max_pages), j = (int)(e % a.max_pages);
-        const int npages = cup[b + 1] - cup[b];
-        int32_t pid = -1;
-        if (j < npages) {
-            pid = a.page_ids[cup[b] + j];
-            if (pid < 0 || pid >= a.num_pool_pages)
-                atomicMin(&err, b);
-        }
-        a.page_table[e] = pid;
-    }
-    __syncthreads();
     if (err != INT_MAX) {
         write_error(a, err);
         return;
@@ -169,10 +221,9 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
     for (int base = 0; base < a.B; base += kMetaThreads) {
         const int b = base + tid;
         long long v[3] = {0, 0, 0}, tot[3];
-        if (b < a.B && a.q_len[b] > 0) {
-            const long long kl = (long long)a.ctx_len[b] + a.q_len[b];
-            const long long need = (kl + a.page_size - 1) / a.page_size;
-            v[0] = (need + split - 1) / split;
+        if (b < a.B && qlen[b] > 0) {
+            const long long kl = (long long)ctxl[b] + qlen[b];
+            v[0] = ceil_div_nn(ceil_div_nn(kl, a.page_size), split);
         }
         const long long ns = v[0];
         block_scan3(v, tot, lds);
@@ -205,7 +256,7 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         }
         const int b = upper_index(cus, a.B, w);
         const int sp = (int)(w - cus[b]);
-        const int kl = a.ctx_len[b] + a.q_len[b];
+        const int kl = ctxl[b] + qlen[b];
         const int need = (kl + a.page_size - 1) / a.page_size;
         const int p0 = (int)(sp * split);
         const int p1 = (int)(p0 + split < need ? p0 + split : need);
@@ -218,14 +269,18 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         d[4] = p1;
         d[5] = cus[b + 1] - cus[b];
         d[6] = cus[b];
-        d[7] = a.q_len[b];
+        d[7] = qlen[b];
+#pragma unroll
         for (int j = 0; j < kWorkPages; ++j)
-            pg[j] = p0 + j < p1 ? a.page_ids[cup[b] + p0 + j] : -1;
+            pg[j] = p0 + j < p1 ? (pt_lds ? s_pt[(long long)b * a.max_pages + p0 + j]
+                                          : a.page_ids[cup[b] + p0 + j])
+                                : -1;
     }
     for (long long i = tid; i < total_q; i += kMetaThreads) {
         const int b = upper_index(cuq, a.B, i);
-        const long long pos = (long long)a.ctx_len[b] + (i - cuq[b]);
-        const int32_t page = a.page_ids[cup[b] + pos / a.page_size];
+        const long long pos = (long long)ctxl[b] + (i - cuq[b]);
+        const long long j = pos / a.page_size;
+        const int32_t page = pt_lds ? s_pt[(long long)b * a.max_pages + j] : a.page_ids[cup[b] + j];
         a.slot_mapping[i] = (int32_t)(page * (long long)a.page_size + pos % a.page_size);
     }
     if (tid == 0) {
@@ -264,7 +319,11 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 }  // namespace
 
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(build_metadata_kernel, dim3(1), dim3(kMetaThreads), 0, stream, a);
+    if (a.B <= kMetaLdsCap)
+        hipLaunchKernelGGL(build_metadata_kernel<true>, dim3(1), dim3(kMetaThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL(build_metadata_kernel<false>, dim3(1), dim3(kMetaThreads), 0, stream,
+                           a);
     return hipGetLastError();
 }
 

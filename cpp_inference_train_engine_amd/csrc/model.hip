@@ -156,31 +156,39 @@ __device__ __forceinline__ void mma_steps(floatx4 (&acc)[MT][NT], const BPre<NT,
 }
 
 // 1/rms of `rows` rows (ops.cpp:33-45: inv = 1/sqrt(mean(x^2) + eps)) from the
-// producer's per-tile partial sums of squares (n_tiles <= 64): four threads a row each
-// load every fourth tile at once (one round trip), then combine in a fixed order.
-// Threads [0, 4*rows) take part; rows is 16 or 64, so they fill whole waves.  Visible
-// to the workgroup after its next barrier.
-__device__ __forceinline__ void inv_rms_to_lds(const float* ss, int n_tiles, int K, float eps,
-                                               int row0, float* inv_s, int rows) {
-    const int t = threadIdx.x;
-    if (t < 4 * rows) {
-        const float* p = ss + (long long)(row0 + (t >> 2)) * n_tiles;
-        float v[16];
+// producer's per-tile partial sums of squares (n_tiles <= 64): TPR threads a row each
+// load every TPR-th tile, then combine in a fixed order.  Threads [0, TPR*rows) take
+// part (whole waves).  issue() goes before the kernel's operand loads and finish()
+// after its MFMAs, so the sums travel with the operands instead of delaying them by a
+// round trip; inv_s is visible after the next barrier.
+template <int TPR>
+struct RmsPrefetch {
+    static_assert(TPR >= 4 && TPR <= 16 && (TPR & (TPR - 1)) == 0, "threads per row");
+    static constexpr int kPer = 64 / TPR;
+    float v[kPer];
+    __device__ __forceinline__ void issue(const float* ss, int n_tiles, int row0, int rows) {
+        const int t = threadIdx.x;
+        const bool mine = t < TPR * rows;
+        const float* p = ss + (long long)(row0 + (mine ? t / TPR : 0)) * n_tiles;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int tile = (t & 3) + 4 * i;
-            v[i] = tile < n_tiles ? p[tile] : 0.0f;
+        for (int i = 0; i < kPer; ++i) {
+            const int tile = t % TPR + TPR * i;
+            v[i] = mine && tile < n_tiles ? p[tile] : 0.0f;
         }
+    }
+    __device__ __forceinline__ void finish(int K, float eps, float* inv_s, int rows) {
+        const int t = threadIdx.x;
         float sum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < kPer; ++i)
             sum += v[i];
-        sum += __shfl_xor(sum, 1, 4);
-        sum += __shfl_xor(sum, 2, 4);
-        if ((t & 3) == 0)
-            inv_s[t >> 2] = 1.0f / sqrtf(sum / (float)K + eps);
+#pragma unroll
+        for (int off = 1; off < TPR; off <<= 1)
+            sum += __shfl_xor(sum, off, TPR);
+        if (t < TPR * rows && t % TPR == 0)
+            inv_s[t / TPR] = 1.0f / sqrtf(sum / (float)K + eps);
     }
-}
+};
 
 // Split-K reduction through LDS `part` (kWaves*MT*NTW*64 floatx4).  Wave w computed K
 // group w % KG of tiles [(w / KG) * NTW, +NTW); after the barrier wave mt < MT sums all
@@ -284,19 +292,19 @@ constexpr int kQkvPad = 8;        // fp16 pad of the LDS A-operand rows
 
 // LDS layout of qkv_kernel (bytes), from the model dims.
 struct QkvLds {
-    int part, y, ya, qf, qn, inv, total;
+    int part, y, ya, qf, qn, total;
 };
 __host__ __device__ inline QkvLds qkv_lds(const ModelDims& m) {
     const int nt = max(m.q_pad, m.kvw_pad) / 16;
     const int ncol = max(m.q_pad, m.kvw_pad);
-    // The split-K partials are dead once y is summed, so ya / qf / qn / inv reuse them.
+    // The split-K partials are dead once y is summed, so ya / qf / qn reuse them.
     QkvLds l;
     l.part = 0;                                             // [8 waves][nt][64] floatx4
     l.ya = 0;                                               // [16][q_pad + pad] fp16
     l.qf = l.ya + kQkvRows * (m.q_pad + kQkvPad) * 2;       // [16][qk_pad + 4] fp32
     l.qn = l.qf + kQkvRows * (m.qk_pad + 4) * 4;            // [16][nope_pad + pad] fp16
-    l.inv = l.qn + kQkvRows * (m.nope_pad + kQkvPad) * 2;   // [16] fp32
-    l.y = max(kQkvWaves * nt * 64 * 16, l.inv + kQkvRows * 4);  // [16][ncol] fp32
+    const int end = l.qn + kQkvRows * (m.nope_pad + kQkvPad) * 2;
+    l.y = max(kQkvWaves * nt * 64 * 16, end);               // [16][ncol] fp32
     l.total = l.y + kQkvRows * ncol * 4;
     return l;
 }
@@ -321,7 +329,6 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     _Float16* ya = reinterpret_cast<_Float16*>(smem + lay.ya);
     float* qf = reinterpret_cast<float*>(smem + lay.qf);
     _Float16* qn = reinterpret_cast<_Float16*>(smem + lay.qn);
-    float* inv_s = reinterpret_cast<float*>(smem + lay.inv);
     __shared__ float inv_x[kQkvRows];
 
     const int h = blockIdx.x, row0 = blockIdx.y * kQkvRows;
@@ -330,7 +337,27 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     const int KT = m.d_pad / 32, q_tiles = m.q_pad / 16;
     const int nt0 = kv ? q_tiles : 0, ntv = kv ? m.kvw_pad / 16 : q_tiles;
     const int ncol = 16 * ntv, ldy = max(m.q_pad, m.kvw_pad);
-    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_x, kQkvRows);
+    __shared__ int32_t slot_s[kQkvRows];
+    RmsPrefetch<16> rms;
+    rms.issue(s.ss_x, m.d_pad / 16, row0, kQkvRows);
+    // Side inputs of the later phases travel with the GEMM operands: the norm weight of
+    // this thread's columns in the row-norm phase (32 threads a row, cols <= 256), the
+    // RoPE rotation of its first RoPE element, and (kv workgroup) the rows' cache slots.
+    const int nr = tid >> 5, nsub = tid & 31, ncols = kv ? m.kv_rank : m.q_rank;
+    const float* nwp = kv ? L.kv_norm : L.q_norm;
+    float nw[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int c = nsub + 32 * k;
+        nw[k] = c < ncols ? nwp[c] : 0.0f;
+    }
+    const int rhalf = m.rope / 2;
+    float2 rcs = {0.0f, 0.0f};
+    if (tid < kQkvRows * rhalf && row0 + tid / rhalf < s.B)
+        rcs = s.rope_rows[(long long)(row0 + tid / rhalf) * rhalf + tid % rhalf];
+    int32_t slot_pf = -1;
+    if (kv && tid < kQkvRows && row0 + tid < s.B)
+        slot_pf = s.slot_mapping[row0 + tid];
 
     // ---- GEMM 1: every operand of this wave in flight at once, chunk by chunk ----
     floatx4 acc[NT];
@@ -378,6 +405,9 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
             for (int j = 0; j < NT; ++j)
                 acc[j] = mma(a[kk], b[kk][j], acc[j]);
     }
+    rms.finish(m.d_model, m.eps, inv_x, kQkvRows);
+    if (kv && tid < kQkvRows)
+        slot_s[tid] = slot_pf;
 #pragma unroll
     for (int j = 0; j < NT; ++j)
         if (j < ntv)
@@ -398,52 +428,62 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     }
     __syncthreads();
 
-    // ---- row norms: q_norm over q_rank columns, or kv_norm over kv_rank ----
+    // ---- row norms: q_norm over q_rank columns (to the fp16 A operand), or kv_norm over
+    // kv_rank (in place); in the kv workgroup also the key's RoPE, in place ----
     {
-        const int r = tid >> 5, sub = tid & 31;  // 32 threads a row (512 threads, 16 rows)
-        const int cols = kv ? m.kv_rank : m.q_rank;
+        const int r = nr, sub = nsub;  // 32 threads a row (512 threads, 16 rows)
         float ss = 0.0f;
-        for (int c = sub; c < cols; c += 32) {
+        for (int c = sub; c < ncols; c += 32) {
             const float v = y[r * ldy + c];
             ss += v * v;
         }
         ss = sum32(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)cols + m.eps);  // ops.cpp:37-44
+        const float inv = 1.0f / sqrtf(ss / (float)ncols + m.eps);  // ops.cpp:37-44
         if (kv) {
-            if (sub == 0)
-                inv_s[r] = inv;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int c = sub + 32 * k;
+                if (c < m.kv_rank)
+                    y[r * ldy + c] = y[r * ldy + c] * inv * nw[k];
+            }
+            for (int e = tid; e < kQkvRows * rhalf; e += 64 * kQkvWaves) {
+                const int rr = e / rhalf, jp = 2 * (e % rhalf);
+                const float2 cs =
+                    e == tid ? rcs : s.rope_rows[(long long)(row0 + rr) * rhalf + e % rhalf];
+                float* yk = y + rr * ldy + m.kv_rank + jp;
+                const float a0 = yk[0], a1 = yk[1];
+                yk[0] = a0 * cs.x - a1 * cs.y;
+                yk[1] = a0 * cs.y + a1 * cs.x;
+            }
         } else {
-            for (int c = sub; c < m.q_pad; c += 32)
-                ya[r * (m.q_pad + kQkvPad) + c] =
-                    (_Float16)(c < m.q_rank ? y[r * ldy + c] * inv * L.q_norm[c] : 0.0f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int c = sub + 32 * k;
+                if (c < m.q_pad)
+                    ya[r * (m.q_pad + kQkvPad) + c] =
+                        (_Float16)(c < m.q_rank ? y[r * ldy + c] * inv * nw[k] : 0.0f);
+            }
         }
     }
     __syncthreads();
 
-    if (kv) {  // ---- kv_norm, RoPE of the key, rounding, append ----
+    if (kv) {  // ---- rounding, append ----
         const bool tiled = page_tiled(m.page_size, m.kv_rank, m.rope);
-        const int half = m.rope / 2, width = m.kv_rank + m.rope, per_row = m.kv_rank + half;
-        for (int e = tid; e < kQkvRows * per_row; e += 64 * kQkvWaves) {
-            const int r = e / per_row, c = e % per_row, row = row0 + r;
+        const int width = m.kv_rank + m.rope;
+        for (int e = tid; e < kQkvRows * width; e += 64 * kQkvWaves) {
+            const int r = e / width, c = e % width, row = row0 + r;
             if (row >= s.B)
                 continue;
-            const int slot = s.slot_mapping[row];
+            const int slot = slot_s[r];
             const int page = slot / m.page_size, off = slot % m.page_size;
             if (slot < 0 || page >= s.num_pool_pages)
                 continue;
             uint16_t* base = pool + (long long)page * m.page_size * width;
-            if (c < m.kv_rank) {
-                base[latent_word(tiled, off, c, m.page_size, m.kv_rank)] =
-                    F16::from_float(y[r * ldy + c] * inv_s[r] * L.kv_norm[c]);
-            } else {
-                const int j2 = c - m.kv_rank, jp = 2 * j2;
-                const float2 cs = s.rope_rows[(long long)row * half + j2];
-                const float a0 = y[r * ldy + m.kv_rank + jp], a1 = y[r * ldy + m.kv_rank + jp + 1];
-                base[rope_word(tiled, off, jp, m.page_size, m.kv_rank, m.rope)] =
-                    F16::from_float(a0 * cs.x - a1 * cs.y);
-                base[rope_word(tiled, off, jp + 1, m.page_size, m.kv_rank, m.rope)] =
-                    F16::from_float(a0 * cs.y + a1 * cs.x);
-            }
+            const uint16_t v = F16::from_float(y[r * ldy + c]);
+            if (c < m.kv_rank)
+                base[latent_word(tiled, off, c, m.page_size, m.kv_rank)] = v;
+            else
+                base[rope_word(tiled, off, c - m.kv_rank, m.page_size, m.kv_rank, m.rope)] = v;
         }
         return;
     }
@@ -463,12 +503,12 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     }
     __syncthreads();
     {   // RoPE of the rope columns (pairs adjacent, ops.cpp:88-108) -> q_rope; q_nope -> fp16
-        const int half = m.rope / 2, ldq = m.nope_pad + kQkvPad;
+        const int half = rhalf, ldq = m.nope_pad + kQkvPad;
         for (int e = tid; e < kQkvRows * half; e += 64 * kQkvWaves) {
             const int r = e / half, j2 = e % half, jp = 2 * j2, row = row0 + r;
             if (row >= s.B)
                 continue;
-            const float2 cs = s.rope_rows[(long long)row * half + j2];
+            const float2 cs = e == tid ? rcs : s.rope_rows[(long long)row * half + j2];
             const float a0 = qf[r * (m.qk_pad + 4) + m.nope + jp];
             const float a1 = qf[r * (m.qk_pad + 4) + m.nope + jp + 1];
             uint16_t* qr = s.q_rope + ((long long)row * m.H + h) * m.rope;
@@ -594,7 +634,8 @@ __global__ __launch_bounds__(64 * kWaves) void g5_kernel(StepArgs s, LayerWeight
     const int row0 = blockIdx.y * 16, p = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32;
-    inv_rms_to_lds(s.ss_res, m.d_pad / 16, m.d_model, m.eps, row0, inv_s, 16);
+    RmsPrefetch<16> rms;
+    rms.issue(s.ss_res, m.d_pad / 16, row0, 16);
     BPre<2, KW> bw;
     bw.load(L.w_gate_up, 2 * p, 2, KT, wave, kWaves, lane);
     APre16<KW, 1> a;
@@ -602,6 +643,7 @@ __global__ __launch_bounds__(64 * kWaves) void g5_kernel(StepArgs s, LayerWeight
     floatx4 acc[1][2];
     zero(acc);
     mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
+    rms.finish(m.d_model, m.eps, inv_s, 16);
     int mt;
     floatx4 v[2];
     if (!splitk_reduce<1, 2, kWaves>(acc, part, mt, v))
@@ -635,7 +677,8 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32, kg = wave % kG7KG, ng = wave / kG7KG;
     const int n_tiles = m.vocab_pad / 16, nt0 = blockIdx.x * kG7Tiles;
-    inv_rms_to_lds(s.ss_x, m.d_pad / 16, m.d_model, m.eps, row0, inv_s, 64);
+    RmsPrefetch<8> rms;
+    rms.issue(s.ss_x, m.d_pad / 16, row0, 64);
     BPre<NTW, KW> bw;
     bw.load(s.embed, nt0 + ng * NTW, min(NTW, n_tiles - nt0 - ng * NTW), KT, kg, kG7KG, lane);
     APre16<KW, 4> a;
@@ -643,6 +686,7 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
     floatx4 acc[4][NTW];
     zero(acc);
     mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
+    rms.finish(m.d_model, m.eps, inv_s, 64);
     int mt;
     floatx4 v[kG7Tiles];
     if (!splitk_reduce<4, NTW, kG7KG>(acc, part, mt, v))
