@@ -50,23 +50,28 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-constexpr int kPfWaves = 4;
+constexpr float kPfNoMax = -1.0e30f;  // running-max floor: below every real score
+constexpr float kPfRescale = 8.0f;    // log2 headroom before the running max is raised
+constexpr int kPfQG = 2;        // q-groups per workgroup (QT 16-row tiles each)
+constexpr int kPfKH = 2;        // token halves: the two waves of a q-group split each page
+constexpr int kPfWaves = kPfQG * kPfKH;
+constexpr int kPfMaxIds = 2048;  // page ids staged in LDS: sessions up to 2048 pages
 
 template <typename T, int KV, int RP, int PS, int QT>
-__global__ __launch_bounds__(64 * kPfWaves) void prefill_page_kernel(PrefillArgs a) {
-    static_assert(KV % 32 == 0 && RP % 8 == 0 && RP <= 32 && PS % 32 == 0, "tile shape");
+__global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void prefill_page_kernel(PrefillArgs a) {
+    static_assert(KV % 32 == 0 && RP % 8 == 0 && RP <= 32 && PS == 64, "tile shape");
     constexpr int KS = KV / 32;               // latent k-steps of the score MFMAs
-    constexpr int TT = PS / 16;               // 16-token tiles per page
-    constexpr int UPP = PS / 32;              // 32-token k-steps of O^T per page
     constexpr int RT = KV / 16;               // 16-row (latent) tiles of O^T
     constexpr int REC = PS * (KV + RP);       // words of a page record
     constexpr int CHUNKS = REC / 8;           // 16-byte chunks of a record
     constexpr int THREADS = 64 * kPfWaves;
-    constexpr int CPT = (CHUNKS + THREADS - 1) / THREADS;
-    constexpr int WG_ROWS = kPfWaves * QT * 16;
-    static_assert(KV % 16 == 0 && (PS * KV) % 8 == 0, "record chunks");
+    constexpr int CPT = (CHUNKS + THREADS - 1) / THREADS;  // chunks per thread and page
+    constexpr int WG_ROWS = kPfQG * QT * 16;
     using V8 = typename T::vec8;
-    __shared__ __attribute__((aligned(16))) uint16_t buf[2][REC];
+    __shared__ __attribute__((aligned(16))) uint16_t buf0[REC];
+    __shared__ __attribute__((aligned(16))) uint16_t buf1[REC];
+    __shared__ int32_t pids[kPfMaxIds];
 
     const int b = blockIdx.y;
     if (a.info[0] <= 0)
@@ -81,46 +86,60 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_page_kernel(PrefillArgs
         return;
     const int ctx = k_len - q_len;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
-    const int wave = tid >> 6;
+    const int wave = tid >> 6, qg = wave >> 1, kh = wave & 1;
     // keys [0, k_hi) are visible to some q-row of this workgroup
     const int last_q = min(n_rows - 1, rb + WG_ROWS - 1) / H;
     const int k_hi = ctx + last_q + 1;
     const int n_pages = (k_hi + PS - 1) / PS;
     const int32_t* ptab = a.page_table + (long long)b * a.max_pages;
 
-    // ---- page staging: 16-byte chunks, slots at or past k_len zeroed ----
-    u32x4 stage[CPT];
-    auto load_page = [&](int p) {
-        const int page = ptab[p];
-        const bool ok = (unsigned)page < (unsigned)a.num_pool_pages;
-        const uint16_t* base = a.pages + (long long)(ok ? page : 0) * REC;
-        const int tok0 = p * PS;
+    // ---- page staging: 16-byte chunks through registers, slots at or past k_len zeroed.
+    // Two register sets hold pages p+1 and p+2 while page p is consumed from LDS.
+    // Raw buffer loads over the page record: a chunk that must read as zero (slot at or
+    // past k_len, an invalid page id, or p >= n_pages) gets an offset outside the record,
+    // which the hardware returns as zero.  Every load is issued unconditionally, so no
+    // register merges (and no early waits) appear between the loads and their use.
+    auto load_page = [&](u32x4 (&st)[CPT], int page_id, int p) {
+        const int page = __builtin_amdgcn_readfirstlane(page_id);  // uniform: scalar rsrc
+        const bool ok = (unsigned)page < (unsigned)a.num_pool_pages && p < n_pages;
+        const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(a.pages + (long long)(ok ? page : 0) * REC), 0, REC * 2,
+            0x00020000);
+        const int valid = ok ? k_len - p * PS : 0;  // slots of the page that hold keys
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
             const int c = tid + k * THREADS;
-            stage[k] = u32x4{0, 0, 0, 0};
-            if (c < CHUNKS) {
+            bool live = c < CHUNKS && valid > 0;
+            if (valid < PS) {  // the session's last page (or nothing to load)
                 // slot of chunk c: latent chunks run (t, j, g, n), rope chunks (t, ch, n)
                 const int slot = c < PS * KV / 8 ? (c / (16 * 4 * KS)) * 16 + (c & 15)
                                                  : ((c - PS * KV / 8) / (16 * (RP / 8))) * 16 +
                                                        (c & 15);
-                if (ok && tok0 + slot < k_len)
-                    stage[k] = __builtin_nontemporal_load(
-                        reinterpret_cast<const u32x4*>(base + (long long)c * 8));
+                live = live && slot < valid;
             }
+            st[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rsrc, live ? c * 16 : 0x40000000, 0, 0));
         }
     };
-    auto store_page = [&](uint16_t* dst) {
+    auto store_page = [&](const u32x4 (&st)[CPT], uint16_t* dst) {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
             const int c = tid + k * THREADS;
             if (c < CHUNKS)
-                *reinterpret_cast<u32x4*>(dst + c * 8) = stage[k];
+                *reinterpret_cast<u32x4*>(dst + c * 8) = st[k];
         }
     };
-
-    // ---- this wave's q-tiles: Q^T operands, causal limits ----
-    const int wr0 = rb + wave * QT * 16;  // first session q-row of the wave
+    // Prologue, in issue order: the page ids (staged in LDS, so issuing a later page
+    // never waits on memory), the Q operands, then the first two pages.
+    const int id0 = ptab[0], id1 = n_pages > 1 ? ptab[1] : 0;
+    constexpr int IDS_PT = kPfMaxIds / THREADS;
+    int ids[IDS_PT];
+#pragma unroll
+    for (int k = 0; k < IDS_PT; ++k) {
+        const int i = tid + k * THREADS;
+        ids[k] = i < n_pages ? ptab[i] : 0;
+    }
+    const int wr0 = rb + qg * QT * 16;  // first session q-row of the wave
     V8 qv[QT][KS + 1];
     int lim[QT];  // lane's q-row n sees keys [0, lim]; -1 = no such row
     const bool rope_lane = 8 * g < RP;
@@ -138,128 +157,182 @@ __global__ __launch_bounds__(64 * kPfWaves) void prefill_page_kernel(PrefillArgs
                         ? *reinterpret_cast<const V8*>(a.q_rope + fr * RP + 8 * g)
                         : V8{};
     }
+    u32x4 st0[CPT], st1[CPT];
+    load_page(st0, id0, 0);
+    load_page(st1, id1, 1);
+#pragma unroll
+    for (int k = 0; k < IDS_PT; ++k)
+        pids[tid + k * THREADS] = ids[k];
+    store_page(st0, buf0);
+    __syncthreads();
     const int rope_off = (16 * (rope_lane ? g : g % (RP / 8)) + n) * 8;
     // transpose-read address of lane (g, j=n) inside a token tile: token 4g + n/4,
     // latent 4*(n%4) + (row-tile offset)
     const int tr_lane = (((n & 3) >> 1) * 128) + (4 * g + (n >> 2)) * 8 + 4 * (n & 1);
 
+    // The lowest causal limit of the wave's rows (-1 when some row is past the chunk).
+    const int lim_min = wr0 + QT * 16 <= n_rows ? ctx + wr0 / H : -1;
     float m_run[QT], l_run[QT];
     floatx4 acc[QT][RT];
 #pragma unroll
     for (int q = 0; q < QT; ++q) {
-        m_run[q] = -INFINITY;
+        m_run[q] = kPfNoMax;
         l_run[q] = 0.0f;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
             acc[q][rt] = floatx4{0, 0, 0, 0};
     }
 
-    load_page(0);
-    store_page(buf[0]);
-    __syncthreads();
-    for (int p = 0; p < n_pages; ++p) {
-        const bool more = p + 1 < n_pages;
-        if (more)
-            load_page(p + 1);  // in flight while this page is consumed
-        const uint16_t* pg = buf[p & 1];
-        const int tok0 = p * PS;
-        // S^T tiles
-        floatx4 sc[TT][QT];
+    // Scores, mask, online softmax and PV of this wave's token half of page p.
+    auto compute = [&](const uint16_t* pg, int p) {
+        const int tok0 = p * PS + 32 * kh;
+        floatx4 sc[2][QT];
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = 2 * kh + tt;
 #pragma unroll
             for (int q = 0; q < QT; ++q)
-                sc[t][q] = floatx4{0, 0, 0, 0};
+                sc[tt][q] = floatx4{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
                 const V8 ka = *reinterpret_cast<const V8*>(pg + (t * KS + j) * 512 + lane * 8);
 #pragma unroll
                 for (int q = 0; q < QT; ++q)
-                    sc[t][q] = T::mma32(ka, qv[q][j], sc[t][q]);
+                    sc[tt][q] = T::mma32(ka, qv[q][j], sc[tt][q]);
             }
             const V8 kr =
                 *reinterpret_cast<const V8*>(pg + PS * KV + t * (RP / 8) * 128 + rope_off);
 #pragma unroll
             for (int q = 0; q < QT; ++q)
-                sc[t][q] = T::mma32(kr, qv[q][KS], sc[t][q]);
+                sc[tt][q] = T::mma32(kr, qv[q][KS], sc[tt][q]);
         }
-        // mask + online softmax per q-row (lane column n)
-        V8 pb[QT][UPP], pl[QT][UPP];  // P^T operands (pl: the low part, bf16 only)
+        V8 pb[QT], pl[QT];  // P^T operands (pl: the low part, bf16 only)
+        // Every row of the wave sees all 32 tokens of this half unless it holds the
+        // causal edge (or rows past the chunk): only then are tokens masked.
+        const bool full = tok0 + 31 <= lim_min;
 #pragma unroll
         for (int q = 0; q < QT; ++q) {
-            float mp = -INFINITY;
+            float mp = -INFINITY;  // raw score units (the scale is > 0)
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int tok = tok0 + 16 * t + 4 * g + i;
-                    const float x = tok <= lim[q] ? sc[t][q][i] * a.scale_log2 : -INFINITY;
-                    sc[t][q][i] = x;
-                    mp = fmaxf(mp, x);
+                    if (!full && tok0 + 16 * tt + 4 * g + i > lim[q])
+                        sc[tt][q][i] = -INFINITY;
+                    mp = fmaxf(mp, sc[tt][q][i]);
                 }
             mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
             mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
-            const float m_new = fmaxf(m_run[q], mp);
-            if (m_new > m_run[q]) {
-                const float alpha = m_run[q] == -INFINITY ? 0.0f : exp2_fast(m_run[q] - m_new);
+            // log2 units; m_run starts at a finite floor, so exp2 never sees inf - inf.
+            // The reference max is raised only when a row's max exceeds it by more than
+            // kPfRescale (then the state is rescaled); below that the probabilities are
+            // exp2(x - m_run) <= 2^kPfRescale, exact in fp32 and fp16, and the final
+            // normalisation divides by the same-based sum.
+            const float m_new = fmaxf(m_run[q], mp * a.scale_log2);
+            if (__builtin_amdgcn_ballot_w64(m_new > m_run[q] + kPfRescale)) {
+                const float alpha = exp2_fast(m_run[q] - m_new);
                 l_run[q] *= alpha;
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt)
                     acc[q][rt] *= alpha;
                 m_run[q] = m_new;
             }
+            const float m_ref = m_run[q];
             float psum = 0.0f;
 #pragma unroll
-            for (int t = 0; t < TT; ++t)
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float e = m_new == -INFINITY ? 0.0f : exp2_fast(sc[t][q][i] - m_new);
+                    const float e = exp2_fast(fmaf(sc[tt][q][i], a.scale_log2, -m_ref));
                     psum += e;
                     const auto hi = static_cast<typename T::scalar>(e);
-                    pb[q][t / 2][4 * (t % 2) + i] = hi;
+                    pb[q][4 * tt + i] = hi;
                     if constexpr (T::split_p)
-                        pl[q][t / 2][4 * (t % 2) + i] =
+                        pl[q][4 * tt + i] =
                             static_cast<typename T::scalar>(e - static_cast<float>(hi));
                 }
             l_run[q] += psum;  // per lane; summed over the 4 lane groups at the end
         }
-        // O^T += C^T . P^T
+        // O^T += C^T . P^T over the 32 tokens of this half (one K-step)
 #pragma unroll
-        for (int u = 0; u < UPP; ++u)
+        for (int rt = 0; rt < RT; ++rt) {
+            const int blk = ((rt >> 1) * 4 + 2 * (rt & 1)) * 128;  // latent rows 16rt..
+            const u32x2 lo = lds_read_tr16(pg + (2 * kh) * KS * 512 + blk + tr_lane);
+            const u32x2 hi = lds_read_tr16(pg + (2 * kh + 1) * KS * 512 + blk + tr_lane);
+            const V8 ca = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const int blk = ((rt >> 1) * 4 + 2 * (rt & 1)) * 128;  // latent rows 16rt..
-                const u32x2 lo = lds_read_tr16(pg + (2 * u) * KS * 512 + blk + tr_lane);
-                const u32x2 hi = lds_read_tr16(pg + (2 * u + 1) * KS * 512 + blk + tr_lane);
-                const V8 ca = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-#pragma unroll
-                for (int q = 0; q < QT; ++q) {
-                    acc[q][rt] = T::mma32(ca, pb[q][u], acc[q][rt]);
-                    if constexpr (T::split_p)
-                        acc[q][rt] = T::mma32(ca, pl[q][u], acc[q][rt]);
-                }
+            for (int q = 0; q < QT; ++q) {
+                acc[q][rt] = T::mma32(ca, pb[q], acc[q][rt]);
+                if constexpr (T::split_p)
+                    acc[q][rt] = T::mma32(ca, pl[q], acc[q][rt]);
             }
-        if (more)
-            store_page(buf[(p + 1) & 1]);  // last read of that buffer was before the barrier
+        }
+    };
+    // Page p lives in buf[p % 2]; its successor waits in st[(p + 1) % 2].  One step:
+    // send page p+2 into the register set page p came through, consume page p, store
+    // page p+1 into the other buffer (its last readers finished before the previous
+    // barrier), barrier.  Steps are unrolled in pairs so every buffer and register set
+    // is named statically.
+    auto step = [&](const uint16_t* cur, uint16_t* nx, u32x4 (&st_next)[CPT],
+                    u32x4 (&st_far)[CPT], int p) {
+        load_page(st_far, pids[min(p + 2, n_pages - 1)], p + 2);
+        compute(cur, p);
+        if (p + 1 < n_pages)
+            store_page(st_next, nx);
         __syncthreads();
+    };
+    for (int p = 0; p < n_pages; p += 2) {
+        step(buf0, buf1, st1, st0, p);
+        if (p + 1 >= n_pages)
+            break;
+        step(buf1, buf0, st0, st1, p + 1);
     }
 
-    // ---- normalise and store ----
+    // ---- the two token halves of each q-group meet in LDS; normalise and store ----
 #pragma unroll
     for (int q = 0; q < QT; ++q) {
-        float l = l_run[q];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        l_run[q] += __shfl_xor(l_run[q], 16, 64);
+        l_run[q] += __shfl_xor(l_run[q], 32, 64);
+    }
+    __syncthreads();  // every wave is done with the page buffers
+    static_assert((QT * RT * 256 + QT * 128) * 4 <= REC * 2, "exchange fits a page buffer");
+    float* xo = reinterpret_cast<float*>(qg == 0 ? buf0 : buf1);
+    if (kh == 1) {
+#pragma unroll
+        for (int q = 0; q < QT; ++q) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                *reinterpret_cast<floatx4*>(xo + ((q * RT + rt) * 64 + lane) * 4) = acc[q][rt];
+            if (g == 0) {
+                xo[QT * RT * 256 + q * 128 + n] = m_run[q];
+                xo[QT * RT * 256 + q * 128 + 64 + n] = l_run[q];
+            }
+        }
+    }
+    __syncthreads();
+    if (kh == 1)
+        return;
+#pragma unroll
+    for (int q = 0; q < QT; ++q) {
+        const float m1 = xo[QT * RT * 256 + q * 128 + n];
+        const float l1 = xo[QT * RT * 256 + q * 128 + 64 + n];
+        const float M = fmaxf(m_run[q], m1);
+        const float f0 = exp2_fast(m_run[q] - M), f1 = exp2_fast(m1 - M);
+        const float l = l_run[q] * f0 + l1 * f1;
         const int r = wr0 + q * 16 + n;
         if (r >= n_rows)
             continue;
         const long long fr = (long long)q0 * H + r;
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-            *reinterpret_cast<floatx4*>(a.out + fr * KV + 16 * rt + 4 * g) = acc[q][rt] * inv;
+        for (int rt = 0; rt < RT; ++rt) {
+            const floatx4 o1 =
+                *reinterpret_cast<const floatx4*>(xo + ((q * RT + rt) * 64 + lane) * 4);
+            *reinterpret_cast<floatx4*>(a.out + fr * KV + 16 * rt + 4 * g) =
+                (acc[q][rt] * f0 + o1 * f1) * inv;
+        }
         if (a.lse && g == 0)
-            a.lse[fr] = (m_run[q] + __log2f(l)) * kLn2;
+            a.lse[fr] = (M + __log2f(l)) * kLn2;
     }
 }
 
@@ -371,7 +444,7 @@ constexpr int kPfQT = 2;
 
 template <typename T>
 hipError_t launch_prefill_page(const PrefillArgs& a, int max_q_len, hipStream_t stream) {
-    constexpr int rows = kPfWaves * kPfQT * 16;
+    constexpr int rows = kPfQG * kPfQT * 16;
     const long long gx = ((long long)max_q_len * a.H + rows - 1) / rows;
     hipLaunchKernelGGL((prefill_page_kernel<T, 128, 16, 64, kPfQT>), dim3((unsigned)gx, a.B),
                        dim3(64 * kPfWaves), 0, stream, a);
@@ -384,11 +457,17 @@ bool prefill_mfma_supported(int H, int kv_rank, int rope_dim, int page_size) {
     return H <= 16 && page_size == 64 && kv_rank == 128 && rope_dim == 16;
 }
 
+// The MFMA kernel stages a session's page ids in LDS (at most kPfMaxIds pages).
+static bool prefill_mfma_fits(const PrefillArgs& a) {
+    return prefill_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size) &&
+           a.max_pages <= kPfMaxIds;
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, int max_q_len, int dtype, bool force_generic,
                           hipStream_t stream) {
     if (a.B <= 0 || max_q_len < 2)
         return hipSuccess;
-    if (!force_generic && prefill_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size))
+    if (!force_generic && prefill_mfma_fits(a))
         return dtype == 0 ? launch_prefill_page<F16>(a, max_q_len, stream)
                           : launch_prefill_page<BF16>(a, max_q_len, stream);
     const size_t shmem = (a.kv_rank + a.rope_dim + kPgChunk + 8) * sizeof(float);

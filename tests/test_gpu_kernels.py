@@ -69,6 +69,37 @@ def test_metadata_bit_exact(gpu, orc, seed):
                                   want["work_pages"][:W])
 
 
+@pytest.mark.parametrize("B,max_pages", [(256, 64), (256, 65), (4096, 2), (4096, 5),
+                                         (4097, 2)])
+def test_metadata_lds_boundaries(gpu, orc, B, max_pages):
+    """The build keeps the session inputs in LDS up to 4096 sessions and the padded page
+    table up to 16384 entries: batches on both sides of each limit, bit-exact."""
+    rng = np.random.default_rng(B + max_pages)
+    ps = 64
+    need = rng.integers(1, max_pages + 1, B)  # pages per session, at most max_pages
+    ctx = (need - 1) * ps + rng.integers(0, ps, B)
+    q = np.ones(B, np.int64)
+    need = (ctx + q + ps - 1) // ps
+    ctx = np.where(need > max_pages, ctx - ps, ctx)  # keep ctx + q within max_pages pages
+    need = (ctx + q + ps - 1) // ps
+    cu_pages = np.concatenate([[0], np.cumsum(need)])
+    P = int(need.sum()) + 3
+    ids = rng.permutation(P)[:int(need.sum())]
+    _say(f"metadata boundary B={B} max_pages={max_pages} entries={B * max_pages}")
+    want = orc.build_metadata(ctx, q, cu_pages, ids, ps, max_pages, P, 1, 512, 65535)
+    rb = _gpu_metadata(gpu, ctx, q, cu_pages, ids, ps, max_pages, P, 1, 512, 65535, 1 << 16)
+    assert rb.read_info() == want["info"].tolist()
+    W, total_q = want["info"][0], want["info"][2]
+    for k, n in (("cu_splits", B + 1), ("work_session", W), ("slot_mapping", total_q)):
+        np.testing.assert_array_equal(getattr(rb, k)[:n].cpu().numpy(), want[k][:n], err_msg=k)
+    np.testing.assert_array_equal(rb.page_table[:B * max_pages].cpu().numpy(),
+                                  want["page_table"].reshape(-1))
+    np.testing.assert_array_equal(rb.work_desc.cpu().numpy().reshape(-1, 8)[:W],
+                                  want["work_desc"][:W])
+    np.testing.assert_array_equal(rb.work_pages.cpu().numpy().reshape(-1, 8)[:W],
+                                  want["work_pages"][:W])
+
+
 @pytest.mark.parametrize("case", ["neg_q", "short_pages", "bad_id", "too_many_pages",
                                   "max_work", "max_rows"])
 def test_metadata_errors_match_oracle(gpu, orc, case):
