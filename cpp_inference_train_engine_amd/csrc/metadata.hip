@@ -69,7 +69,7 @@ __device__ int upper_index(const int32_t* a, int n, long long x) {
 // every later lookup and binary search reads LDS.
 constexpr int kMetaLdsCap = 4096;
 constexpr int kMetaPtCap = 16384;
-constexpr int kMetaUnroll = 4;  // page-table entries whose loads a thread issues together
+constexpr int kMetaUnroll = 16;  // page-table entries whose loads a thread issues together
 
 __device__ void write_error(const MetadataArgs& a, int session) {
     for (int w = threadIdx.x; w < a.max_work; w += kMetaThreads)
