@@ -212,7 +212,7 @@ void prefill_page_kernel(PrefillArgs a) {
         const bool full = tok0 + 31 <= lim_min;
 #pragma unroll
         for (int q = 0; q < QT; ++q) {
-            float mp = -INFINITY;  // raw score units (the scale is > 0)
+            float mp = -INFINITY;  // this lane's max, raw score units (the scale is > 0)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -221,15 +221,16 @@ void prefill_page_kernel(PrefillArgs a) {
                         sc[tt][q][i] = -INFINITY;
                     mp = fmaxf(mp, sc[tt][q][i]);
                 }
-            mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
-            mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
             // log2 units; m_run starts at a finite floor, so exp2 never sees inf - inf.
-            // The reference max is raised only when a row's max exceeds it by more than
-            // kPfRescale (then the state is rescaled); below that the probabilities are
-            // exp2(x - m_run) <= 2^kPfRescale, exact in fp32 and fp16, and the final
-            // normalisation divides by the same-based sum.
-            const float m_new = fmaxf(m_run[q], mp * a.scale_log2);
-            if (__builtin_amdgcn_ballot_w64(m_new > m_run[q] + kPfRescale)) {
+            // The reference max m_run is raised only when a score exceeds it by more than
+            // kPfRescale; below that the probabilities are exp2(x - m_run) <= 2^kPfRescale,
+            // exact in fp32 and fp16, and the final normalisation divides by the same-based
+            // sum.  Each lane checks its own scores, so the row max (a cross-lane
+            // reduction) is formed only on the rare pages that raise the reference.
+            if (__builtin_amdgcn_ballot_w64(mp * a.scale_log2 > m_run[q] + kPfRescale)) {
+                mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
+                mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+                const float m_new = fmaxf(m_run[q], mp * a.scale_log2);
                 const float alpha = exp2_fast(m_run[q] - m_new);
                 l_run[q] *= alpha;
 #pragma unroll

@@ -180,3 +180,20 @@ def test_prefill_leaves_decode_rows_alone(gpu, orc):
     dec_rows = np.concatenate([[0], np.cumsum(batch.q_len)])[2:-1]
     assert np.isnan(got[dec_rows]).all()
     _check(got[:80], want[:80], "prefill rows")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("max_pages", [2048, 2049])
+def test_prefill_wide_page_table(gpu, orc, max_pages):
+    """The MFMA kernel stages a session's page ids in LDS (up to 2048 pages per session);
+    a wider page table (max_pages 2049) takes the generic kernel.  Same results either way."""
+    import dataclasses
+    from cpp_inference_train_engine_amd.workloads import mixed_prefill_batch
+    batch = mixed_prefill_batch(n_prefill=2, chunk=70, max_prefill_ctx=300, n_decode=3,
+                                seed=5)
+    batch = dataclasses.replace(batch, max_pages=max_pages)
+    _say(f"prefill wide table max_pages={max_pages}")
+    got, lse = _run(gpu, batch)
+    want, want_lse = _oracle(orc, batch)
+    _check(got, want, f"max_pages={max_pages}")
+    np.testing.assert_allclose(lse, want_lse, rtol=1e-4, atol=1e-3)
