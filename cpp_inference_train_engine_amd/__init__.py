@@ -79,6 +79,11 @@ _SIGNATURES = {
     "mla_session_prefill": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
     "mla_session_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_uint16, C.c_void_p]),
     "mla_engine_step": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 5),
+    "mla_export_read_config": (C.c_int, [C.c_char_p, C.c_void_p]),
+    "mla_export_read": (C.c_int, [C.c_char_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    "mla_config_hash": (C.c_int, [C.c_void_p, C.c_char_p]),
+    "mla_model_load": (C.c_int, [C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
+    "mla_engine_load": (C.c_int, [C.c_char_p] + [C.c_int] * 4 + [C.c_void_p, C.c_void_p]),
 }
 
 
@@ -126,11 +131,13 @@ from .ops import (  # noqa: E402  (re-exported operator interface)
     PagedLatentCache, RaggedBatch, append_latent, build_metadata, decode_attention,
     decode_merge, decode_partials, decode_workspace, decode_workspace_bytes, prefill_attention)
 
-from .model import HipModel, ModelConfig, config_parameter_count, config_validate  # noqa: E402
+from .model import (HipModel, ModelConfig, config_hash, config_parameter_count,  # noqa: E402
+                    config_validate, read_export)
 from .engine import HipEngine, HipExecution, generate_tokens  # noqa: E402
 
 __all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
-           "decode_partials", "decode_merge", "prefill_attention", "HipModel", "HipEngine", "HipExecution", "generate_tokens", "ModelConfig", "config_validate",
-           "config_parameter_count",
+           "decode_partials", "decode_merge", "prefill_attention", "HipModel", "HipEngine",
+           "HipExecution", "generate_tokens", "ModelConfig", "config_validate",
+           "config_parameter_count", "config_hash", "read_export",
            "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",
            "DTYPE_BF16"]

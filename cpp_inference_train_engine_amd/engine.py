@@ -12,6 +12,7 @@ session on the same weights.  ``step`` batches several sessions into one GPU for
 from __future__ import annotations
 
 import ctypes as C
+import os
 
 import numpy as np
 
@@ -33,6 +34,19 @@ class HipEngine:
         check(lib().mla_engine_create(C.byref(cfg), params.ctypes.data, max_sessions, max_rows,
                                       num_pages, page_size, C.byref(h)))
         self._h = h
+
+    @classmethod
+    def load(cls, path: str, max_sessions: int = 16, max_rows: int = 1024,
+             num_pages: int = 1024, page_size: int = 64) -> "HipEngine":
+        """mla_engine_load: an engine over a model export or checkpoint directory
+        (load_checkpoint(path, training=false), src/train/checkpoint.cpp:186-324)."""
+        self = cls.__new__(cls)
+        self.cfg = ModelConfig()
+        h = C.c_void_p()
+        check(lib().mla_engine_load(os.fsencode(path), max_sessions, max_rows, num_pages,
+                                    page_size, C.byref(self.cfg), C.byref(h)))
+        self._h = h
+        return self
 
     @property
     def handle(self):

@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes as C
 import json
+import os
 
 from . import check, lib, ptr, stream_handle
 
@@ -50,6 +51,26 @@ def config_validate(cfg: ModelConfig) -> None:
     check(lib().mla_config_validate(C.byref(cfg)))
 
 
+def config_hash(cfg: ModelConfig) -> str:
+    """ModelConfig::hash (src/model/config.cpp:71-73): SHA-256 of the canonical JSON."""
+    out = C.create_string_buffer(65)
+    check(lib().mla_config_hash(C.byref(cfg), out))
+    return out.value.decode()
+
+
+def read_export(path: str):
+    """load_checkpoint(path, training=false) (src/train/checkpoint.cpp:186-324) of a model
+    export or checkpoint directory: (ModelConfig, fp32 parameters in registry order).
+    Raises MlaError with the reference's code and message when a check fails."""
+    import numpy as np
+    cfg = ModelConfig()
+    enc = os.fsencode(path)
+    check(lib().mla_export_read_config(enc, C.byref(cfg)))
+    params = np.empty(config_parameter_count(cfg), np.float32)
+    check(lib().mla_export_read(enc, C.byref(cfg), params.ctypes.data, params.size))
+    return cfg, params
+
+
 def config_parameter_count(cfg: ModelConfig) -> int:
     """ModelConfig::parameter_count (src/model/config.cpp:7-19)."""
     return int(lib().mla_config_parameter_count(C.byref(cfg)))
@@ -69,6 +90,17 @@ class HipModel:
         check(lib().mla_model_create(C.byref(cfg), params.ctypes.data, max_batch, page_size,
                                      C.byref(h)))
         self._h = h
+
+    @classmethod
+    def load(cls, path: str, max_batch: int, page_size: int = 64) -> "HipModel":
+        """mla_model_load: a model export or checkpoint directory straight to the device."""
+        self = cls.__new__(cls)
+        self.cfg, self.max_batch, self.page_size = ModelConfig(), max_batch, page_size
+        h = C.c_void_p()
+        check(lib().mla_model_load(os.fsencode(path), max_batch, page_size, C.byref(self.cfg),
+                                   C.byref(h)))
+        self._h = h
+        return self
 
     def close(self):
         if getattr(self, "_h", None):

@@ -340,6 +340,38 @@ int mla_session_decode(void* engine, int session, uint16_t token, float* logits)
 int mla_engine_step(void* engine, int n, const int* sessions, const int* counts,
                     const uint16_t* tokens, float* logits, int32_t* next_tokens);
 
+/* ------------------------------------------------------------ model exports
+ * The reference's inference-side weight load, load_checkpoint(path, training =
+ * false) (src/train/checkpoint.cpp:186-324; format: docs/file_formats.md,
+ * "Checkpoint directory"): a mini-mla-model export or mini-mla-checkpoint
+ * directory is checked in the reference's order with its codes and messages --
+ * COMPLETE against the manifest's SHA-256 (MLA_ERR_IO), format and version
+ * (MLA_ERR_UNSUPPORTED), config.json (ModelConfig::from_json, config.cpp:74-107)
+ * against model_config_sha256 and parameter_count (MLA_ERR_INVALID_ARGUMENT
+ * "Checkpoint model configuration mismatch"), tokenizer.json (Tokenizer::load's
+ * checks, tokenizer.cpp:70-127) against tokenizer_sha256 and the vocabulary,
+ * every listed file's SHA-256, then each tensor entry's file, uniqueness,
+ * contiguous extent, CRC-32, name, role, shape and dtype (f32 or f16), and finite
+ * values (all MLA_ERR_IO with the reference's message).  Training state in a
+ * checkpoint (optimizer.bin) is checked and skipped. */
+
+/* ModelConfig::load of <dir>/config.json, so a caller can size the parameters. */
+int mla_export_read_config(const char* dir, mla_model_config* config);
+/* The checks above; on success *config is the export's architecture and, when params
+ * is not NULL, params[params_count] (params_count = mla_config_parameter_count)
+ * receives every parameter as fp32 in registry order (f16 tensors widened exactly). */
+int mla_export_read(const char* dir, mla_model_config* config, float* params,
+                    size_t params_count);
+/* ModelConfig::hash (config.cpp:71-73): SHA-256 of the architecture's canonical JSON,
+ * 64 hex digits and a terminating NUL into hex_out[65]. */
+int mla_config_hash(const mla_model_config* config, char* hex_out);
+/* mla_export_read, then mla_model_create / mla_engine_create with the export's weights;
+ * *config receives the architecture. */
+int mla_model_load(const char* dir, int max_batch, int page_size, mla_model_config* config,
+                   void** model);
+int mla_engine_load(const char* dir, int max_sessions, int max_rows, int num_pages,
+                    int page_size, mla_model_config* config, void** engine);
+
 #ifdef __cplusplus
 }
 #endif

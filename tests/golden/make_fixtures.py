@@ -9,6 +9,16 @@
 2. ``rng_vectors.json`` -- known answers of the reference's own Rng
    (``include/mini_mla/rng.hpp``) from ``oracle/_ref/rng_ref``, which
    ``oracle/Makefile`` compiles from the reference header.
+3. ``export_tiny.json`` / ``export_mla36m.json`` -- the model-export contract of the
+   reference's own verification records (``docs/verification/pretrain-cpu`` and
+   ``docs/verification/full-model-pilot``: tiny-test and mla36m checkpoints): the
+   architecture (``config/tiny-test.json``, ``config/mla36m-v1.json``), the manifest's
+   ``model_config_sha256``, ``tokenizer_sha256`` and ``parameter_count``, and every
+   ``weights.bin`` tensor entry (name, role, shape, dtype, offset, nbytes; the CRCs
+   belong to trained weights that are not in the repository and are dropped).
+   ``tokenizer_tiny.json`` / ``tokenizer_pilot.json`` are the reference's
+   ``examples/tokenizer.json`` and ``examples/pilot-tokenizer.json``, byte for byte
+   (their SHA-256 is the manifests' ``tokenizer_sha256``).
 
 Usage: python tests/golden/make_fixtures.py [REFERENCE_ROOT]
 """
@@ -70,7 +80,27 @@ def rng_vectors() -> None:
     print("rng_vectors.json:", len(out), "series")
 
 
+def export_fixtures(ref: str) -> None:
+    for name, record, config, tok in [
+            ("tiny", "pretrain-cpu", "tiny-test.json", "tokenizer.json"),
+            ("mla36m", "full-model-pilot", "mla36m-v1.json", "pilot-tokenizer.json")]:
+        m = json.load(open(os.path.join(ref, "docs", "verification", record, "manifest.json")))
+        arch = json.load(open(os.path.join(ref, "config", config)))
+        tensors = [{k: e[k] for k in ("name", "role", "shape", "dtype", "offset", "nbytes")}
+                   for e in m["tensors"] if e["file"] == "weights.bin"]
+        out = {"source": f"docs/verification/{record}/manifest.json, config/{config}",
+               "config": arch, "model_config_sha256": m["model_config_sha256"],
+               "tokenizer_sha256": m["tokenizer_sha256"],
+               "parameter_count": m["parameter_count"], "weights": tensors}
+        json.dump(out, open(os.path.join(HERE, f"export_{name}.json"), "w"), indent=0)
+        raw = open(os.path.join(ref, "examples", tok), "rb").read()
+        dst = "tokenizer_tiny.json" if name == "tiny" else "tokenizer_pilot.json"
+        open(os.path.join(HERE, dst), "wb").write(raw)
+        print(f"export_{name}.json: {len(tensors)} tensors; {dst}: {len(raw)} bytes")
+
+
 if __name__ == "__main__":
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
-    tiny_forward(ref)
-    rng_vectors()
+    what = sys.argv[2:] or ["tiny_forward", "rng_vectors", "export_fixtures"]
+    for fn in what:
+        globals()[fn](ref)
