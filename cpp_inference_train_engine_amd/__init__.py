@@ -84,6 +84,14 @@ _SIGNATURES = {
     "mla_config_hash": (C.c_int, [C.c_void_p, C.c_char_p]),
     "mla_model_load": (C.c_int, [C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "mla_engine_load": (C.c_int, [C.c_char_p] + [C.c_int] * 4 + [C.c_void_p, C.c_void_p]),
+    "mla_tokenizer_load": (C.c_int, [C.c_char_p, C.c_void_p]),
+    "mla_tokenizer_destroy": (C.c_int, [C.c_void_p]),
+    "mla_tokenizer_info": (C.c_int, [C.c_void_p, C.c_void_p, C.c_char_p]),
+    "mla_tokenizer_special": (C.c_int, [C.c_void_p, C.c_char_p, C.c_void_p]),
+    "mla_tokenizer_encode": (C.c_int, [C.c_void_p, C.c_char_p, C.c_size_t, C.c_int, C.c_void_p,
+                                       C.c_size_t, C.c_void_p]),
+    "mla_tokenizer_decode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p,
+                                       C.c_size_t, C.c_void_p]),
 }
 
 
@@ -134,10 +142,12 @@ from .ops import (  # noqa: E402  (re-exported operator interface)
 from .model import (HipModel, ModelConfig, config_hash, config_parameter_count,  # noqa: E402
                     config_validate, read_export)
 from .engine import HipEngine, HipExecution, generate_tokens  # noqa: E402
+from .tokenizer import HipTokenizer, clean_utf8, generate  # noqa: E402
 
 __all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
            "decode_partials", "decode_merge", "prefill_attention", "HipModel", "HipEngine",
            "HipExecution", "generate_tokens", "ModelConfig", "config_validate",
-           "config_parameter_count", "config_hash", "read_export",
+           "config_parameter_count", "config_hash", "read_export", "HipTokenizer",
+           "clean_utf8", "generate",
            "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",
            "DTYPE_BF16"]

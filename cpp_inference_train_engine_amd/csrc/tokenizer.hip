@@ -1,0 +1,249 @@
+// Byte-level BPE tokenizer of the reference (src/infer/tokenizer.cpp), host code: the
+// mini-mla-tokenizer JSON format (docs/file_formats.md, "Tokenizer"), its validation,
+// encode (ranked merges applied lowest id first, leftmost first on ties; optional
+// special-token parsing), decode, and the file's SHA-256 identity.  Prompts for
+// generation are BOS + encode(text) (inference.cpp:461-468).
+#include "mla_capi_util.hpp"
+#include "mla_hip.h"
+#include "mla_io.hpp"
+#include "mla_tokenizer.hpp"
+
+#include <memory>
+#include <set>
+
+namespace mla {
+
+namespace {
+const char* const kSpecialNames[8] = {"<|pad|>",       "<|bos|>",    "<|eos|>",  "<|user|>",
+                                      "<|assistant|>", "<|system|>", "<|tool|>", "<|sep|>"};
+}  // namespace
+
+int tokenizer_load(const std::string& path, Tokenizer& t) {
+    std::string text, err;
+    if (!io::read_file(path, text, err))
+        return fail(MLA_ERR_IO, err);
+    io::Json j;
+    try {
+        j = io::JsonReader(text).parse();
+    } catch (const std::exception& e) {
+        return fail(MLA_ERR_INVALID_ARGUMENT, e.what());
+    }
+    try {
+        if (j.at("format").string() != "mini-mla-tokenizer" || j.at("version").integer() != 1 ||
+            j.at("pretokenizer").string() != "bytes-v1")
+            return fail(MLA_ERR_UNSUPPORTED, "Unsupported tokenizer format or pretokenizer");
+        const int vocab = j.at("vocab_size").integer();
+        if (vocab < 264 || vocab > 65535)
+            return fail(MLA_ERR_INVALID_ARGUMENT, "Tokenizer vocabulary must be in [264,65535]");
+        Tokenizer out;
+        out.vocab = vocab;
+        out.bytes.assign((size_t)vocab, std::string());
+        for (int i = 0; i < 256; ++i)
+            out.bytes[(size_t)i] = std::string(1, (char)i);
+        size_t id = 256;
+        for (const io::Json& m : j.at("merges").array()) {
+            const io::Json::Array& a = m.array();
+            if (a.size() != 3 || id >= (size_t)(vocab - 8) || a[2].integer() != (int)id)
+                throw std::invalid_argument("Malformed BPE merge");
+            const int left = a[0].integer(), right = a[1].integer();
+            if (left < 0 || right < 0 || (size_t)left >= id || (size_t)right >= id)
+                throw std::invalid_argument("BPE merge references a future token");
+            if (!out.merges.emplace((uint32_t)left << 16 | (uint32_t)right, (uint16_t)id).second)
+                throw std::invalid_argument("Duplicate BPE pair");
+            out.bytes[id] = out.bytes[(size_t)left] + out.bytes[(size_t)right];
+            if (out.bytes[id].size() > 1024 * 1024)
+                throw std::invalid_argument("BPE token exceeds size limit");
+            ++id;
+        }
+        if (j.at("specials").object().size() != 8)
+            throw std::invalid_argument("Tokenizer must define exactly eight special tokens");
+        for (int k = 0; k < 8; ++k) {
+            const int sid = j.at("specials").at(kSpecialNames[k]).integer();
+            if (sid != vocab - 8 + k)
+                throw std::invalid_argument(
+                    "Special token IDs disagree with the native chat template");
+            out.specials.emplace_back(kSpecialNames[k], (uint16_t)sid);
+            out.bytes[(size_t)sid] = kSpecialNames[k];
+        }
+        out.hash = io::sha256_hex(text);
+        t = std::move(out);
+        return MLA_OK;
+    } catch (const std::exception& e) {
+        return fail(MLA_ERR_INVALID_ARGUMENT, e.what());
+    }
+}
+
+namespace {
+
+// Ranked BPE over one run of bytes.  Every adjacent pair that has a merge is a candidate
+// keyed by (merged id, left position); the smallest key is merged first.  A merged id is
+// always larger than both of its parts' ids (merges reference earlier ids only), so a
+// merge never creates a candidate that ranks before the one just taken, and taking the
+// smallest key each time applies the merges in id order, leftmost first within an id.
+void encode_run(const Tokenizer& t, const char* s, size_t n, std::vector<uint16_t>& out) {
+    if (t.merges.empty()) {
+        for (size_t i = 0; i < n; ++i)
+            out.push_back((uint8_t)s[i]);
+        return;
+    }
+    const size_t none = (size_t)-1;
+    std::vector<uint16_t> id(n);
+    std::vector<size_t> next(n), prev(n);
+    std::vector<int> cand(n, -1);  // merged id of the pair starting here, -1 for none
+    for (size_t i = 0; i < n; ++i) {
+        id[i] = (uint8_t)s[i];
+        next[i] = i + 1 < n ? i + 1 : none;
+        prev[i] = i ? i - 1 : none;
+    }
+    std::set<std::pair<int, size_t>> agenda;
+    auto refresh = [&](size_t i) {
+        if (i == none)
+            return;
+        if (cand[i] >= 0)
+            agenda.erase({cand[i], i});
+        cand[i] = -1;
+        if (next[i] == none)
+            return;
+        auto it = t.merges.find((uint32_t)id[i] << 16 | id[next[i]]);
+        if (it != t.merges.end()) {
+            cand[i] = it->second;
+            agenda.insert({cand[i], i});
+        }
+    };
+    for (size_t i = 0; i < n; ++i)
+        refresh(i);
+    while (!agenda.empty()) {
+        const auto [merged, i] = *agenda.begin();
+        agenda.erase(agenda.begin());
+        cand[i] = -1;
+        const size_t r = next[i];
+        if (cand[r] >= 0) {  // the right part's own pair disappears with it
+            agenda.erase({cand[r], r});
+            cand[r] = -1;
+        }
+        id[i] = (uint16_t)merged;
+        next[i] = next[r];
+        if (next[r] != none)
+            prev[next[r]] = i;
+        refresh(prev[i]);
+        refresh(i);
+    }
+    for (size_t i = 0; n && i != none; i = next[i])
+        out.push_back(id[i]);
+}
+
+// Tokenizer::encode (tokenizer.cpp:183-205): with allow_special, a special token's exact
+// spelling becomes its id; everything else is bytes merged by encode_run.
+std::vector<uint16_t> encode(const Tokenizer& t, const char* s, size_t n, bool allow_special) {
+    std::vector<uint16_t> out;
+    if (!allow_special) {
+        encode_run(t, s, n, out);
+        return out;
+    }
+    size_t begin = 0, i = 0;
+    while (i < n) {
+        bool hit = false;
+        if (s[i] == '<')
+            for (const auto& [name, sid] : t.specials)
+                if (n - i >= name.size() && std::memcmp(s + i, name.data(), name.size()) == 0) {
+                    encode_run(t, s + begin, i - begin, out);
+                    out.push_back(sid);
+                    i += name.size();
+                    begin = i;
+                    hit = true;
+                    break;
+                }
+        if (!hit)
+            ++i;
+    }
+    encode_run(t, s + begin, n - begin, out);
+    return out;
+}
+
+}  // namespace
+}  // namespace mla
+
+using namespace mla;
+
+extern "C" {
+
+int mla_tokenizer_load(const char* path, void** tokenizer) {
+    if (!path || !tokenizer)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_load: null argument");
+    auto t = std::make_unique<Tokenizer>();
+    const int st = tokenizer_load(path, *t);
+    if (st != MLA_OK)
+        return st;
+    *tokenizer = t.release();
+    return MLA_OK;
+}
+
+int mla_tokenizer_destroy(void* tokenizer) {
+    delete static_cast<Tokenizer*>(tokenizer);
+    return MLA_OK;
+}
+
+int mla_tokenizer_info(void* tokenizer, int* vocab_size, char* sha256_hex) {
+    const Tokenizer* t = static_cast<Tokenizer*>(tokenizer);
+    if (!t || !vocab_size || !sha256_hex)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_info: null argument");
+    *vocab_size = t->vocab;
+    std::memcpy(sha256_hex, t->hash.c_str(), 65);
+    return MLA_OK;
+}
+
+int mla_tokenizer_special(void* tokenizer, const char* name, uint16_t* id) {
+    const Tokenizer* t = static_cast<Tokenizer*>(tokenizer);
+    if (!t || !name || !id)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_special: null argument");
+    for (const auto& [n, sid] : t->specials)
+        if (n == name) {
+            *id = sid;
+            return MLA_OK;
+        }
+    return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown special token");
+}
+
+int mla_tokenizer_encode(void* tokenizer, const char* text, size_t len, int allow_special,
+                         uint16_t* ids, size_t capacity, size_t* n_ids) {
+    const Tokenizer* t = static_cast<Tokenizer*>(tokenizer);
+    if (!t || (!text && len) || !n_ids)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_encode: null argument");
+    const std::vector<uint16_t> out = encode(*t, text ? text : "", len, allow_special != 0);
+    *n_ids = out.size();
+    if (!ids)
+        return MLA_OK;  // size query
+    if (capacity < out.size())
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_encode: needs " +
+                                                  std::to_string(out.size()) + " ids");
+    if (!out.empty())
+        std::memcpy(ids, out.data(), out.size() * sizeof(uint16_t));
+    return MLA_OK;
+}
+
+int mla_tokenizer_decode(void* tokenizer, const uint16_t* ids, size_t n, int skip_special,
+                         char* text, size_t capacity, size_t* len) {
+    const Tokenizer* t = static_cast<Tokenizer*>(tokenizer);
+    if (!t || (!ids && n) || !len)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_decode: null argument");
+    std::string out;
+    for (size_t k = 0; k < n; ++k) {  // Tokenizer::decode (tokenizer.cpp:206-215)
+        const uint16_t id = ids[k];
+        if (id >= t->bytes.size() || t->bytes[id].empty())
+            return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown token ID");
+        const bool special = id >= t->vocab - 8;
+        if (!skip_special || !special)
+            out += t->bytes[id];
+    }
+    *len = out.size();
+    if (!text)
+        return MLA_OK;  // size query
+    if (capacity < out.size())
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "mla_tokenizer_decode: needs " + std::to_string(out.size()) + " bytes");
+    if (!out.empty())
+        std::memcpy(text, out.data(), out.size());
+    return MLA_OK;
+}
+
+}  // extern "C"

@@ -372,6 +372,30 @@ int mla_model_load(const char* dir, int max_batch, int page_size, mla_model_conf
 int mla_engine_load(const char* dir, int max_sessions, int max_rows, int num_pages,
                     int page_size, mla_model_config* config, void** engine);
 
+/* ---------------------------------------------------------------- tokenizer
+ * The reference's byte-level BPE tokenizer (src/infer/tokenizer.cpp; format:
+ * docs/file_formats.md, "Tokenizer"), host code.  Generation prompts are
+ * <|bos|> + encode(text) (inference.cpp:461-468). */
+
+/* Tokenizer::load (tokenizer.cpp:70-127) with its checks, codes and messages. */
+int mla_tokenizer_load(const char* path, void** tokenizer);
+int mla_tokenizer_destroy(void* tokenizer);
+/* Vocabulary size and the SHA-256 of the file bytes (hex, into sha256_hex[65]). */
+int mla_tokenizer_info(void* tokenizer, int* vocab_size, char* sha256_hex);
+/* Tokenizer::special: the id of "<|bos|>", "<|eos|>", ... */
+int mla_tokenizer_special(void* tokenizer, const char* name, uint16_t* id);
+/* Tokenizer::encode (tokenizer.cpp:128-205): ranked merges applied lowest id first,
+ * leftmost first on ties; with allow_special, special-token spellings become their ids.
+ * *n_ids receives the count; ids == NULL only queries it, and a capacity below the
+ * count is MLA_ERR_INVALID_ARGUMENT. */
+int mla_tokenizer_encode(void* tokenizer, const char* text, size_t len, int allow_special,
+                         uint16_t* ids, size_t capacity, size_t* n_ids);
+/* Tokenizer::decode (tokenizer.cpp:206-215): the tokens' bytes, optionally without the
+ * special tokens; an id past the vocabulary or without bytes is
+ * MLA_ERR_INVALID_ARGUMENT "Unknown token ID".  Sizing as for encode. */
+int mla_tokenizer_decode(void* tokenizer, const uint16_t* ids, size_t n, int skip_special,
+                         char* text, size_t capacity, size_t* len);
+
 #ifdef __cplusplus
 }
 #endif
