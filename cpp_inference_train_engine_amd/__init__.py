@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(PKG, "libmla_hip.so")
 
 MLA_OK = 0
 ERROR_NAMES = {1: "invalid_argument", 2: "io_error", 3: "unsupported", 4: "out_of_memory",
-               5: "gpu_error", 6: "numerical_error"}
+               5: "gpu_error", 6: "numerical_error", 7: "unavailable"}
 DTYPE_F16, DTYPE_BF16 = 0, 1
 WORK_DESC_INTS, WORK_PAGES, MAX_WORK = 8, 8, 65535
 DECODE_FORCE_GENERIC = 1
@@ -92,6 +92,31 @@ _SIGNATURES = {
                                        C.c_size_t, C.c_void_p]),
     "mla_tokenizer_decode": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p,
                                        C.c_size_t, C.c_void_p]),
+    "mla_model_set_banned": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "mla_engine_set_banned": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
+    "mla_engine_config": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "mla_generation_config_init": (None, [C.c_void_p]),
+    "mla_generation_config_validate": (C.c_int, [C.c_void_p]),
+    "mla_sample_token": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
+                                   C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "mla_tokenizer_banned": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "mla_generation_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_int,
+                                        C.c_void_p, C.c_void_p, C.c_void_p]),
+    "mla_generation_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "mla_generation_finished": (C.c_int, [C.c_void_p]),
+    "mla_generation_result": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
+                                        C.c_void_p, C.c_size_t, C.c_void_p, C.c_char_p]),
+    "mla_generation_destroy": (C.c_int, [C.c_void_p]),
+    "mla_scheduler_config_init": (None, [C.c_void_p]),
+    "mla_scheduler_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "mla_scheduler_destroy": (C.c_int, [C.c_void_p]),
+    "mla_scheduler_submit": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_int,
+                                       C.c_void_p]),
+    "mla_scheduler_cancel": (C.c_int, [C.c_void_p, C.c_uint64]),
+    "mla_scheduler_poll": (C.c_int, [C.c_void_p, C.c_uint64, C.c_int, C.c_void_p, C.c_size_t,
+                                     C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "mla_scheduler_metrics_get": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "mla_scheduler_metrics_text": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
 }
 
 
@@ -142,12 +167,16 @@ from .ops import (  # noqa: E402  (re-exported operator interface)
 from .model import (HipModel, ModelConfig, config_hash, config_parameter_count,  # noqa: E402
                     config_validate, read_export)
 from .engine import HipEngine, HipExecution, generate_tokens  # noqa: E402
-from .tokenizer import HipTokenizer, clean_utf8, generate  # noqa: E402
+from .tokenizer import HipTokenizer, clean_utf8  # noqa: E402
+from .generation import (GenerationConfig, banned_tokens, generate,  # noqa: E402
+                         generate_ids, sample_token)
+from .scheduler import Scheduler  # noqa: E402
 
 __all__ = ["MlaError", "lib", "check", "build_metadata", "append_latent", "decode_attention",
            "decode_partials", "decode_merge", "prefill_attention", "HipModel", "HipEngine",
            "HipExecution", "generate_tokens", "ModelConfig", "config_validate",
            "config_parameter_count", "config_hash", "read_export", "HipTokenizer",
-           "clean_utf8", "generate",
+           "clean_utf8", "generate", "generate_ids", "GenerationConfig", "sample_token",
+           "banned_tokens", "Scheduler",
            "decode_workspace_bytes", "RaggedBatch", "PagedLatentCache", "DTYPE_F16",
            "DTYPE_BF16"]

@@ -287,10 +287,11 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
         return st;
     }
     ++E->steps;
-    bool finite = true;
+    bool finite = true, open = true;
     for (int i = 0; i < n; ++i) {
         E->sessions[ids[i]].length += counts[i];
-        finite = finite && E->h_out[4 + i] >= 0;
+        finite = finite && E->h_out[4 + i] != -1;
+        open = open && E->h_out[4 + i] != -2;
         if (next)
             next[i] = E->h_out[4 + i];
     }
@@ -298,6 +299,8 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
         std::memcpy(logits, E->h_logits, (size_t)n * c.vocab_size * sizeof(float));
     if (!finite)  // inference.cpp:170-172
         return fail(MLA_ERR_NUMERICAL, "Nonfinite decode output");
+    if (!open)  // inference.cpp:375-377
+        return fail(MLA_ERR_INVALID_ARGUMENT, "All tokens are banned");
     return MLA_OK;
 }
 
@@ -403,6 +406,14 @@ int mla_engine_info(void* engine, int64_t* info) {
     return MLA_OK;
 }
 
+int mla_engine_config(void* engine, mla_model_config* config) {
+    Engine* E = as_engine(engine);
+    if (!E || !config)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_engine_config: invalid argument");
+    *config = E->cfg;
+    return MLA_OK;
+}
+
 int mla_session_create(void* engine, int* session) {
     Engine* E = as_engine(engine);
     if (!E || !session)
@@ -502,6 +513,14 @@ int mla_session_decode(void* engine, int session, uint16_t token, float* logits)
                     "token");
     const int one = 1;
     return step(E, 1, &session, &one, &token, logits, nullptr, "mla_session_decode");
+}
+
+int mla_engine_set_banned(void* engine, const uint16_t* ids, size_t n) {
+    Engine* E = static_cast<Engine*>(engine);
+    if (!E)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_engine_set_banned: null engine");
+    std::lock_guard<std::mutex> lock(E->mu);
+    return mla_model_set_banned(E->model, ids, n);
 }
 
 int mla_engine_step(void* engine, int n, const int* sessions, const int* counts,

@@ -65,6 +65,7 @@ struct StepArgs {
     float* logits;              // [B x vocab]
     float* arg_v;               // [B x parts] greedy partials
     int32_t* arg_c;
+    const uint32_t* ban;        // bitmap of token ids the greedy token skips, or null
     int32_t* next_tokens;       // [B]
     // Per-row sums of squares of each 16-column tile of an activation, written by its
     // producer and summed (in tile order) into 1/rms by the RMSNorm-ing consumer.

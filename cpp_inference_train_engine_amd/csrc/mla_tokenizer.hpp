@@ -20,5 +20,11 @@ struct Tokenizer {
 // Tokenizer::load (tokenizer.cpp:70-127): MLA_OK, or the reference's code and message
 // (recorded as this thread's last error).
 int tokenizer_load(const std::string& path, Tokenizer& t);
+// Tokenizer::decode (tokenizer.cpp:206-218): false on an id with no bytes ("Unknown token
+// ID"); with skip_special the eight special tokens are left out.
+bool tokenizer_decode(const Tokenizer& t, const uint16_t* ids, size_t n, bool skip_special,
+                      std::string& out);
+// Tokenizer::special (tokenizer.cpp:219-224): the id of a special token's name, -1 if none.
+int tokenizer_special(const Tokenizer& t, const std::string& name);
 
 }  // namespace mla

@@ -664,7 +664,8 @@ __global__ __launch_bounds__(64 * kWaves) void g5_kernel(StepArgs s, LayerWeight
 // Final RMSNorm + tied logits h . E^T for 64 rows and four 16-column tiles per
 // workgroup (the waves split K four ways and the tiles two ways); each workgroup also
 // leaves, per row, the greedy winner of its 64 columns (strict >, so the lowest index
-// wins ties) and whether all of them were finite.
+// wins ties; banned ids never win) and whether all of them were finite (banned or not:
+// sample_token checks every logit, inference.cpp:352-353).
 constexpr int kG7Tiles = 4, kG7KG = 4;
 
 template <int KW>
@@ -703,6 +704,7 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
     for (int j = 0; j < kG7Tiles; ++j) {  // tiles in increasing column order
         const int col = (nt0 + j) * 16 + n;
         const bool valid = nt0 + j < n_tiles && col < m.vocab;
+        const bool open = valid && !(s.ban && ((s.ban[col >> 5] >> (col & 31)) & 1u));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = row0 + 16 * mt + 4 * g + i;
@@ -711,7 +713,7 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
                 s.logits[(long long)row * m.vocab + col] = y;
             if (valid && !isfinite(y))
                 fin[i] = 0.0f;
-            if (valid && (bc[i] == 0x7fffffff || y > bv[i])) {  // strict >: lowest column
+            if (open && (bc[i] == 0x7fffffff || y > bv[i])) {  // strict >: lowest column
                 bv[i] = y;
                 bc[i] = col;
             }
@@ -754,8 +756,10 @@ __global__ __launch_bounds__(256) void gather_last_kernel(StepArgs s, int B, con
         ss_out[(long long)b * d_tiles + c] = src >= 0 ? s.ss_x[(long long)src * d_tiles + c] : 0.0f;
 }
 
-// Greedy token per row (inference.cpp:363-373 with no penalty or bans): the lowest
-// column among the maxima; -1 when a logit is not finite (numerical_error).  256
+// Greedy token per row (inference.cpp:354-380 with no repetition penalty): the lowest
+// column among the maxima of the ids not banned; -1 when a logit is not finite
+// (numerical_error, checked first as the reference does), -2 when every id is banned
+// ("All tokens are banned").  256
 // threads load up to four partials each at once (parts <= 1024).
 constexpr int kArgItems = 4;
 
@@ -812,7 +816,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(StepArgs s, int parts) {
                 bc = sc[w];
             }
         }
-        s.next_tokens[row] = bad || bc == 0x7fffffff ? -1 : bc;
+        s.next_tokens[row] = bad ? -1 : bc == 0x7fffffff ? -2 : bc;
     }
 }
 

@@ -125,6 +125,8 @@ struct Model {
     float2* rope_rows;
     uint16_t *xw, *resw, *u, *q_latent, *q_rope;
     int32_t* arg_c;
+    uint32_t* ban_bits = nullptr;  // [ceil(vocab/32)] banned token ids, allocated on first use
+    bool banning = false;          // some id is banned: the greedy token skips them
 
     ~Model() {
         for (void* p : allocations)
@@ -232,6 +234,7 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     s.logits = logits ? logits : M->logits;
     s.arg_v = M->arg_v;
     s.arg_c = M->arg_c;
+    s.ban = M->banning ? M->ban_bits : nullptr;
     s.next_tokens = next_tokens;
     s.ss_x = M->ss_x;
     s.ss_res = M->ss_res;
@@ -507,6 +510,30 @@ int mla_model_forward(void* model, void* stream, int rows, const int32_t* tokens
     return model_forward(static_cast<Model*>(model), static_cast<hipStream_t>(stream), rows,
                          tokens, positions, B, max_q_len, md, pages, workspace, workspace_bytes,
                          logits, next_tokens);
+}
+
+int mla_model_set_banned(void* model, const uint16_t* ids, size_t n) {
+    Model* M = static_cast<Model*>(model);
+    if (!M || (!ids && n))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_set_banned: null argument");
+    const int vocab = M->cfg.vocab_size;
+    std::vector<uint32_t> bits((size_t)(vocab + 31) / 32, 0u);
+    bool any = false;
+    for (size_t k = 0; k < n; ++k)
+        if (ids[k] < vocab) {  // ids outside the vocabulary are ignored (inference.cpp:357-359)
+            bits[ids[k] >> 5] |= 1u << (ids[k] & 31);
+            any = true;
+        }
+    hipError_t e = hipSuccess;
+    if (!M->ban_bits)
+        e = M->alloc(M->ban_bits, bits.size());
+    if (e == hipSuccess)
+        e = hipMemcpy(M->ban_bits, bits.data(), bits.size() * sizeof(uint32_t),
+                      hipMemcpyHostToDevice);
+    if (e != hipSuccess)
+        return gpu_status(e, "mla_model_set_banned");
+    M->banning = any;
+    return MLA_OK;
 }
 
 const float* mla_model_logits(void* model) {

@@ -73,6 +73,26 @@ int tokenizer_load(const std::string& path, Tokenizer& t) {
     }
 }
 
+bool tokenizer_decode(const Tokenizer& t, const uint16_t* ids, size_t n, bool skip_special,
+                      std::string& out) {
+    out.clear();
+    for (size_t k = 0; k < n; ++k) {
+        const uint16_t id = ids[k];
+        if (id >= t.bytes.size() || t.bytes[id].empty())
+            return false;
+        if (!skip_special || id < t.vocab - 8)  // the specials are the last eight ids
+            out += t.bytes[id];
+    }
+    return true;
+}
+
+int tokenizer_special(const Tokenizer& t, const std::string& name) {
+    for (const auto& [n, sid] : t.specials)
+        if (n == name)
+            return sid;
+    return -1;
+}
+
 namespace {
 
 // Ranked BPE over one run of bytes.  Every adjacent pair that has a merge is a candidate
@@ -196,12 +216,11 @@ int mla_tokenizer_special(void* tokenizer, const char* name, uint16_t* id) {
     const Tokenizer* t = static_cast<Tokenizer*>(tokenizer);
     if (!t || !name || !id)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_special: null argument");
-    for (const auto& [n, sid] : t->specials)
-        if (n == name) {
-            *id = sid;
-            return MLA_OK;
-        }
-    return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown special token");
+    const int sid = tokenizer_special(*t, name);
+    if (sid < 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown special token");
+    *id = (uint16_t)sid;
+    return MLA_OK;
 }
 
 int mla_tokenizer_encode(void* tokenizer, const char* text, size_t len, int allow_special,
@@ -227,14 +246,8 @@ int mla_tokenizer_decode(void* tokenizer, const uint16_t* ids, size_t n, int ski
     if (!t || (!ids && n) || !len)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_tokenizer_decode: null argument");
     std::string out;
-    for (size_t k = 0; k < n; ++k) {  // Tokenizer::decode (tokenizer.cpp:206-215)
-        const uint16_t id = ids[k];
-        if (id >= t->bytes.size() || t->bytes[id].empty())
-            return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown token ID");
-        const bool special = id >= t->vocab - 8;
-        if (!skip_special || !special)
-            out += t->bytes[id];
-    }
+    if (!tokenizer_decode(*t, ids, n, skip_special != 0, out))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown token ID");
     *len = out.size();
     if (!text)
         return MLA_OK;  // size query

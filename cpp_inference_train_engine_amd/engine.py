@@ -75,6 +75,12 @@ class HipEngine:
         check(lib().mla_session_create(self.handle, C.byref(s)))
         return HipExecution(self, s.value)
 
+    def set_banned(self, ids) -> None:
+        """mla_engine_set_banned: the ids the greedy next tokens of later steps skip
+        (sample_token's banned list, inference.cpp:345-380)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint16).ravel()
+        check(lib().mla_engine_set_banned(self.handle, ids.ctypes.data, ids.size))
+
     def step(self, sessions, token_lists, want_logits: bool = True):
         """One batched forward: ``sessions[i]`` appends ``token_lists[i]`` (one token =
         decode, several = chunked prefill).  Returns (logits [n, vocab] or None,
@@ -115,6 +121,10 @@ class HipExecution:
         s = C.c_int()
         check(lib().mla_session_fork(self.engine.handle, self.session_id, C.byref(s)))
         return HipExecution(self.engine, s.value)
+
+    @property
+    def max_sequence_length(self) -> int:
+        return self.engine.cfg.max_sequence_length
 
     @property
     def position(self) -> int:

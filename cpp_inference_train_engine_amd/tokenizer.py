@@ -1,13 +1,9 @@
-"""Text in and out of the engine: the reference's tokenizer over the C ABI
-(``mla_tokenizer_*``, src/infer/tokenizer.cpp) and greedy text generation
-(``InferenceEngine::generate``, src/infer/inference.cpp:461-579).
+"""The reference's tokenizer over the C ABI (``mla_tokenizer_*``, src/infer/tokenizer.cpp).
 
 ``HipTokenizer`` loads a ``mini-mla-tokenizer`` file with the reference's checks and
 encodes (ranked byte-level BPE), decodes and builds chat prompts
-(``Tokenizer::chat_prompt``, tokenizer.cpp:236-262).  ``generate`` prefixes
-``<|bos|>`` to the encoded prompt, runs the greedy generation loop with the reference's
-stop rules (EOS, stop token sequences, stop strings) and returns the text cleaned as
-``clean_utf8`` does (tokenizer.cpp:44-57).
+(``Tokenizer::chat_prompt``, tokenizer.cpp:236-262); ``clean_utf8`` is the reference's
+text cleaning (tokenizer.cpp:13-57).
 """
 from __future__ import annotations
 
@@ -116,46 +112,3 @@ def clean_utf8(b: bytes) -> str:
             out += "\ufffd".encode()
             i += 1
     return out.decode()
-
-
-def generate(execution, tokenizer: HipTokenizer, prompt: str, max_new_tokens: int,
-             max_sequence_length: int, stop=(), stop_tokens=()) -> dict:
-    """InferenceEngine::generate + generate_tokens (inference.cpp:461-579), greedy: the
-    prompt is <|bos|> + encode(prompt); generation stops at <|eos|>, at the end of a stop
-    token sequence (its text removed) or at a stop string (text cut before it)."""
-    ids = [tokenizer.special("<|bos|>")] + tokenizer.encode(prompt).tolist()
-    if not ids or len(ids) + max_new_tokens > max_sequence_length:
-        raise MlaError(1, "Prompt plus requested tokens exceeds context")
-    for seq in stop_tokens:
-        if any(t >= tokenizer.vocab_size for t in seq):
-            raise MlaError(1, "Stop token exceeds vocabulary")
-    eos = tokenizer.special("<|eos|>")
-    logits = execution.prefill(ids)
-    tokens, text, reason = [], b"", "length"
-    for i in range(max_new_tokens):
-        if not np.isfinite(logits).all():
-            raise MlaError(6, "Invalid sampler logits")
-        token = int(np.argmax(logits))  # the lowest index among the maxima
-        tokens.append(token)
-        if token == eos:
-            reason = "stop"
-            break
-        hit = next((list(s) for s in stop_tokens
-                    if len(tokens) >= len(s) and tokens[-len(s):] == list(s)), None)
-        if hit is not None:
-            text = tokenizer.decode(tokens, skip_special=True)
-            tail = tokenizer.decode(hit, skip_special=True)
-            if len(tail) <= len(text):
-                text = text[:len(text) - len(tail)]
-            reason = "stop"
-            break
-        text += tokenizer.token_bytes(token)
-        found = next((text.find(s.encode()) for s in stop if text.find(s.encode()) >= 0), -1)
-        if found >= 0:  # the first stop string of the list that occurs
-            text = text[:found]
-            reason = "stop"
-            break
-        if i + 1 < max_new_tokens:
-            logits = execution.decode(token)
-    return {"tokens": tokens, "text": clean_utf8(text), "finish_reason": reason,
-            "prompt_tokens": len(ids)}

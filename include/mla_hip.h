@@ -12,8 +12,9 @@
  *
  * Conventions
  *  - Every function returns an int status: MLA_OK or MLA_ERR_* (the reference
- *    ErrorCode values of include/mini_mla/result.hpp:12-19, plus one).  The
- *    message of the last failure on the calling thread is mla_last_error().
+ *    ErrorCode values of include/mini_mla/result.hpp:12-19, plus one, and
+ *    MLA_ERR_UNAVAILABLE of the scheduler).  The message of the last failure on
+ *    the calling thread is mla_last_error().
  *  - Pointers named d_* / documented "device" are device (HBM) pointers;
  *    `stream` is a hipStream_t (NULL = the default stream).  Work is
  *    stream-ordered and asynchronous unless stated.
@@ -251,7 +252,8 @@ int mla_model_destroy(void* model);
  * fp32 (device; NULL = the model's own buffer, see mla_model_logits) and
  * next_tokens[B] (device int32): the greedy token of sample_token with
  * temperature 0 and no penalty (inference.cpp:345-380: lowest index among the
- * maxima), or -1 when a logit is not finite (numerical_error). */
+ * maxima of the ids not banned, see mla_model_set_banned), -1 when a logit is not
+ * finite (numerical_error), -2 when every id is banned. */
 int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
                    const int32_t* positions, const int32_t* cu_seqlens_q,
                    const int32_t* page_table, int max_pages, int num_pool_pages,
@@ -281,6 +283,13 @@ int mla_model_forward(void* model, void* stream, int rows, const int32_t* tokens
                       const int32_t* work_pages, const int32_t* info, int max_work,
                       void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
                       int32_t* next_tokens);
+/* Token ids the greedy next token of later steps skips: sample_token's `banned`
+ * (inference.cpp:345-380), which InferenceEngine::load fills with the special tokens
+ * other than <|eos|> and the ids with no bytes (inference.cpp:441-447; see
+ * mla_tokenizer_banned).  Ids >= vocab are ignored; n == 0 bans nothing.  A row whose
+ * every id is banned gets next token -2 ("All tokens are banned"); a non-finite logit
+ * still gives -1 first.  Not stream-ordered: call it between steps. */
+int mla_model_set_banned(void* model, const uint16_t* ids, size_t n);
 /* The model's own logits buffer [max_batch x vocab] (device). */
 const float* mla_model_logits(void* model);
 
@@ -309,6 +318,8 @@ int mla_engine_destroy(void* engine);
 /* info[8] = {active sessions, free pages, pages, page_size, max_rows, max_sessions,
  *            steps run, page-pool bytes}. */
 int mla_engine_info(void* engine, int64_t* info);
+/* The model configuration the engine was created with. */
+int mla_engine_config(void* engine, mla_model_config* config);
 
 /* A new, empty session sharing the engine's weights: Execution::fork_inference
  * (inference.cpp:182-188; mps_backend.mm:670-676 shares weights and programs, the
@@ -335,10 +346,15 @@ int mla_session_decode(void* engine, int session, uint16_t token, float* logits)
  * order from `tokens` (a count > 1 is a chunked prefill on top of the session's
  * cached context; an empty session may start this way).  logits (host [n x vocab],
  * may be NULL) and next_tokens (host [n], may be NULL: the greedy token of
- * sample_token, inference.cpp:345-380) are those of each session's last new token.
- * On an error no session advances. */
+ * sample_token, inference.cpp:345-380, skipping the ids of mla_engine_set_banned) are
+ * those of each session's last new token.  On an error no session advances, except
+ * MLA_ERR_NUMERICAL (a non-finite logit) and "All tokens are banned", reported after
+ * the step as the reference reports them after appending (inference.cpp:170-172). */
 int mla_engine_step(void* engine, int n, const int* sessions, const int* counts,
                     const uint16_t* tokens, float* logits, int32_t* next_tokens);
+/* mla_model_set_banned for the engine's model: the ids next_tokens of mla_engine_step
+ * skip (MLA_ERR_INVALID_ARGUMENT "All tokens are banned" when none is left). */
+int mla_engine_set_banned(void* engine, const uint16_t* ids, size_t n);
 
 /* ------------------------------------------------------------ model exports
  * The reference's inference-side weight load, load_checkpoint(path, training =
@@ -395,6 +411,127 @@ int mla_tokenizer_encode(void* tokenizer, const char* text, size_t len, int allo
  * MLA_ERR_INVALID_ARGUMENT "Unknown token ID".  Sizing as for encode. */
 int mla_tokenizer_decode(void* tokenizer, const uint16_t* ids, size_t n, int skip_special,
                          char* text, size_t capacity, size_t* len);
+
+/* --------------------------------------------------------------- generation
+ * Token selection and the generation loop of InferenceEngine (src/infer/inference.cpp:
+ * 330-579), host code: GenerationConfig, sample_token, the banned ids of
+ * InferenceEngine::load and generate_tokens' loop (stop rules, streaming, cancel). */
+
+/* GenerationConfig (include/mini_mla/inference.hpp:27-34).  Stop strings are stop[i]
+ * of stop_len[i] bytes; stop token sequences are stop_tokens_len[i] ids each, one after
+ * the other in stop_tokens. */
+typedef struct mla_generation_config {
+    int max_new_tokens;       /* [0, 65535]; default 128 */
+    int top_k;                /* 0 = all ids; default 0 */
+    float temperature;        /* 0 = greedy; default 0.8 */
+    float top_p;              /* (0, 1]; default 0.95 */
+    float repetition_penalty; /* > 0; default 1 */
+    uint64_t seed;            /* sampling stream (SplitMix64); default 42 */
+    int n_stop;
+    const char* const* stop;
+    const size_t* stop_len;
+    int n_stop_tokens;
+    const int* stop_tokens_len;
+    const uint16_t* stop_tokens;
+} mla_generation_config;
+/* The reference's defaults, no stop lists. */
+void mla_generation_config_init(mla_generation_config* config);
+/* GenerationConfig::validate (inference.cpp:330-344) with its messages. */
+int mla_generation_config_validate(const mla_generation_config* config);
+/* sample_token (inference.cpp:345-412): greedy (temperature 0: lowest id among the
+ * maxima, repetition penalty on the history's ids) or seeded sampling (penalty, bans,
+ * top_k, top_p, temperature; *rng_state is the Rng state, advanced by the draw).
+ * MLA_ERR_NUMERICAL "Invalid sampler logits" on a non-finite logit or vocab outside
+ * [1, 65535]; MLA_ERR_INVALID_ARGUMENT "All tokens are banned". */
+int mla_sample_token(const float* logits, size_t vocab, const uint16_t* history,
+                     size_t n_history, const mla_generation_config* config, uint64_t* rng_state,
+                     const uint16_t* banned, size_t n_banned, uint16_t* token);
+/* The ids InferenceEngine::load bans from sampling (inference.cpp:441-447): the special
+ * tokens other than <|eos|> and the ids with no bytes.  Sizing as for encode. */
+int mla_tokenizer_banned(void* tokenizer, uint16_t* ids, size_t capacity, size_t* n);
+
+/* Streamed text (UTF-8, cleaned); len 0 asks whether to go on.  Return 0 to cancel. */
+typedef int (*mla_text_callback)(void* user, const char* text, size_t len);
+/* generate_tokens (inference.cpp:469-579) as a state machine: create() checks the
+ * config, prompt + max_new_tokens <= max_sequence_length and the stop tokens, with the
+ * tokenizer's banned ids.  The caller prefills the prompt and passes the last
+ * position's logits to step(), which sets *next_token to the token to decode and pass
+ * back next, or -1 when the generation has finished (then result() holds the text,
+ * tokens and finish reason "stop", "length" or "cancelled"; finish_reason[16]). */
+int mla_generation_create(void* tokenizer, const mla_generation_config* config,
+                          const uint16_t* prompt, size_t n, int max_sequence_length,
+                          mla_text_callback callback, void* user, void** generation);
+int mla_generation_step(void* generation, const float* logits, size_t vocab,
+                        int32_t* next_token);
+int mla_generation_finished(void* generation);
+int mla_generation_result(void* generation, char* text, size_t text_capacity, size_t* text_len,
+                          uint16_t* tokens, size_t tokens_capacity, size_t* n_tokens,
+                          char* finish_reason);
+int mla_generation_destroy(void* generation);
+
+/* ---------------------------------------------------------------- scheduler
+ * Continuous batching for a server: the reference's mini_mla_serve gives each of its
+ * `workers` threads a private forked session and runs one request at a time on each
+ * (src/serve/server.cpp:195-198, 254-266).  Here one stepping thread serves every
+ * request through mla_engine_step: each step carries one decode row per running
+ * request and prompt chunks of newly admitted ones, up to the engine's max_rows.  Kept
+ * from the reference: the bounded queue (MLA_ERR_UNAVAILABLE "Request queue is full",
+ * its 429), the per-request deadline counted from submission (not yet started:
+ * "Request queue deadline exceeded", its 503; running: finish reason "cancelled", its
+ * 408), cancellation, the request limits and the /metrics counters and text
+ * (server.cpp:221-227, 272-300, 320-337).  A request is admitted when a session slot
+ * and enough cache pages for prompt + max_new_tokens are free, so a running request
+ * never runs out of pages.  The HTTP layer itself stays with the caller. */
+#define MLA_ERR_UNAVAILABLE 7 /* no ErrorCode counterpart: queue full or deadline passed */
+
+/* ServerConfig's limits (include/mini_mla/server.hpp:5-10). */
+typedef struct mla_scheduler_config {
+    int max_context;             /* <= the model's max_sequence_length; default 2048 */
+    int max_new_tokens;          /* per request (also the default); default 128 */
+    int max_queue;               /* requests waiting to start; default 16 */
+    int request_timeout_seconds; /* from submission to the end; default 60 */
+} mla_scheduler_config;
+typedef struct mla_request_status {
+    int done;                  /* 1: finished; this poll retired the request */
+    int error;                 /* MLA_OK, or the code that ended the request */
+    char error_message[240];
+    char finish_reason[16];    /* "stop", "length" or "cancelled" */
+    uint64_t prompt_tokens, completion_tokens;
+    double queue_seconds, prefill_seconds, decode_seconds, first_token_seconds;
+} mla_request_status;
+typedef struct mla_scheduler_metrics {
+    uint64_t requests, completed, rejected, errors, generated_tokens;
+    double queue_seconds, prefill_seconds, decode_seconds, first_token_seconds;
+    uint64_t queue_depth, running, steps;
+} mla_scheduler_metrics;
+
+void mla_scheduler_config_init(mla_scheduler_config* config);
+/* Starts the stepping thread.  The engine's banned ids become the tokenizer's
+ * (mla_engine_set_banned).  Engine and tokenizer must outlive the scheduler. */
+int mla_scheduler_create(void* engine, void* tokenizer, const mla_scheduler_config* config,
+                         void** scheduler);
+/* Cancels what is queued or running and joins the thread. */
+int mla_scheduler_destroy(void* scheduler);
+/* Queues a generation of prompt (token ids, <|bos|> included).  config NULL or
+ * max_new_tokens < 0: the server default min(max_new_tokens, max_context - n)
+ * (server.cpp:300-304).  Checks in the reference's order: queue full
+ * (MLA_ERR_UNAVAILABLE, counted as rejected), generation settings, the request limits
+ * ("Request exceeds context or token limit"), empty prompt, stop tokens.  stream != 0
+ * hands out text as it is produced; otherwise the whole text comes at the end. */
+int mla_scheduler_submit(void* scheduler, const uint16_t* prompt, size_t n,
+                         const mla_generation_config* config, int stream, uint64_t* request);
+/* Ends the request at its next token ("cancelled"); a queued one never starts. */
+int mla_scheduler_cancel(void* scheduler, uint64_t request);
+/* Waits up to timeout_ms for new text or the end, moves up to text_capacity bytes of
+ * the text not yet handed out into text (*text_len), and fills status.  Once done and
+ * all text is out, tokens (capacity >= completion_tokens, may be NULL) receives the
+ * generated ids, status->done is 1 and the request is forgotten. */
+int mla_scheduler_poll(void* scheduler, uint64_t request, int timeout_ms, char* text,
+                       size_t text_capacity, size_t* text_len, uint16_t* tokens,
+                       size_t tokens_capacity, mla_request_status* status);
+int mla_scheduler_metrics_get(void* scheduler, mla_scheduler_metrics* metrics);
+/* The /metrics page of server.cpp:272-289 (Prometheus text); sizing as for encode. */
+int mla_scheduler_metrics_text(void* scheduler, char* text, size_t capacity, size_t* len);
 
 #ifdef __cplusplus
 }

@@ -7,7 +7,8 @@ special tokens round-trip, ``encode("ababa") == [256, 257]`` under merges
 (a,b)->256, (256,a)->257, a merge naming a later id is refused.  Beyond those, the ranked
 BPE is checked against a brute-force encoder written from the format's rule
 (docs/file_formats.md: "Ranked merges are applied with stable left-position tie
-breaking"): repeatedly merge the lowest-id pair, leftmost first.  Host code: CPU tests.
+breaking"): repeatedly merge the lowest-id pair, leftmost first.  Host code: CPU tests;
+generation with this tokenizer is tested in test_generation.py and test_serving.py.
 """
 import hashlib
 import json
@@ -192,70 +193,3 @@ def test_clean_utf8():
     assert clean_utf8(b"\xe2\x82") == "��"       # truncated 3-byte sequence
     assert clean_utf8(b"\xed\xa0\x80") == "�" * 3     # encoded surrogate
     assert clean_utf8(b"\xc0\x80") == "��"       # overlong NUL
-
-
-class _Scripted:
-    """An execution whose logits follow a script (one argmax per step)."""
-
-    def __init__(self, vocab, argmaxes):
-        self.vocab, self.left = vocab, list(argmaxes)
-        self.calls = []
-
-    def _logits(self):
-        x = np.zeros(self.vocab, np.float32)
-        x[self.left.pop(0)] = 1.0
-        return x
-
-    def prefill(self, ids):
-        self.calls.append(("prefill", list(ids)))
-        return self._logits()
-
-    def decode(self, token):
-        self.calls.append(("decode", token))
-        return self._logits()
-
-
-def test_generate_stop_rules():
-    """generate_tokens' stop rules (inference.cpp:504-560): EOS ends without text, a stop
-    token sequence ends with its text removed, a stop string cuts the text before it;
-    the last token is never decoded."""
-    import cpp_inference_train_engine_amd as mla
-    t = _tok(TOK_TINY)
-    eos = t.special("<|eos|>")
-    ex = _Scripted(264, [72, 105, eos, 0])
-    out = mla.generate(ex, t, "Q", 8, 64)
-    assert out["tokens"] == [72, 105, eos] and out["text"] == "Hi" and \
-        out["finish_reason"] == "stop"
-    assert ex.calls[0] == ("prefill", [257, 81]) and ex.calls[1:] == [("decode", 72),
-                                                                     ("decode", 105)]
-    ex = _Scripted(264, [65, 66, 67, 68])
-    out = mla.generate(ex, t, "Q", 8, 64, stop_tokens=[[66, 67]])
-    assert out["tokens"] == [65, 66, 67] and out["text"] == "A"
-    ex = _Scripted(264, [65, 66, 67, 68, 69])
-    out = mla.generate(ex, t, "Q", 8, 64, stop=["CD", "B"])
-    assert out["text"] == "A" and out["finish_reason"] == "stop"  # first listed that occurs
-    ex = _Scripted(264, [65, 66, 67])
-    out = mla.generate(ex, t, "Q", 3, 64)
-    assert out["finish_reason"] == "length" and len(ex.calls) == 3  # prefill + 2 decodes
-    with pytest.raises(mla.MlaError):
-        mla.generate(_Scripted(264, [1]), t, "Q" * 60, 8, 64)
-    with pytest.raises(mla.MlaError):
-        mla.generate(_Scripted(264, [1]), t, "Q", 4, 64, stop_tokens=[[300]])
-
-
-# ------------------------------------------------------------------ GPU ----
-@pytest.mark.gpu
-def test_text_generation_on_the_engine(gpu, tiny_fixture):
-    """<|bos|> + encode(prompt) through the engine with the reference's tiny-test weights:
-    the tokens are generate_tokens' greedy tokens for the same ids, the text their bytes."""
-    t = gpu.HipTokenizer(TOK_TINY)
-    eng = gpu.HipEngine(gpu.ModelConfig.from_dict(TINY), tiny_fixture["params"],
-                        max_sessions=2, max_rows=64, num_pages=16, page_size=16)
-    out = gpu.generate(eng.session(), t, "Say hi.", 12, TINY["max_sequence_length"])
-    ids = [t.special("<|bos|>")] + list(b"Say hi.")
-    want = gpu.generate_tokens(eng.session(), ids, len(out["tokens"]),
-                               TINY["max_sequence_length"])
-    assert out["tokens"] == want
-    if out["finish_reason"] == "length":
-        assert out["text"] == gpu.clean_utf8(t.decode(out["tokens"]))
-    eng.close()
