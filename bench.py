@@ -61,7 +61,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=6.0,
                     help="seconds of CPU work per baseline leg (all threads, then 1 thread)")
     ap.add_argument("--flags", type=int, default=0)
-    ap.add_argument("--only", choices=["config2", "config4", "config5"], default=None,
+    ap.add_argument("--only", choices=["config2", "config4", "config5", "serve"], default=None,
                     help="run only this secondary leg and print its JSON (for profiling)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration)")
@@ -158,6 +158,44 @@ def config2_leg(mla, params, steps: int = 64, prompt_len: int = 1024):
             "tok_per_s": round(1e3 / med, 1),
             "reference_mps_fp16_ms": 3.583,
             "vs_reference_mps": round(3.583 / med, 2)}
+
+
+def serve_leg(mla, params, temperature: float, requests: int = 64, new_tokens: int = 64):
+    """Serving through the continuous-batching scheduler (mla_scheduler_*): the mla36m
+    model, `requests` requests submitted at once, prompts of U[64, 512] ids (reference
+    Rng seed 0, <|bos|> first), `new_tokens` tokens each (no stop), greedy (the device
+    token) or sampled with the server's defaults (temperature 0.8, top_p 0.95, on the
+    host from the step's logits).  Wall clock from the first submission to the last
+    result; prompts are prefilled in chunks beside the running requests' decode rows."""
+    from cpp_inference_train_engine_amd.workloads import MLA36M, SplitMix64
+    cfg = mla.ModelConfig.from_dict(MLA36M)
+    tok = mla.HipTokenizer(os.path.join(REPO, "tests", "golden", "tokenizer_pilot.json"))
+    rng = SplitMix64(0)
+    bos = tok.special("<|bos|>")
+    prompts = [[bos] + [rng.bounded(256) for _ in range(64 + rng.bounded(449) - 1)]
+               for _ in range(requests)]
+    eng = mla.HipEngine(cfg, params, max_sessions=requests, max_rows=1024, num_pages=1024)
+    gen = mla.GenerationConfig(max_new_tokens=new_tokens, temperature=temperature)
+    out = {}
+    with mla.Scheduler(eng, tok, max_context=2048, max_new_tokens=new_tokens,
+                       max_queue=requests) as sch:
+        sch.result(sch.submit(prompts[0][:8], gen))  # warm
+        base = sch.metrics()
+        t0 = time.perf_counter()
+        ids = [sch.submit(p, gen) for p in prompts]
+        res = [sch.result(i, timeout=300) for i in ids]
+        wall = time.perf_counter() - t0
+        m = sch.metrics()
+    eng.close()
+    done = sum(r["completion_tokens"] for r in res)
+    out.update(workload=f"{requests} requests at once, prompts U[64,512] ids, {new_tokens} "
+                        f"new tokens each, temperature {temperature}",
+               wall_s=round(wall, 4), generated_tok_per_s=round(done / wall, 1),
+               prompt_tokens=sum(len(p) for p in prompts), completion_tokens=done,
+               steps=int(m["steps"] - base["steps"]),
+               ms_per_step=round(wall * 1e3 / max(m["steps"] - base["steps"], 1), 4),
+               mean_first_token_s=round(float(np.mean([r["first_token_seconds"] for r in res])), 4))
+    return out
 
 
 def config4_leg(mla, torch, reps: int = 20):
@@ -293,7 +331,9 @@ def main():
     if args.only:
         legs = {"config2": lambda: config2_leg(mla, model_params(MLA36M, seed=0)),
                 "config4": lambda: config4_leg(mla, torch),
-                "config5": lambda: config5_leg(mla, torch)}
+                "config5": lambda: config5_leg(mla, torch),
+                "serve": lambda: {"greedy": serve_leg(mla, model_params(MLA36M, seed=0), 0.0),
+                                  "sampled": serve_leg(mla, model_params(MLA36M, seed=0), 0.8)}}
         print(json.dumps({args.only: legs[args.only]()}), flush=True)
         return
     t_gen = time.perf_counter()

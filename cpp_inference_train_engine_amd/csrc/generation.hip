@@ -34,6 +34,38 @@ namespace {
 float penalised(float score, float penalty) {
     return score > 0 ? score / penalty : score * penalty;
 }
+
+// One 64-bit key per id whose ascending order is sample_token's order: higher score
+// first, then lower id (-0 and +0 tie, as they compare equal).
+uint64_t order_key(float score, uint16_t id) {
+    if (score == 0.0f)
+        score = 0.0f;
+    uint32_t u;
+    std::memcpy(&u, &score, sizeof(u));
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // ascending in the score
+    return ((uint64_t)~u << 16) | id;
+}
+
+// LSD radix sort of 48-bit keys, 12 bits per pass.
+void radix_sort48(std::vector<uint64_t>& keys, std::vector<uint64_t>& tmp) {
+    constexpr int kBits = 12, kBuckets = 1 << kBits;
+    tmp.resize(keys.size());
+    std::vector<uint32_t> count(kBuckets);
+    for (int shift = 0; shift < 48; shift += kBits) {
+        std::fill(count.begin(), count.end(), 0u);
+        for (const uint64_t k : keys)
+            ++count[(k >> shift) & (kBuckets - 1)];
+        uint32_t sum = 0;
+        for (uint32_t& c : count) {
+            const uint32_t n = c;
+            c = sum;
+            sum += n;
+        }
+        for (const uint64_t k : keys)
+            tmp[count[(k >> shift) & (kBuckets - 1)]++] = k;
+        keys.swap(tmp);
+    }
+}
 }  // namespace
 
 int sample_token(const float* logits, size_t vocab, const uint16_t* history, size_t n_history,
@@ -88,28 +120,34 @@ int sample_token(const float* logits, size_t vocab, const uint16_t* history, siz
     for (size_t k = 0; k < n_banned; ++k)
         if (banned[k] < vocab)
             score[banned[k]] = -std::numeric_limits<float>::infinity();
-    std::vector<uint16_t> order;
-    order.reserve(vocab);
+    // The order is a strict total order, so the first top_k ids are the same whichever
+    // selection or sorting algorithm finds them.
+    thread_local std::vector<uint64_t> keys, tmp;
+    keys.clear();
     for (size_t i = 0; i < vocab; ++i)
         if (std::isfinite(score[i]))
-            order.push_back((uint16_t)i);
-    if (order.empty())
+            keys.push_back(order_key(score[i], (uint16_t)i));
+    if (keys.empty())
         return fail(MLA_ERR_INVALID_ARGUMENT, "All tokens are banned");
-    const auto before = [&](uint16_t a, uint16_t b) {
-        return score[a] > score[b] || (score[a] == score[b] && a < b);
-    };
-    // `before` is a strict total order, so the first top_k ids are the same whichever
-    // selection algorithm finds them.
-    if (c.top_k > 0 && (size_t)c.top_k < order.size()) {
-        std::partial_sort(order.begin(), order.begin() + c.top_k, order.end(), before);
-        order.resize((size_t)c.top_k);
+    if (c.top_k > 0 && (size_t)c.top_k < keys.size()) {
+        std::partial_sort(keys.begin(), keys.begin() + c.top_k, keys.end());
+        keys.resize((size_t)c.top_k);
     } else {
-        std::sort(order.begin(), order.end(), before);
+        radix_sort48(keys, tmp);
     }
-    std::vector<double> prob(order.size());
+    thread_local std::vector<uint16_t> order;
+    thread_local std::vector<double> prob;
+    order.resize(keys.size());
+    prob.resize(keys.size());
+    for (size_t i = 0; i < keys.size(); ++i)
+        order[i] = (uint16_t)(keys[i] & 0xffff);
+    // exp of an argument below -746 is 0 in double precision; skipping the call for
+    // those terms leaves every probability and the sum unchanged.
+    const float top = score[order[0]];
     double sum = 0;
     for (size_t i = 0; i < order.size(); ++i) {
-        prob[i] = std::exp((double)(score[order[i]] - score[order[0]]) / c.temperature);
+        const double z = (double)(score[order[i]] - top) / c.temperature;
+        prob[i] = z < -746.0 ? 0.0 : std::exp(z);
         sum += prob[i];
     }
     double kept = 0;

@@ -27,6 +27,7 @@
 #include <condition_variable>
 #include <cstring>
 #include <deque>
+#include <functional>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -70,6 +71,76 @@ struct Request {
 };
 using RequestPtr = std::shared_ptr<Request>;
 
+// A few helper threads that run the host side of a step's rows (sampling from 16 K-wide
+// logits is the one costly part) in parallel with the stepping thread.
+class Workers {
+  public:
+    explicit Workers(int helpers) {
+        for (int i = 0; i < helpers; ++i)
+            threads_.emplace_back([this] { loop(); });
+    }
+    ~Workers() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            quit_ = true;
+        }
+        go_.notify_all();
+        for (std::thread& t : threads_)
+            t.join();
+    }
+    // fn(i) for every i in [0, count), on the helpers and the calling thread.
+    void run(int count, const std::function<void(int)>& fn) {
+        if (threads_.empty() || count < 2) {
+            for (int i = 0; i < count; ++i)
+                fn(i);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            fn_ = &fn;
+            count_ = count;
+            next_ = 0;
+            busy_ = (int)threads_.size();
+            ++epoch_;
+        }
+        go_.notify_all();
+        drain();
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [&] { return busy_ == 0; });
+        fn_ = nullptr;
+    }
+
+  private:
+    void drain() {
+        for (int i; (i = next_.fetch_add(1)) < count_;)
+            (*fn_)(i);
+    }
+    void loop() {
+        uint64_t seen = 0;
+        for (;;) {
+            {
+                std::unique_lock<std::mutex> lk(mu_);
+                go_.wait(lk, [&] { return quit_ || epoch_ != seen; });
+                if (quit_)
+                    return;
+                seen = epoch_;
+            }
+            drain();
+            std::lock_guard<std::mutex> lk(mu_);
+            if (--busy_ == 0)
+                done_.notify_one();
+        }
+    }
+    std::vector<std::thread> threads_;
+    std::mutex mu_;
+    std::condition_variable go_, done_;
+    const std::function<void(int)>* fn_ = nullptr;
+    int count_ = 0, busy_ = 0;
+    std::atomic<int> next_{0};
+    uint64_t epoch_ = 0;
+    bool quit_ = false;
+};
+
 struct Row {
     Request* r;
     int count;
@@ -102,7 +173,9 @@ struct Scheduler {
     std::vector<int> b_sessions, b_counts;
     std::vector<uint16_t> b_tokens;
     std::vector<int32_t> b_next;
+    std::vector<int> picks;
     std::vector<float> b_logits;
+    std::unique_ptr<Workers> workers;
 
     void run();
     void admit(Clock::time_point now);
@@ -277,6 +350,7 @@ void Scheduler::run() {
         bool advanced = st == MLA_OK || st == MLA_ERR_NUMERICAL;
         for (int i = 0; i < n && !advanced; ++i)
             advanced = st == MLA_ERR_INVALID_ARGUMENT && b_next[i] == -2;
+        picks.clear();
         for (int i = 0; i < n; ++i) {
             const Row& w = rows[i];
             Request* r = w.r;
@@ -293,8 +367,15 @@ void Scheduler::run() {
             } else {
                 r->decode_s += seconds(t0, t1);
             }
-            if (!w.last)
-                continue;
+            if (w.last)
+                picks.push_back(i);
+        }
+        // Each pick touches only its own request (and reads the shared tokenizer and
+        // banned list), so the picks run in parallel.
+        workers->run((int)picks.size(), [&](int k) {
+            const int i = picks[(size_t)k];
+            const Row& w = rows[(size_t)i];
+            Request* r = w.r;
             const size_t before = r->gen.tokens().size();
             int32_t next = -1;
             int gs;
@@ -314,7 +395,7 @@ void Scheduler::run() {
                 r->failure = mla_last_error();
             }
             r->next = next;
-        }
+        });
 
         lk.lock();
         ++steps;
@@ -400,6 +481,8 @@ int mla_scheduler_create(void* engine, void* tokenizer, const mla_scheduler_conf
         return st;
     Scheduler* raw = S.get();
     try {
+        const unsigned hw = std::thread::hardware_concurrency();
+        S->workers = std::make_unique<Workers>((int)std::min(7u, hw > 1 ? hw - 1 : 0u));
         S->thread = std::thread([raw] { raw->run(); });
     } catch (const std::exception& e) {
         return fail(MLA_ERR_OUT_OF_MEMORY, std::string("mla_scheduler_create: ") + e.what());
