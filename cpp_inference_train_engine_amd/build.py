@@ -1,8 +1,10 @@
-"""Build recipe of the HIP product library ``libmla_hip.so`` (gfx950 only).
+"""Build recipe of the HIP product library ``libmla_hip.so`` (gfx950 only) and of the
+C++ host API ``libmla_host.so`` over it.
 
 Every ``csrc/*.hip`` translation unit is compiled in parallel with hipcc into
 ``_build/`` and linked into ``libmla_hip.so`` next to this file (in-tree, so the
-built library travels with the repository snapshot to the GPU box).
+built library travels with the repository snapshot to the GPU box); ``host/mla_host.cpp``
+is compiled with g++ into ``libmla_host.so`` beside it.
 """
 from __future__ import annotations
 
@@ -53,7 +55,28 @@ def build(verbose: bool = False) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)
+    build_host(verbose)
     return LIB
+
+
+HOST_LIB = os.path.join(PKG, "libmla_host.so")
+
+
+def build_host(verbose: bool = False) -> str:
+    """libmla_host.so: the C++20 host API (host/mla_host.hpp) over libmla_hip.so."""
+    tmp = HOST_LIB + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-std=c++20", "-O2", "-fPIC", "-shared", "-Wall",
+           "-Wextra", "-I", os.path.join(REPO, "include"), "-I", os.path.join(PKG, "host"),
+           os.path.join(PKG, "host", "mla_host.cpp"), "-L", PKG, "-lmla_hip",
+           "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("build of libmla_host.so failed")
+    os.replace(tmp, HOST_LIB)
+    if verbose:
+        print("built", HOST_LIB)
+    return HOST_LIB
 
 
 if __name__ == "__main__":

@@ -7,8 +7,9 @@
  * (include/mini_mla/execution.hpp:28-62) with the factory `make_execution`
  * (execution.hpp:63-66, src/infer/inference.cpp:314-329) dispatching to
  * `make_mps_execution` (execution.hpp:67-68, src/backends/mps_backend.mm:1943-1977).
- * A C++ adapter (cpp_inference_train_engine_amd/host) implements that
- * interface over these functions; other hosts bind them with ctypes / FFI.
+ * The C++20 host API in cpp_inference_train_engine_amd/host (libmla_host.so:
+ * Execution / HipExecution, Tokenizer, InferenceEngine, Server) implements those
+ * interfaces over these functions; other hosts bind them with ctypes / FFI.
  *
  * Conventions
  *  - Every function returns an int status: MLA_OK or MLA_ERR_* (the reference

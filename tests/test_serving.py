@@ -148,12 +148,15 @@ def test_scheduler_matches_private_sessions(gpu, tiny_fixture):
                  "mini_mla_rejected_total 0\n", "mini_mla_first_token_seconds_sum ",
                  "mini_mla_queue_depth 0\n"):
         assert line in text
-    for (p, c, _), g in zip(reqs, got):
+    for (p, c, stream), g in zip(reqs, got):
         private = eng.session()
-        alone = gpu.generate_ids(private, t, p, c)
+        chunks = []
+        alone = gpu.generate_ids(private, t, p, c, callback=lambda s: chunks.append(s) or True)
         private.release()
+        # a streamed request's text is its chunks, each cleaned on its own
+        want_text = "".join(chunks) if stream else alone["text"]
         assert (g["tokens"], g["text"], g["finish_reason"]) == \
-            (alone["tokens"], alone["text"], alone["finish_reason"]), (p, c)
+            (alone["tokens"], want_text, alone["finish_reason"]), (p, c)
         assert g["prompt_tokens"] == len(p) and g["completion_tokens"] == len(g["tokens"])
     eng.close()
 
