@@ -71,6 +71,8 @@ class HipExecution final : public Execution {
             return fail_as<std::span<const float>>(s);
         return Result<std::span<const float>>::success(logits_);
     }
+    [[nodiscard]] int session() const { return session_; }
+    [[nodiscard]] const HipEngine* engine() const { return engine_.get(); }
     Result<std::span<const float>> decode(std::uint16_t token) override {
         const Status s = check(mla_session_decode(engine_->handle(), session_, token, logits_.data()));
         if (!s)
@@ -138,6 +140,32 @@ Result<std::unique_ptr<Execution>> HipEngine::session() {
 
 Status HipEngine::set_banned(std::span<const std::uint16_t> ids) {
     return check(mla_engine_set_banned(h_, ids.data(), ids.size()));
+}
+
+Status HipEngine::step(std::span<Execution* const> sessions,
+                       std::span<const std::vector<std::uint16_t>> tokens,
+                       std::vector<float>* logits, std::vector<std::int32_t>* next_tokens) {
+    if (sessions.size() != tokens.size())
+        return Status::failure(ErrorCode::invalid_argument, "step: one token list per session");
+    std::vector<int> ids, counts;
+    std::vector<std::uint16_t> flat;
+    for (size_t i = 0; i < sessions.size(); ++i) {
+        const auto* x = dynamic_cast<const HipExecution*>(sessions[i]);
+        if (!x || x->engine() != this)
+            return Status::failure(ErrorCode::invalid_argument,
+                                   "step: a session of another engine or backend");
+        ids.push_back(x->session());
+        counts.push_back((int)tokens[i].size());
+        flat.insert(flat.end(), tokens[i].begin(), tokens[i].end());
+    }
+    const size_t n = ids.size();
+    if (logits)
+        logits->assign(n * (size_t)config_.vocab_size, 0.0f);
+    if (next_tokens)
+        next_tokens->assign(n, 0);
+    return check(mla_engine_step(h_, (int)n, ids.data(), counts.data(), flat.data(),
+                                 logits ? logits->data() : nullptr,
+                                 next_tokens ? next_tokens->data() : nullptr));
 }
 
 Result<std::unique_ptr<Execution>> make_hip_execution(const std::shared_ptr<HipEngine>& engine) {

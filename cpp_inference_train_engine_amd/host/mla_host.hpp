@@ -111,6 +111,13 @@ class HipEngine : public std::enable_shared_from_this<HipEngine> {
     Result<std::unique_ptr<Execution>> session();
     // The ids the greedy token of batched steps skips (sample_token's banned list).
     Status set_banned(std::span<const std::uint16_t> ids);
+    // One batched forward (continuous batching): sessions[i], a session of this engine,
+    // appends tokens[i] (one token: a decode; several: a prompt chunk).  logits (may be
+    // null) receives [n x vocab] of each session's last new token, next_tokens (may be
+    // null) its greedy token (mla_engine_step).
+    Status step(std::span<Execution* const> sessions,
+                std::span<const std::vector<std::uint16_t>> tokens, std::vector<float>* logits,
+                std::vector<std::int32_t>* next_tokens);
 
   private:
     HipEngine() = default;

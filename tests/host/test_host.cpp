@@ -251,6 +251,51 @@ HOST_TEST(forks_share_weights_and_reject_bad_input, true) {
     CHECK(!none && none.error().code == ErrorCode::invalid_argument);
 }
 
+HOST_TEST(batched_step_equals_single_sessions, true) {
+    const ModelConfig m = tiny();
+    const std::vector<float> params = tiny_params(m, 2);
+    auto engine = HipEngine::create(m, params, {8, 64, 48, 16});
+    REQUIRE(engine);
+    HipEngine& e = *engine.value();
+    std::vector<std::vector<uint16_t>> prompts;
+    for (int k = 0; k < 4; ++k)
+        prompts.push_back(prompt_ids(1 + 9 * k, m.vocab_size, 30 + (uint64_t)k));
+    std::vector<std::unique_ptr<Execution>> solo, batch;
+    std::vector<std::vector<float>> want;
+    for (const auto& p : prompts) {
+        auto a = e.session(), b = e.session();
+        REQUIRE(a && b);
+        auto l = a.value()->prefill(p);
+        REQUIRE(l);
+        want.emplace_back(l.value().begin(), l.value().end());
+        solo.push_back(std::move(a).value());
+        batch.push_back(std::move(b).value());
+    }
+    // sessions 0 and 1 prefilled alone, then one step: their decodes beside 2 and 3's prompts
+    REQUIRE(batch[0]->prefill(prompts[0]) && batch[1]->prefill(prompts[1]));
+    const std::vector<std::vector<uint16_t>> chunks = {{7}, {9}, prompts[2], prompts[3]};
+    for (int k = 0; k < 2; ++k) {
+        auto l = solo[(size_t)k]->decode(chunks[(size_t)k][0]);
+        REQUIRE(l);
+        want[(size_t)k].assign(l.value().begin(), l.value().end());
+    }
+    std::vector<Execution*> raw;
+    for (auto& b : batch)
+        raw.push_back(b.get());
+    std::vector<float> logits;
+    std::vector<int32_t> next;
+    REQUIRE(e.step(raw, chunks, &logits, &next));
+    float worst = 0;
+    for (size_t k = 0; k < 4; ++k)
+        worst = std::max(worst, max_abs_diff(std::span<const float>(logits).subspan(
+                                                 k * (size_t)m.vocab_size, (size_t)m.vocab_size),
+                                             want[k]));
+    CHECK(worst <= 1e-5F);
+    CHECK(next.size() == 4);
+    std::vector<Execution*> wrong = {raw[0], raw[0]};  // a session twice
+    CHECK(!e.step(wrong, std::vector<std::vector<uint16_t>>{{1}, {2}}, nullptr, nullptr));
+}
+
 HOST_TEST(inference_engine_and_server_on_an_export, true) {
     auto loaded = InferenceEngine::load(export_dir, {8, 64, 64, 16});
     REQUIRE(loaded);
