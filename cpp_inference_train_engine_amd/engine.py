@@ -55,9 +55,18 @@ class HipEngine:
         return self._h
 
     def close(self):
+        # Schedulers running on this engine stop first: their threads use it.
+        for dependent in list(getattr(self, "_dependents", ())):
+            dependent.close()
         if getattr(self, "_h", None):
             lib().mla_engine_destroy(self._h)
             self._h = None
+
+    def _attach(self, dependent) -> None:
+        import weakref
+        if not hasattr(self, "_dependents"):
+            self._dependents = weakref.WeakSet()
+        self._dependents.add(dependent)
 
     def __del__(self):
         self.close()

@@ -50,6 +50,7 @@ class Scheduler:
         check(lib().mla_scheduler_create(engine.handle, tokenizer._h, C.byref(c), C.byref(h)))
         self._h, self.engine, self.tokenizer = h, engine, tokenizer
         self.max_new_tokens = max_new_tokens
+        engine._attach(self)  # closing the engine stops this scheduler first
 
     def close(self):
         if getattr(self, "_h", None):
