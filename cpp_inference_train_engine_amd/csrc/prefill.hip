@@ -14,8 +14,9 @@
 //
 // prefill_page_kernel -- the production kernel (H <= 16, kv_rank 128, rope 16,
 //   64-token tiled pages).  Every head of a query shares the latent, so the kernel
-//   flattens (query, head) into q-rows r = i*H + h: a workgroup of 4 waves owns 128
-//   consecutive q-rows of one session (16 queries at H = 8), a wave QT 16-row tiles.
+//   flattens (query, head) into q-rows r = i*H + h: a workgroup of 4 waves (two
+//   q-groups x two halves of each page's tokens) owns 32 consecutive q-rows of one
+//   session (4 queries at H = 8), a q-group QT = 1 16-row tile.
 //   The session's pages stream through a double-buffered LDS copy (the tiled record
 //   as stored); per page and q-tile
 //     S^T = K . Q^T     v_mfma_f32_16x16x32: the page's token tiles, read from LDS
@@ -441,7 +442,10 @@ __global__ __launch_bounds__(kPgThreads) void prefill_generic_kernel(PrefillArgs
         a.lse[fr] = (m_run + __log2f(l_run)) * kLn2;
 }
 
-constexpr int kPfQT = 2;
+// One 16-row tile per q-group: 32 q-rows per workgroup, 158 VGPRs, three workgroups per
+// CU.  Twice as many workgroups as two tiles would give (measured on config 4: 55.7 us
+// against 62.4 us), so the dispatcher can even out the sessions' unequal key ranges.
+constexpr int kPfQT = 1;
 
 template <typename T>
 hipError_t launch_prefill_page(const PrefillArgs& a, int max_q_len, hipStream_t stream) {
