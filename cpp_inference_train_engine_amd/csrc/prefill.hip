@@ -95,7 +95,8 @@ void prefill_page_kernel(PrefillArgs a) {
     const int32_t* ptab = a.page_table + (long long)b * a.max_pages;
 
     // ---- page staging: 16-byte chunks through registers, slots at or past k_len zeroed.
-    // Two register sets hold pages p+1 and p+2 while page p is consumed from LDS.
+    // One register set holds page p+1 while page p is consumed from LDS (a second set
+    // holding p+2 as well measured no faster and cost 20 VGPRs).
     // Raw buffer loads over the page record: a chunk that must read as zero (slot at or
     // past k_len, an invalid page id, or p >= n_pages) gets an offset outside the record,
     // which the hardware returns as zero.  Every load is issued unconditionally, so no
@@ -132,7 +133,7 @@ void prefill_page_kernel(PrefillArgs a) {
     };
     // Prologue, in issue order: the page ids (staged in LDS, so issuing a later page
     // never waits on memory), the Q operands, then the first two pages.
-    const int id0 = ptab[0], id1 = n_pages > 1 ? ptab[1] : 0;
+    const int id0 = ptab[0];
     constexpr int IDS_PT = kPfMaxIds / THREADS;
     int ids[IDS_PT];
 #pragma unroll
@@ -158,9 +159,8 @@ void prefill_page_kernel(PrefillArgs a) {
                         ? *reinterpret_cast<const V8*>(a.q_rope + fr * RP + 8 * g)
                         : V8{};
     }
-    u32x4 st0[CPT], st1[CPT];
+    u32x4 st0[CPT];
     load_page(st0, id0, 0);
-    load_page(st1, id1, 1);
 #pragma unroll
     for (int k = 0; k < IDS_PT; ++k)
         pids[tid + k * THREADS] = ids[k];
@@ -271,23 +271,21 @@ void prefill_page_kernel(PrefillArgs a) {
         }
     };
     // Page p lives in buf[p % 2]; its successor waits in st[(p + 1) % 2].  One step:
-    // send page p+2 into the register set page p came through, consume page p, store
-    // page p+1 into the other buffer (its last readers finished before the previous
-    // barrier), barrier.  Steps are unrolled in pairs so every buffer and register set
-    // is named statically.
-    auto step = [&](const uint16_t* cur, uint16_t* nx, u32x4 (&st_next)[CPT],
-                    u32x4 (&st_far)[CPT], int p) {
-        load_page(st_far, pids[min(p + 2, n_pages - 1)], p + 2);
+    // load page p+1 into the registers, consume page p, store page p+1 into the other
+    // buffer (its last readers finished before the previous barrier), barrier.  Steps
+    // are unrolled in pairs so every buffer is named statically.
+    auto step = [&](const uint16_t* cur, uint16_t* nx, int p) {
+        load_page(st0, pids[min(p + 1, n_pages - 1)], p + 1);
         compute(cur, p);
         if (p + 1 < n_pages)
-            store_page(st_next, nx);
+            store_page(st0, nx);
         __syncthreads();
     };
     for (int p = 0; p < n_pages; p += 2) {
-        step(buf0, buf1, st1, st0, p);
+        step(buf0, buf1, p);
         if (p + 1 >= n_pages)
             break;
-        step(buf1, buf0, st0, st1, p + 1);
+        step(buf1, buf0, p + 1);
     }
 
     // ---- the two token halves of each q-group meet in LDS; normalise and store ----
@@ -442,8 +440,8 @@ __global__ __launch_bounds__(kPgThreads) void prefill_generic_kernel(PrefillArgs
         a.lse[fr] = (m_run + __log2f(l_run)) * kLn2;
 }
 
-// One 16-row tile per q-group: 32 q-rows per workgroup, 158 VGPRs, three workgroups per
-// CU.  Twice as many workgroups as two tiles would give (measured on config 4: 55.7 us
+// One 16-row tile per q-group: 32 q-rows per workgroup, 138 VGPRs, three workgroups per
+// CU (four, at 124 VGPRs and 1024 staged page ids, measured slower: 62.3 us).  Twice as many workgroups as two tiles would give (measured on config 4: 55.7 us
 // against 62.4 us), so the dispatcher can even out the sessions' unequal key ranges.
 constexpr int kPfQT = 1;
 
