@@ -200,3 +200,40 @@ def test_scheduler_limits_queue_deadline_cancel(gpu, tiny_fixture):
         m = sch.metrics()
         assert (m["rejected"], m["errors"], m["completed"]) == (1, 3, 2)
     eng.close()
+
+
+def test_scheduler_from_many_threads(gpu, tiny_fixture):
+    """Submitters and pollers on several host threads at once (the server's accept loop
+    and its clients): every request's result equals the same request run alone."""
+    import threading
+    eng = _engine(gpu, tiny_fixture, sessions=4)
+    t = gpu.HipTokenizer(TOK_TINY)
+    reqs = _requests(gpu, t) * 2  # 20 requests, 4 sessions: most of them queue
+    results = [None] * len(reqs)
+    errors = []
+    with gpu.Scheduler(eng, t, max_context=64, max_new_tokens=32, max_queue=32) as sch:
+        def client(k0):
+            try:
+                for k in range(k0, len(reqs), 4):
+                    p, c, stream = reqs[k]
+                    results[k] = sch.result(sch.submit(p, c, stream=stream), timeout=60)
+            except Exception as e:  # reported below, with the thread's request
+                errors.append((k0, repr(e)))
+        threads = [threading.Thread(target=client, args=(k0,)) for k0 in range(4)]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join(120)
+        assert not any(th.is_alive() for th in threads)
+        m = sch.metrics()
+    assert not errors, errors
+    assert m["completed"] == len(reqs) and m["rejected"] == 0
+    for (p, c, stream), g in zip(reqs, results):
+        private = eng.session()
+        chunks = []
+        alone = gpu.generate_ids(private, t, p, c, callback=lambda s: chunks.append(s) or True)
+        private.release()
+        want_text = "".join(chunks) if stream else alone["text"]
+        assert (g["tokens"], g["text"], g["finish_reason"]) == \
+            (alone["tokens"], want_text, alone["finish_reason"]), (p, c)
+    eng.close()
