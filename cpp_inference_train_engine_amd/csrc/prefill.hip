@@ -270,7 +270,7 @@ void prefill_page_kernel(PrefillArgs a) {
             }
         }
     };
-    // Page p lives in buf[p % 2]; its successor waits in st[(p + 1) % 2].  One step:
+    // Page p lives in buf[p % 2]; its successor waits in the registers st0.  One step:
     // load page p+1 into the registers, consume page p, store page p+1 into the other
     // buffer (its last readers finished before the previous barrier), barrier.  Steps
     // are unrolled in pairs so every buffer is named statically.
