@@ -482,7 +482,7 @@ int mla_scheduler_create(void* engine, void* tokenizer, const mla_scheduler_conf
     Scheduler* raw = S.get();
     try {
         const unsigned hw = std::thread::hardware_concurrency();
-        S->workers = std::make_unique<Workers>((int)std::min(7u, hw > 1 ? hw - 1 : 0u));
+        S->workers = std::make_unique<Workers>((int)std::min(15u, hw > 1 ? hw - 1 : 0u));
         S->thread = std::thread([raw] { raw->run(); });
     } catch (const std::exception& e) {
         return fail(MLA_ERR_OUT_OF_MEMORY, std::string("mla_scheduler_create: ") + e.what());
