@@ -122,6 +122,63 @@ def test_mla36m_engine_matches_oracle(gpu, orc):
 
 
 @pytest.mark.gpu
+def test_config2_full_workload_matches_oracle(gpu, orc):
+    """Config 2 at its own workload: mla36m (Model::create seed 0, fp16 weights), one
+    session, a 1024-id prompt from Rng(0).bounded(16384) prefilled as ONE 1024-row chunk,
+    then 64 greedy decode calls, against the oracle's CpuDecoder on the same fp16 weights
+    with an fp16-rounded cache (tests/test_mps.cpp:126-166 runs the same prefill / decode
+    comparison at 0.015; LOGIT_ATOL here).  The decode tokens follow the oracle's greedy
+    choice; the GPU's greedy token must equal it wherever the oracle's top-2 margin
+    exceeds 2 * LOGIT_ATOL."""
+    cfg, params, p16 = _models(MLA36M)
+    prompt = _prompt(1024, MLA36M["vocab_size"], seed=0)
+    eng = _engine(gpu, MLA36M, params, max_sessions=2, max_rows=1024, num_pages=20)
+    ex = eng.session()
+    dec = orc.Decoder(cfg, p16, round_cache=True)
+    got, want = ex.prefill(prompt), dec.prefill(prompt)
+    err = np.abs(got - want).max()
+    _say(f"config2 prefill (1024 rows, one chunk) max |err| {err:.3e}")
+    assert err <= LOGIT_ATOL
+    worst, checked = err, 0
+    for i in range(64):
+        tok = int(np.argmax(want))
+        if _margin_ok(want):
+            assert int(np.argmax(got)) == tok, f"greedy token at step {i}"
+            checked += 1
+        got, want = ex.decode(tok), dec.decode(tok)
+        err = np.abs(got - want).max()
+        worst = max(worst, err)
+        assert err <= LOGIT_ATOL, f"decode step {i}: {err}"
+    assert ex.position == 1088
+    _say(f"config2 64 decodes: max |err| {worst:.3e}, greedy tokens checked {checked}/64")
+    eng.close()
+
+
+@pytest.mark.gpu
+def test_shorter_reprefill_after_decoding(gpu, orc):
+    """tests/test_mps.cpp:158-165: an execution that has prefilled and decoded takes a new,
+    shorter prompt; prefill restarts at position 0 and returns that prompt's logits."""
+    cfg, params, p16 = _models(MLA36M, seed=9)
+    eng = _engine(gpu, MLA36M, params, max_sessions=2, max_rows=64, num_pages=8)
+    ex = eng.session()
+    dec = orc.Decoder(cfg, p16, round_cache=True)
+    tokens = [1, 5, 8]
+    np.testing.assert_allclose(ex.prefill(tokens), dec.prefill(tokens), rtol=0, atol=LOGIT_ATOL)
+    for i in range(14):
+        t = (i * 3 + 2) % 32
+        np.testing.assert_allclose(ex.decode(t), dec.decode(t), rtol=0, atol=LOGIT_ATOL)
+    assert ex.position == 17
+    free_before = eng.info()["free_pages"]
+    got = ex.prefill([2, 3])
+    assert ex.position == 2 and eng.info()["free_pages"] == free_before
+    want = orc.forward(cfg, p16, [2, 3])[-1]
+    np.testing.assert_allclose(got, want, rtol=0, atol=LOGIT_ATOL)
+    np.testing.assert_allclose(ex.decode(4), orc.forward(cfg, p16, [2, 3, 4])[-1], rtol=0,
+                               atol=LOGIT_ATOL)
+    eng.close()
+
+
+@pytest.mark.gpu
 def test_decode_equals_full_recomputation_on_gpu(gpu):
     """tests/test_training.cpp:52-76 on the engine: after prefill(prompt) and k decodes,
     the logits equal those of prefill(prompt + the k tokens) (one chunk and 3 chunks)."""

@@ -157,6 +157,69 @@ def _check_step(r, what):
     assert (r["next"] >= 0).all()
 
 
+def _config3_case(seed=0):
+    """Config 3 exactly as bench.py times it: mla36m (max_sequence_length 4608) with
+    Model::create-scaled weights from the oracle (seed 0, fp16), 64 sessions whose lengths
+    after the append are U[128, 4096] (ragged_decode_batch, reference Rng), 10 layers of
+    N(0,1) fp16 pages at a random page permutation, one new token per session."""
+    import torch
+    import oracle
+    import cpp_inference_train_engine_amd as mla
+    from cpp_inference_train_engine_amd.ops import latent_word, rope_word
+    from cpp_inference_train_engine_amd.workloads import MLA36M as CFG3, ragged_decode_batch
+    ocfg = oracle.Config.from_dict(CFG3)
+    params = oracle.bits_to_f32(oracle.round_f16(oracle.model_init(ocfg, seed)))
+    L, kv, rp, V, H = (ocfg.n_layers, ocfg.kv_lora_rank, ocfg.head_dim_rope, ocfg.vocab_size,
+                       ocfg.n_heads)
+    batch = ragged_decode_batch(B=64, n_layers=L, seed=seed)
+    B, ps = batch.ctx_len.size, batch.page_size
+    ctx = batch.ctx_len
+    tokens = np.random.default_rng(seed).integers(0, V, size=B).astype(np.int32)
+    _say(f"config3 step: B={B} cached tokens/layer={int(batch.k_len.sum())} "
+         f"pages={batch.num_pages}")
+    model = mla.HipModel(mla.ModelConfig.from_dict(CFG3), params, max_batch=B, page_size=ps)
+    rb = mla.build_metadata(_dev(ctx), _dev(batch.q_len), _dev(batch.cu_pages),
+                            _dev(batch.page_ids), ps, batch.max_pages, batch.num_pages,
+                            split_pages=4)
+    gpu_pages = [_dev(batch.pages[l].view(np.int16)).view(torch.float16) for l in range(L)]
+    ws = mla.decode_workspace(rb.max_work, B, H, kv)
+    logits, nxt = model.step(rb, _dev(tokens), _dev(ctx), gpu_pages, ws)
+    torch.cuda.synchronize()
+    rb.read_info()
+    got_pages = np.stack([p.view(torch.int16).cpu().numpy().view(np.uint16) for p in gpu_pages])
+    model.close()
+    del gpu_pages
+    proj = oracle.output_projection(ocfg, params)
+    lw_all = latent_word(np.arange(ps)[:, None], np.arange(kv)[None, :], ps, kv, rp)
+    rw_all = rope_word(np.arange(ps)[:, None], np.arange(rp)[None, :], ps, kv, rp)
+    want_logits, want_lat, want_rope, got_lat, got_rope = [], [], [], [], []
+    for b in range(B):
+        ids = batch.page_ids[batch.cu_pages[b]:batch.cu_pages[b + 1]]
+        t = np.arange(int(ctx[b]))
+        pg, slot = ids[t // ps], t % ps
+        dec = oracle.Decoder(ocfg, params, absorbed=True, round_cache=True, proj=proj)
+        dec.latent[:, :ctx[b]] = oracle.bits_to_f32(batch.pages[:, pg[:, None], lw_all[slot]])
+        dec.rope[:, :ctx[b]] = oracle.bits_to_f32(batch.pages[:, pg[:, None], rw_all[slot]])
+        dec.position = int(ctx[b])
+        want_logits.append(dec.decode(int(tokens[b])))
+        want_lat.append(dec.latent[:, ctx[b]].copy())
+        want_rope.append(dec.rope[:, ctx[b]].copy())
+        p_new, s_new = ids[ctx[b] // ps], ctx[b] % ps
+        got_lat.append(oracle.bits_to_f32(got_pages[:, p_new, lw_all[s_new]]))
+        got_rope.append(oracle.bits_to_f32(got_pages[:, p_new, rw_all[s_new]]))
+    return dict(logits=logits.cpu().numpy(), next=nxt.cpu().numpy(),
+                want_logits=np.stack(want_logits), lat=np.stack(got_lat),
+                want_lat=np.stack(want_lat), rope=np.stack(got_rope),
+                want_rope=np.stack(want_rope))
+
+
+@pytest.mark.gpu
+def test_model_step_config3_full_lengths(gpu, orc):
+    """The headline step (config 3) at its real lengths: every one of the 64 sessions'
+    logits, appended cache rows and greedy token against the oracle's CpuDecoder."""
+    _check_step(_config3_case(seed=0), "config3 (64 sessions, U[128,4096])")
+
+
 @pytest.mark.gpu
 def test_model_step_tiny_matches_oracle(gpu, orc):
     """tiny-test config (H=2, kv_rank=8, rope=4): generic attention path, padded tiles."""
