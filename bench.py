@@ -78,17 +78,37 @@ def traffic_from_profile(path=TRAFFIC_FILE):
         return None
 
 
-def cpu_baseline(batch, params, seconds: float):
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(batch, params, seconds: float, config2_trace=None):
     """The reference CPU path for the same step: the oracle's fp32 restatement of
     CpuDecoder::decode (inference.cpp:69-174: projections, absorbed attention over the
     session's contiguous cache, FFN, tied logits) on a bounded sample of the batch's
     sessions, one session per thread (forks decode concurrently, inference.cpp:238),
-    repeated for `seconds`; then the same sample on one thread."""
+    repeated for `seconds`; then the same sample on one thread.  Its products run on the
+    CBLAS numpy ships (OpenBLAS, one thread per call) in place of the reference's
+    Accelerate calls.  With `config2_trace` (the GPU's config-2 run), the CPU path also
+    replays config 2 on the same fp16 weights and tokens and reports the GPU's logit
+    error against it, as the reference's decode bench records (apps/bench_main.cpp:
+    378-396)."""
     import concurrent.futures as cf
     import oracle
     from cpp_inference_train_engine_amd.workloads import MLA36M
+    blas = oracle.use_blas(True)
     cfg = oracle.Config.from_dict(MLA36M)
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    visible = len(os.sched_getaffinity(0))
+    # A one-GPU box allots 16 host cores to its GPU; more threads than that would time
+    # contention with other jobs, not the CPU path.
+    cores = max(1, min(16, visible))
     pick = np.argsort(batch.k_len)[np.linspace(0, len(batch.k_len) - 1, cores).astype(int)]
     decs = []
     proj = oracle.output_projection(cfg, params)  # prepare_projections, once per model
@@ -118,12 +138,37 @@ def cpu_baseline(batch, params, seconds: float):
     many, n_many = run(cores)
     single, n_single = run(1)
     mean_ctx = float(np.mean([n for _, n in decs]))
-    return {"value": round(many, 2), "unit": "tok/s", "cores": cores, "kind": "port",
-            "one_core_value": round(single, 2),
-            "sample": f"full decode step (oracle CpuDecoder restatement, fp32) of {len(decs)} "
-                      f"sessions spread over the batch's lengths (mean context {mean_ctx:.0f}): "
-                      f"{n_many} tokens on {cores} threads, one session per thread; "
-                      f"{n_single} tokens on 1 thread"}
+    out = {"value": round(many, 2), "unit": "tok/s", "cores": cores, "kind": "port",
+           "one_core_value": round(single, 2),
+           "cpu_model": cpu_model(), "host_cores_visible": visible,
+           "blas": f"{blas} (numpy's scipy_openblas64, standing in for Accelerate)"
+                   if blas else "none found: unblocked C loops",
+           "sample": f"full decode step (oracle CpuDecoder restatement, fp32) of {len(decs)} "
+                     f"sessions spread over the batch's lengths (mean context {mean_ctx:.0f}): "
+                     f"{n_many} tokens on {cores} threads, one session per thread; "
+                     f"{n_single} tokens on 1 thread"}
+    if config2_trace is not None:
+        p16 = oracle.bits_to_f32(oracle.round_f16(params))
+        d = oracle.Decoder(cfg, p16, round_cache=True)
+        t0 = time.perf_counter()
+        want = d.prefill(config2_trace["prompt"])
+        prefill_s = time.perf_counter() - t0
+        pre_err = float(np.abs(config2_trace["prefill_logits"] - want).max())
+        dec_err, times = 0.0, []
+        for tok, got in zip(config2_trace["tokens"], config2_trace["decode_logits"]):
+            t0 = time.perf_counter()
+            want = d.decode(int(tok))
+            times.append(time.perf_counter() - t0)
+            dec_err = max(dec_err, float(np.abs(got - want).max()))
+        out["config2"] = {"prefill_max_abs_err": round(pre_err, 6),
+                          "decode_max_abs_err": round(dec_err, 6),
+                          "cpu_prefill_ms": round(prefill_s * 1e3, 1),
+                          "cpu_decode_ms_median": round(float(np.median(times)) * 1e3, 3),
+                          "sample": "config 2 replayed on the CPU path (1 thread): the same "
+                                    "1024-token prompt and the GPU run's 64 decode tokens, "
+                                    "fp16-rounded weights and cache"}
+    oracle.use_blas(False)
+    return out
 
 
 def config2_leg(mla, params, steps: int = 64, prompt_len: int = 1024):
@@ -131,33 +176,48 @@ def config2_leg(mla, params, steps: int = 64, prompt_len: int = 1024):
     ids uniform in [0, vocab)), then 64 greedy decode steps through the session engine
     (mla_session_prefill / mla_session_decode: the reference's Execution::prefill and
     decode, logits returned to the host every step).  Times each decode call on the host
-    clock like apps/bench_main.cpp:12-30 (median, p95)."""
+    clock like apps/bench_main.cpp:12-30 (median, p95).  Every decode's logits are then
+    checked against the same backend's full forward of prompt + tokens (the reference's
+    decode bench compares decode with Model::forward, bench_main.cpp:378-396).  Returns
+    (record, trace): the trace (prompt, tokens, logits) lets the CPU-baseline leg measure
+    the same logits against the CPU path."""
     from cpp_inference_train_engine_amd.workloads import MLA36M, SplitMix64
     cfg = mla.ModelConfig.from_dict(MLA36M)
     rng = SplitMix64(0)
     prompt = [rng.bounded(MLA36M["vocab_size"]) for _ in range(prompt_len)]
-    eng = mla.HipEngine(cfg, params, max_sessions=1, max_rows=prompt_len, num_pages=32)
+    eng = mla.HipEngine(cfg, params, max_sessions=2, max_rows=prompt_len, num_pages=48)
     ex = eng.session()
     ex.prefill(prompt)  # warm
     t0 = time.perf_counter()
     logits = ex.prefill(prompt)
     prefill_ms = (time.perf_counter() - t0) * 1e3
+    trace = {"prompt": prompt, "prefill_logits": logits, "tokens": [], "decode_logits": []}
     times = []
     for _ in range(steps):
         tok = int(np.argmax(logits))
         t0 = time.perf_counter()
         logits = ex.decode(tok)
         times.append((time.perf_counter() - t0) * 1e3)
+        trace["tokens"].append(tok)
+        trace["decode_logits"].append(logits)
+    st = ex.stats()
+    full = eng.forward(prompt + trace["tokens"], 1, prompt_len + steps)
+    fwd_err = float(np.abs(trace["prefill_logits"] - full[prompt_len - 1]).max())
+    for i, got in enumerate(trace["decode_logits"]):
+        fwd_err = max(fwd_err, float(np.abs(got - full[prompt_len + i]).max()))
     eng.close()
     med = float(np.median(times))
-    return {"workload": "config 2: mla36m, one session, 1024-token prompt, 64 greedy decode "
-                        "steps through the session engine (host-timed decode calls, logits "
-                        "to host each step)",
-            "prefill_ms": round(prefill_ms, 3), "decode_ms_median": round(med, 4),
-            "decode_ms_p95": round(float(np.percentile(times, 95)), 4),
-            "tok_per_s": round(1e3 / med, 1),
-            "reference_mps_fp16_ms": 3.583,
-            "vs_reference_mps": round(3.583 / med, 2)}
+    rec = {"workload": "config 2: mla36m, one session, 1024-token prompt, 64 greedy decode "
+                       "steps through the session engine (host-timed decode calls, logits "
+                       "to host each step)",
+           "prefill_ms": round(prefill_ms, 3), "decode_ms_median": round(med, 4),
+           "decode_ms_p95": round(float(np.percentile(times, 95)), 4),
+           "tok_per_s": round(1e3 / med, 1),
+           "decode_vs_forward_max_abs_err": round(fwd_err, 6),
+           "kernels_per_decode": round((st["kernel_submissions"]) / max(st["graph_submissions"], 1), 1),
+           "reference_mps_fp16_ms": 3.583,
+           "vs_reference_mps": round(3.583 / med, 2)}
+    return rec, trace
 
 
 def serve_leg(mla, params, temperature: float, requests: int = 64, new_tokens: int = 64):
@@ -198,7 +258,7 @@ def serve_leg(mla, params, temperature: float, requests: int = 64, new_tokens: i
     return out
 
 
-def config4_leg(mla, torch, reps: int = 20):
+def config4_leg(mla, torch, reps: int = 20, n_pools: int = 4):
     """Config 4 (one layer, kernels only): 8 prefill chunks of 512 tokens on contexts
     U[0, 2048] + 120 decode sessions with log-normal lengths (median 2048, sigma 1, cap
     16384), half of the sessions aliasing a 256-token prefix.  Times the chunked-prefill
@@ -213,6 +273,9 @@ def config4_leg(mla, torch, reps: int = 20):
     rb = mla.build_metadata(dev(b.ctx_len), dev(b.q_len), dev(b.cu_pages), dev(b.page_ids), 64,
                             b.max_pages, b.num_pages, split_pages=4, max_work=mw, max_rows=rows)
     pages = dev(b.pages[0].view(np.int16)).view(torch.float16)
+    # Copies of the layer's pool, visited in turn, so the working set (n_pools x ~120 MB)
+    # exceeds the 256 MB Infinity Cache and every call reads HBM.
+    pools = [pages] + [pages.clone() for _ in range(n_pools - 1)]
     ql = dev(b.q_latent.view(np.int16)).view(torch.float16)
     qr = dev(b.q_rope.view(np.int16)).view(torch.float16)
     out = torch.empty((rows, 8, 128), dtype=torch.float32, device="cuda")
@@ -223,12 +286,13 @@ def config4_leg(mla, torch, reps: int = 20):
     res = {}
     for kind in ("prefill", "decode"):
         def run(n):
-            for _ in range(n):
+            for i in range(n):
+                pool = pools[i % n_pools]
                 if kind == "prefill":
-                    mla.prefill_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16,
+                    mla.prefill_attention(rb, pool, ql, qr, 0.125, kv_rank=128, rope_dim=16,
                                           max_q_len=512, out=out)
                 else:
-                    mla.decode_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16,
+                    mla.decode_attention(rb, pool, ql, qr, 0.125, kv_rank=128, rope_dim=16,
                                          out=out, workspace=ws)
         run(3)
         torch.cuda.synchronize()
@@ -241,9 +305,13 @@ def config4_leg(mla, torch, reps: int = 20):
     rb.read_info()
     tf = flops / res["prefill"] / 1e6
     gbs = dec_tokens * 288 / res["decode"] / 1e3
+    pool_mb = pages.numel() * 2 / 1e6
+    del pools
     return {"workload": "config 4 (one layer): 8 x 512-token chunks on contexts U[0,2048] + "
                         "120 log-normal decode sessions (median 2048, sigma 1, cap 16384), "
                         "4-page prefix shared by 64 sessions, fp16",
+            "pools": f"{n_pools} copies of the layer's {pool_mb:.0f} MB pool visited in turn "
+                     f"({n_pools * pool_mb:.0f} MB > the 256 MB Infinity Cache)",
             "prefill_kernel": {"us": round(res["prefill"], 2), "gflop": round(flops / 1e9, 3),
                                "tflops": round(tf, 1), "mfma_peak_tflops": 2500.0,
                                "frac": round(tf / 2500.0, 4)},
@@ -329,7 +397,7 @@ def main():
         copy_probe(torch, args.copy_probe_mib)
     from cpp_inference_train_engine_amd.workloads import MLA36M, model_params
     if args.only:
-        legs = {"config2": lambda: config2_leg(mla, model_params(MLA36M, seed=0)),
+        legs = {"config2": lambda: config2_leg(mla, model_params(MLA36M, seed=0))[0],
                 "config4": lambda: config4_leg(mla, torch),
                 "config5": lambda: config5_leg(mla, torch),
                 "serve": lambda: {"greedy": serve_leg(mla, model_params(MLA36M, seed=0), 0.0),
@@ -467,12 +535,18 @@ def main():
                            "frac": round(attn_gbs / HBM_PEAK_GBS, 4)},
     }
     model.close()
+    trace = None
     if not args.no_secondary:
-        result["config2"] = config2_leg(mla, params)
+        result["config2"], trace = config2_leg(mla, params)
         result["config4"] = config4_leg(mla, torch)
         result["config5"] = config5_leg(mla, torch)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(batch, params, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(batch, params, args.cpu_seconds, trace)
+        if trace is not None:  # the CPU path's verdict on config 2's logits
+            c2 = result["cpu_baseline"].pop("config2")
+            result["config2"]["decode_max_abs_err"] = c2["decode_max_abs_err"]
+            result["config2"]["prefill_max_abs_err"] = c2["prefill_max_abs_err"]
+            result["config2"]["cpu_path"] = c2
     print(json.dumps(result), flush=True)
 
 

@@ -79,6 +79,10 @@ _SIGNATURES = {
     "mla_session_prefill": (C.c_int, [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p]),
     "mla_session_decode": (C.c_int, [C.c_void_p, C.c_int, C.c_uint16, C.c_void_p]),
     "mla_engine_step": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 5),
+    "mla_model_update_weights": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "mla_engine_update_weights": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "mla_engine_stats": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "mla_engine_forward": (C.c_int, [C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_void_p]),
     "mla_export_read_config": (C.c_int, [C.c_char_p, C.c_void_p]),
     "mla_export_read": (C.c_int, [C.c_char_p, C.c_void_p, C.c_void_p, C.c_size_t]),
     "mla_config_hash": (C.c_int, [C.c_void_p, C.c_char_p]),
@@ -110,6 +114,7 @@ _SIGNATURES = {
     "mla_scheduler_config_init": (None, [C.c_void_p]),
     "mla_scheduler_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "mla_scheduler_destroy": (C.c_int, [C.c_void_p]),
+    "mla_scheduler_stop": (C.c_int, [C.c_void_p]),
     "mla_scheduler_submit": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_int,
                                        C.c_void_p]),
     "mla_scheduler_cancel": (C.c_int, [C.c_void_p, C.c_uint64]),

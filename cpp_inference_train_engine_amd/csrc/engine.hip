@@ -18,6 +18,7 @@
 #include "mla_model.hpp"
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -31,6 +32,7 @@ constexpr int kSplitPages = 4;  // MLA_DECODE_SPLIT_PAGES
 struct Session {
     bool active = false;
     int length = 0;              // tokens cached: the reference's position_
+    uint64_t revision = 0;       // weight revision its cache was computed with
     std::vector<int32_t> pages;  // physical page ids, position order
 };
 
@@ -48,6 +50,9 @@ struct Engine {
     std::vector<int32_t> free_;  // free page ids (stack)
     std::vector<Session> sessions;
     uint64_t steps = 0;
+    uint64_t revision = 0;  // bumped by mla_engine_update_weights
+    // stats: model forwards submitted, host waits on the stream, kernels and copies issued
+    uint64_t host_waits = 0, meta_launches = 0, copies = 0;
     // device
     int32_t* d_in = nullptr;  // staged inputs, see step()
     size_t in_cap = 0;        // int32 elements
@@ -55,11 +60,14 @@ struct Engine {
             *nsplit = nullptr, *cu_split = nullptr, *w_sess = nullptr, *w_split = nullptr,
             *w_desc = nullptr, *w_pages = nullptr, *info = nullptr, *d_next = nullptr;
     float* d_logits = nullptr;
+    float* d_logits_all = nullptr;  // [max_rows x vocab] for mla_engine_forward (first use)
+    int32_t* d_next_all = nullptr;  // [max_rows]
     void* workspace = nullptr;
     size_t ws_bytes = 0;
     // pinned host
     int32_t* h_in = nullptr;
     float* h_logits = nullptr;
+    float* h_logits_all = nullptr;  // [max_rows x vocab] pinned, with d_logits_all
     int32_t* h_out = nullptr;  // info[4] then next tokens[max_sessions]
     std::vector<void*> dev_allocs, host_allocs;
 
@@ -123,6 +131,7 @@ hipError_t copy_page(Engine* E, int32_t dst, int32_t src) {
                                             hipMemcpyDeviceToDevice, E->stream);
         if (e != hipSuccess)
             return e;
+        ++E->copies;
     }
     return hipSuccess;
 }
@@ -132,7 +141,7 @@ hipError_t copy_page(Engine* E, int32_t dst, int32_t src) {
 // may be null), greedy tokens to `next` [n] (host, may be null).  Lengths advance only
 // on success.
 int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* tokens,
-         float* logits, int32_t* next, const char* fn) {
+         float* logits, int32_t* next, const char* fn, bool all_rows = false) {
     const mla_model_config& c = E->cfg;
     if (n < 1 || n > E->max_sessions || !ids || !counts || !tokens)
         return fail(MLA_ERR_INVALID_ARGUMENT, std::string(fn) + ": invalid batch");
@@ -149,6 +158,10 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
         if (counts[i] < 1 || (long long)S.length + counts[i] > c.max_sequence_length)
             return fail(MLA_ERR_INVALID_ARGUMENT,
                         std::string(fn) + ": prompt exceeds context or is empty");
+        if (S.length > 0 && S.revision != E->revision)  // inference.cpp:71-75
+            return fail(MLA_ERR_INVALID_ARGUMENT,
+                        "Decode requires current-weight prefill, available context, and a "
+                        "valid token");
         rows += counts[i];
         max_q = std::max(max_q, counts[i]);
     }
@@ -229,6 +242,10 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
         rollback();
         return fail(MLA_ERR_INVALID_ARGUMENT, std::string(fn) + ": batch exceeds engine capacity");
     }
+    float* const d_logits = all_rows ? E->d_logits_all : E->d_logits;
+    int32_t* const d_next = all_rows ? E->d_next_all : E->d_next;
+    float* const h_logits = all_rows ? E->h_logits_all : E->h_logits;
+    const long long out_rows = all_rows ? rows : n;
     int32_t* h = E->h_in;
     int32_t *h_ctx = h, *h_q = h + n, *h_cup = h + 2 * n, *h_tok = h + 3 * n + 1;
     int32_t *h_pos = h_tok + rows, *h_ids = h_pos + rows;
@@ -262,19 +279,23 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
                           E->num_pages, E->work_cap};
         st = model_forward(static_cast<Model*>(E->model), E->stream, (int)rows, d_tok, d_pos, n,
                            max_q, md, E->layer_pools.data(), E->workspace, E->ws_bytes,
-                           E->d_logits, E->d_next);
+                           d_logits, d_next, all_rows);
     }
     if (!st) {
         e = hipMemcpyAsync(E->h_out, E->info, 4 * sizeof(int32_t), hipMemcpyDeviceToHost,
                            E->stream);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(E->h_out + 4, E->d_next, n * sizeof(int32_t),
+        if (e == hipSuccess && !all_rows)
+            e = hipMemcpyAsync(E->h_out + 4, d_next, n * sizeof(int32_t),
                                hipMemcpyDeviceToHost, E->stream);
         if (e == hipSuccess && logits)
-            e = hipMemcpyAsync(E->h_logits, E->d_logits, (size_t)n * c.vocab_size * sizeof(float),
+            e = hipMemcpyAsync(h_logits, d_logits,
+                               (size_t)out_rows * c.vocab_size * sizeof(float),
                                hipMemcpyDeviceToHost, E->stream);
         if (e == hipSuccess)
             e = hipStreamSynchronize(E->stream);
+        E->meta_launches += 1;
+        E->copies += 2 + !all_rows + (logits != nullptr);
+        E->host_waits += 1;
         st = gpu_status(e, fn);
     }
     if (!st && E->h_out[0] < 0)
@@ -289,14 +310,21 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
     ++E->steps;
     bool finite = true, open = true;
     for (int i = 0; i < n; ++i) {
-        E->sessions[ids[i]].length += counts[i];
+        Session& S = E->sessions[ids[i]];
+        S.length += counts[i];
+        S.revision = E->revision;
+        if (all_rows)
+            continue;
         finite = finite && E->h_out[4 + i] != -1;
         open = open && E->h_out[4 + i] != -2;
         if (next)
             next[i] = E->h_out[4 + i];
     }
-    if (logits)
-        std::memcpy(logits, E->h_logits, (size_t)n * c.vocab_size * sizeof(float));
+    if (logits && logits != h_logits)
+        std::memcpy(logits, h_logits, (size_t)out_rows * c.vocab_size * sizeof(float));
+    if (all_rows && logits)
+        for (size_t k = 0; k < (size_t)out_rows * c.vocab_size && finite; ++k)
+            finite = std::isfinite(logits[k]);
     if (!finite)  // inference.cpp:170-172
         return fail(MLA_ERR_NUMERICAL, "Nonfinite decode output");
     if (!open)  // inference.cpp:375-377
@@ -530,6 +558,116 @@ int mla_engine_step(void* engine, int n, const int* sessions, const int* counts,
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_engine_step: invalid argument");
     std::lock_guard lock(E->mu);
     return step(E, n, sessions, counts, tokens, logits, next_tokens, "mla_engine_step");
+}
+
+int mla_engine_update_weights(void* engine, const float* params) {
+    Engine* E = as_engine(engine);
+    if (!E || !params)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_engine_update_weights: invalid argument");
+    std::lock_guard lock(E->mu);
+    if (hipError_t e = hipStreamSynchronize(E->stream); e != hipSuccess)
+        return gpu_status(e, "mla_engine_update_weights");
+    ++E->host_waits;
+    uint64_t rev = 0;
+    if (int st = mla_model_update_weights(E->model, params, &rev))
+        return st;
+    // Every cached token was computed with the old weights: sessions must prefill again
+    // (CpuDecoder::decode's revision check, inference.cpp:71-75).
+    E->revision = rev;
+    return MLA_OK;
+}
+
+int mla_engine_stats(void* engine, uint64_t* stats) {
+    Engine* E = as_engine(engine);
+    if (!E || !stats)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_engine_stats: invalid argument");
+    std::lock_guard lock(E->mu);
+    stats[0] = E->steps;
+    stats[1] = E->host_waits;
+    stats[2] = E->meta_launches + model_launches(static_cast<Model*>(E->model));
+    stats[3] = E->copies;
+    stats[4] = E->revision;
+    return MLA_OK;
+}
+
+int mla_engine_forward(void* engine, int batch, int sequence, const uint16_t* ids,
+                       float* logits) {
+    Engine* E = as_engine(engine);
+    if (!E)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_engine_forward: invalid argument");
+    std::lock_guard lock(E->mu);
+    const mla_model_config& c = E->cfg;
+    if (!ids || !logits || batch < 1 || sequence < 1 || sequence > c.max_sequence_length ||
+        (long long)batch * sequence > (1LL << 31) / std::max(1, c.vocab_size))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "Forward requires a positive batch and sequence "
+                                              "within the context");
+    for (long long k = 0; k < (long long)batch * sequence; ++k)
+        if (ids[k] >= c.vocab_size)
+            return fail(MLA_ERR_INVALID_ARGUMENT, "mla_engine_forward: token exceeds vocabulary");
+    hipError_t e = hipSuccess;
+    if (!E->d_logits_all) {
+        e = E->dalloc(E->d_logits_all, (size_t)E->max_rows * c.vocab_size);
+        if (e == hipSuccess)
+            e = E->dalloc(E->d_next_all, (size_t)E->max_rows);
+        if (e == hipSuccess)
+            e = E->halloc(E->h_logits_all, (size_t)E->max_rows * c.vocab_size);
+        if (e != hipSuccess) {
+            E->d_logits_all = nullptr;
+            return gpu_status(e, "mla_engine_forward");
+        }
+    }
+    // Temporary sessions, one per sequence; a step takes whole rows of as many sequences
+    // as fit in max_rows (a longer sequence goes through in chunks of its own), so each
+    // chunk's rows attend to everything before them in their sequence (causality makes
+    // the chunks equal to one full pass, tests/test_model.cpp:65-77).
+    std::vector<int> temp;
+    auto release_all = [&]() {
+        for (int s : temp) {
+            release_pages(E, E->sessions[s]);
+            E->sessions[s].active = false;
+        }
+        temp.clear();
+    };
+    const int per_step = std::max(1, E->max_rows / sequence);
+    for (int b0 = 0; b0 < batch;) {
+        const int nb = std::min(per_step, batch - b0);
+        for (int s = 0; s < E->max_sessions && (int)temp.size() < nb; ++s)
+            if (!E->sessions[s].active) {
+                E->sessions[s] = Session{};
+                E->sessions[s].active = true;
+                temp.push_back(s);
+            }
+        if ((int)temp.size() < nb) {
+            release_all();
+            return fail(MLA_ERR_OUT_OF_MEMORY, "mla_engine_forward: no free session slots");
+        }
+        for (int off = 0; off < sequence;) {
+            const int cnt = std::min(sequence - off, E->max_rows);
+            std::vector<int> counts(nb, cnt);
+            std::vector<uint16_t> toks((size_t)nb * cnt);
+            for (int i = 0; i < nb; ++i)
+                std::memcpy(toks.data() + (size_t)i * cnt,
+                            ids + (size_t)(b0 + i) * sequence + off, (size_t)cnt * 2);
+            const int st = step(E, nb, temp.data(), counts.data(), toks.data(), E->h_logits_all,
+                                nullptr, "mla_engine_forward", true);
+            if (st && st != MLA_ERR_NUMERICAL) {
+                release_all();
+                return st;
+            }
+            for (int i = 0; i < nb; ++i)
+                std::memcpy(logits + ((size_t)(b0 + i) * sequence + off) * c.vocab_size,
+                            E->h_logits_all + (size_t)i * cnt * c.vocab_size,
+                            (size_t)cnt * c.vocab_size * sizeof(float));
+            if (st) {  // a non-finite logit: the rows are out, the error stands
+                release_all();
+                return st;
+            }
+            off += cnt;
+        }
+        release_all();
+        b0 += nb;
+    }
+    return MLA_OK;
 }
 
 }  // extern "C"

@@ -101,12 +101,16 @@ struct Model;  // model_capi.hip
 // the paged append, decode attention for q_len == 1 sessions and chunked-prefill
 // attention for the others, the FFN; then logits and the greedy token of each
 // session's LAST row into logits [B x vocab] / next_tokens [B].  When every session
-// has q_len == 1 (rows == B) the rows are the sessions.  Returns an MLA status.
+// has q_len == 1 (rows == B) the rows are the sessions.  all_rows: logits and greedy
+// token of EVERY row instead (logits [rows x vocab], next_tokens [rows]), as a full
+// forward returns them.  Returns an MLA status.
 int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
                   const int32_t* positions, int B, int max_q_len, const MetaPtrs& md,
                   void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
-                  int32_t* next_tokens);
+                  int32_t* next_tokens, bool all_rows = false);
 int model_max_rows(const Model* M);
+// Kernels model_forward has launched since the model was created.
+uint64_t model_launches(const Model* M);
 const mla_model_config& model_config(const Model* M);
 
 }  // namespace mla

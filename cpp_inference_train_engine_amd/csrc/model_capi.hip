@@ -127,6 +127,12 @@ struct Model {
     int32_t* arg_c;
     uint32_t* ban_bits = nullptr;  // [ceil(vocab/32)] banned token ids, allocated on first use
     bool banning = false;          // some id is banned: the greedy token skips them
+    uint64_t revision = 0;         // weight uploads after the first (mla_model_update_weights)
+    uint64_t launches = 0;         // kernels launched by model_forward
+    // Every weight buffer in upload order, so an update rewrites them in place.
+    std::vector<std::pair<void*, size_t>> weight_slots;
+    size_t slot_cursor = 0;
+    bool updating = false;
 
     ~Model() {
         for (void* p : allocations)
@@ -142,14 +148,24 @@ struct Model {
         out = static_cast<T*>(p);
         return hipMemset(p, 0, count * sizeof(T) + 16);
     }
+    // First upload: a new buffer.  During an update: the buffer this upload filled at
+    // creation (same order, same size).
     template <typename T>
     hipError_t upload(const T*& out, const std::vector<T>& host) {
+        const size_t bytes = host.size() * sizeof(T);
         T* p = nullptr;
-        hipError_t e = alloc(p, host.size());
-        if (e == hipSuccess)
-            e = hipMemcpy(p, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice);
+        if (updating) {
+            if (slot_cursor >= weight_slots.size() || weight_slots[slot_cursor].second != bytes)
+                return hipErrorInvalidValue;
+            p = static_cast<T*>(weight_slots[slot_cursor++].first);
+        } else {
+            const hipError_t e = alloc(p, host.size());
+            if (e != hipSuccess)
+                return e;
+            weight_slots.emplace_back(p, bytes);
+        }
         out = p;
-        return e;
+        return hipMemcpy(p, host.data(), bytes, hipMemcpyHostToDevice);
     }
 };
 
@@ -184,15 +200,112 @@ ModelDims make_dims(const mla_model_config& c, int page_size) {
     return m;
 }
 
+// Packs and uploads every weight of `params` (registry order) in one fixed order: at
+// creation into new buffers, during mla_model_update_weights into the same buffers.
+hipError_t upload_weights(Model* M, const float* params) {
+    const mla_model_config& c = M->cfg;
+    const ModelDims& m = M->dims;
+    const Registry R = view(c, params);
+    const int d = c.d_model, q = c.q_lora_rank, H = c.n_heads, nope = c.head_dim_nope;
+    const int qk = m.qk, kv = c.kv_lora_rank, kvw = kv + c.head_dim_rope, dv = c.head_dim_value;
+    const int ff = c.d_ff;
+    // Tied embedding as the logits weight: K = d_model, N = vocab.
+    hipError_t e = M->upload(M->embed, pack(d, c.vocab_size, m.d_pad, m.vocab_pad,
+                                 [&](int k, int col) { return R.embed[(size_t)col * d + k]; }));
+    if (e == hipSuccess)
+        e = M->upload(M->final_norm, std::vector<float>(R.final_norm, R.final_norm + d));
+    if (e == hipSuccess) {  // RoPE angles exactly as ops.cpp:88-108 forms them, per position
+        const int half = c.head_dim_rope / 2;
+        std::vector<float> tab((size_t)c.max_sequence_length * half * 2);
+        for (int pos = 0; pos < c.max_sequence_length; ++pos)
+            for (int j = 0; j < c.head_dim_rope; j += 2) {
+                const float angle =
+                    (float)pos * powf(c.rope_theta, -(float)j / (float)c.head_dim_rope);
+                tab[((size_t)pos * half + j / 2) * 2] = cosf(angle);
+                tab[((size_t)pos * half + j / 2) * 2 + 1] = sinf(angle);
+            }
+        e = M->upload(M->rope_tab, tab);
+    }
+    std::vector<float> proj((size_t)H * kv * d);
+    std::vector<LayerWeights> layers;
+    for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
+        const float* const* P = R.layer.data() + (size_t)l * P_COUNT;
+        LayerWeights w{};
+        e = M->upload(w.attn_norm, std::vector<float>(P[P_ATTN_NORM], P[P_ATTN_NORM] + d));
+        if (e == hipSuccess)
+            e = M->upload(w.q_norm, std::vector<float>(P[P_Q_NORM], P[P_Q_NORM] + q));
+        if (e == hipSuccess)
+            e = M->upload(w.kv_norm, std::vector<float>(P[P_KV_NORM], P[P_KV_NORM] + kv));
+        if (e == hipSuccess)
+            e = M->upload(w.ffn_norm, std::vector<float>(P[P_FFN_NORM], P[P_FFN_NORM] + d));
+        if (e == hipSuccess)  // [w_dq | w_dkv]: q columns padded to q_pad, then the kv columns
+            e = M->upload(w.w_dq_dkv,
+                          pack(d, m.q_pad + kvw, m.d_pad, m.q_pad + m.kvw_pad, [&](int k, int col) {
+                              if (col < q)
+                                  return P[P_W_DQ][(size_t)k * q + col];
+                              if (col < m.q_pad)
+                                  return 0.0f;
+                              return P[P_W_DKV][(size_t)k * kvw + (col - m.q_pad)];
+                          }));
+        if (e == hipSuccess)  // w_uq: head h at columns h*qk_pad ..
+            e = M->upload(w.w_uq, pack(q, H * m.qk_pad, m.q_pad, H * m.qk_pad, [&](int k, int col) {
+                              const int h = col / m.qk_pad, cc = col % m.qk_pad;
+                              return cc < qk ? P[P_W_UQ][(size_t)k * H * qk + h * qk + cc] : 0.0f;
+                          }));
+        if (e == hipSuccess) {  // W_uk_h^T per head: (k = nope index, col = latent index)
+            std::vector<uint16_t> all;
+            for (int h = 0; h < H; ++h) {
+                auto blk = pack(nope, kv, m.nope_pad, m.kv_pad, [&](int k, int col) {
+                    return P[P_W_UK][(size_t)col * H * nope + h * nope + k];
+                });
+                all.insert(all.end(), blk.begin(), blk.end());
+            }
+            e = M->upload(w.w_uk, all);
+        }
+        if (e == hipSuccess) {  // combined W_uv.W_o (CpuDecoder::prepare_projections, inference.cpp:28-46)
+            for (int h = 0; h < H; ++h)
+                for (int r = 0; r < kv; ++r) {
+                    float* row = proj.data() + ((size_t)h * kv + r) * d;
+                    std::memset(row, 0, (size_t)d * sizeof(float));
+                    for (int t = 0; t < dv; ++t) {
+                        const float a = P[P_W_UV][(size_t)r * H * dv + h * dv + t];
+                        const float* b = P[P_W_O] + (size_t)(h * dv + t) * d;
+                        for (int j = 0; j < d; ++j)
+                            row[j] += a * b[j];
+                    }
+                }
+            e = M->upload(w.w_out, pack(H * kv, d, m.ctx_pad, m.d_pad, [&](int k, int col) {
+                              return proj[(size_t)k * d + col];
+                          }));
+        }
+        if (e == hipSuccess)  // gate/up tiles interleaved: tile 2j gate, 2j+1 up, columns 16j..
+            e = M->upload(w.w_gate_up, pack(d, 2 * m.ff_pad, m.d_pad, 2 * m.ff_pad, [&](int k, int col) {
+                              const int t = col / 16, fcol = (t / 2) * 16 + col % 16;
+                              if (fcol >= ff)
+                                  return 0.0f;
+                              return (t % 2 ? P[P_W_UP] : P[P_W_GATE])[(size_t)k * ff + fcol];
+                          }));
+        if (e == hipSuccess)
+            e = M->upload(w.w_down, pack(ff, d, m.ff_pad, m.d_pad, [&](int k, int col) {
+                              return P[P_W_DOWN][(size_t)k * d + col];
+                          }));
+        layers.push_back(w);
+    }
+    if (e == hipSuccess)
+        M->layers = std::move(layers);
+    return e;
+}
+
 }  // namespace
 
 int model_max_rows(const Model* M) { return M->max_batch; }
+uint64_t model_launches(const Model* M) { return M->launches; }
 const mla_model_config& model_config(const Model* M) { return M->cfg; }
 
 int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
                   const int32_t* positions, int B, int max_q_len, const MetaPtrs& md,
                   void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
-                  int32_t* next_tokens) {
+                  int32_t* next_tokens, bool all_rows) {
     if (!M || rows < 0 || rows > M->max_batch || B < 0 || B > rows || max_q_len < 1 ||
         max_q_len > rows + (rows == 0) || md.max_work < 0 || md.max_work > kMaxWork ||
         md.max_pages < 0 || md.num_pool_pages < 0 || (rows == B) != (max_q_len == 1))
@@ -279,7 +392,9 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     pa.out = M->ctx;
     pa.lse = nullptr;
     const bool generic = (reinterpret_cast<uintptr_t>(workspace) & 15) != 0;
+    const int attn_launches = md.max_work > 0 && B > 0 ? 2 : 0;  // decode partials + merge
     hipError_t e = launch_embed(s, M->layers[0].attn_norm, st);
+    uint64_t launched = 1;
     for (int l = 0; l < m.n_layers && e == hipSuccess; ++l) {
         const float* next_norm = l + 1 < m.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
         uint16_t* pool = static_cast<uint16_t*>(pages[l]);
@@ -297,8 +412,9 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
             e = launch_prefill(pa, max_q_len, MLA_DTYPE_F16, false, st);
         if (e == hipSuccess)
             e = launch_layer_post(s, M->layers[l], next_norm, st);
+        launched += 1 + attn_launches + (max_q_len > 1) + 3;
     }
-    if (e == hipSuccess && rows != B) {  // logits of each session's last row only
+    if (e == hipSuccess && rows != B && !all_rows) {  // logits of each session's last row only
         StepArgs t = s;
         t.B = B;
         t.m_pad = round_up(B, 64);
@@ -307,9 +423,12 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
         e = launch_gather_last(s, B, md.cu_seqlens_q, t.xw, t.ss_x, st);  // from s.xw, s.ss_x
         if (e == hipSuccess)
             e = launch_logits(t, st);
-    } else if (e == hipSuccess) {
+        launched += 3;
+    } else if (e == hipSuccess) {  // every row's logits (rows == B, or all_rows)
         e = launch_logits(s, st);
+        launched += 2;
     }
+    M->launches += launched;
     return gpu_status(e, "model forward");
 }
 
@@ -355,10 +474,6 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
     M->max_batch = max_batch;
     M->m_pad_max = round_up(max_batch, 64);
     M->parts = g7_parts(m);
-    const Registry R = view(c, params);
-    const int d = c.d_model, q = c.q_lora_rank, H = c.n_heads, nope = c.head_dim_nope;
-    const int qk = m.qk, kv = c.kv_lora_rank, kvw = kv + c.head_dim_rope, dv = c.head_dim_value;
-    const int ff = c.d_ff;
     if (qkv_lds_bytes(m) > 150 * 1024) {  // the gfx950 workgroup LDS is 160 KB
         delete M;
         return fail(MLA_ERR_UNSUPPORTED, "mla_model_create: projection tiles exceed the LDS");
@@ -370,88 +485,9 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
     };
     if (e != hipSuccess)
         return bail(e);
-    // Tied embedding as the logits weight: K = d_model, N = vocab.
-    e = M->upload(M->embed, pack(d, c.vocab_size, m.d_pad, m.vocab_pad,
-                                 [&](int k, int col) { return R.embed[(size_t)col * d + k]; }));
-    if (e == hipSuccess)
-        e = M->upload(M->final_norm, std::vector<float>(R.final_norm, R.final_norm + d));
-    if (e == hipSuccess) {  // RoPE angles exactly as ops.cpp:88-108 forms them, per position
-        const int half = c.head_dim_rope / 2;
-        std::vector<float> tab((size_t)c.max_sequence_length * half * 2);
-        for (int pos = 0; pos < c.max_sequence_length; ++pos)
-            for (int j = 0; j < c.head_dim_rope; j += 2) {
-                const float angle =
-                    (float)pos * powf(c.rope_theta, -(float)j / (float)c.head_dim_rope);
-                tab[((size_t)pos * half + j / 2) * 2] = cosf(angle);
-                tab[((size_t)pos * half + j / 2) * 2 + 1] = sinf(angle);
-            }
-        e = M->upload(M->rope_tab, tab);
-    }
-    std::vector<float> proj((size_t)H * kv * d);
-    for (int l = 0; l < c.n_layers && e == hipSuccess; ++l) {
-        const float* const* P = R.layer.data() + (size_t)l * P_COUNT;
-        LayerWeights w{};
-        e = M->upload(w.attn_norm, std::vector<float>(P[P_ATTN_NORM], P[P_ATTN_NORM] + d));
-        if (e == hipSuccess)
-            e = M->upload(w.q_norm, std::vector<float>(P[P_Q_NORM], P[P_Q_NORM] + q));
-        if (e == hipSuccess)
-            e = M->upload(w.kv_norm, std::vector<float>(P[P_KV_NORM], P[P_KV_NORM] + kv));
-        if (e == hipSuccess)
-            e = M->upload(w.ffn_norm, std::vector<float>(P[P_FFN_NORM], P[P_FFN_NORM] + d));
-        if (e == hipSuccess)  // [w_dq | w_dkv]: q columns padded to q_pad, then the kv columns
-            e = M->upload(w.w_dq_dkv,
-                          pack(d, m.q_pad + kvw, m.d_pad, m.q_pad + m.kvw_pad, [&](int k, int col) {
-                              if (col < q)
-                                  return P[P_W_DQ][(size_t)k * q + col];
-                              if (col < m.q_pad)
-                                  return 0.0f;
-                              return P[P_W_DKV][(size_t)k * kvw + (col - m.q_pad)];
-                          }));
-        if (e == hipSuccess)  // w_uq: head h at columns h*qk_pad ..
-            e = M->upload(w.w_uq, pack(q, H * m.qk_pad, m.q_pad, H * m.qk_pad, [&](int k, int col) {
-                              const int h = col / m.qk_pad, cc = col % m.qk_pad;
-                              return cc < qk ? P[P_W_UQ][(size_t)k * H * qk + h * qk + cc] : 0.0f;
-                          }));
-        if (e == hipSuccess) {  // W_uk_h^T per head: (k = nope index, col = latent index)
-            std::vector<uint16_t> all;
-            for (int h = 0; h < H; ++h) {
-                auto blk = pack(nope, kv, m.nope_pad, m.kv_pad, [&](int k, int col) {
-                    return P[P_W_UK][(size_t)col * H * nope + h * nope + k];
-                });
-                all.insert(all.end(), blk.begin(), blk.end());
-            }
-            e = M->upload(w.w_uk, all);
-        }
-        if (e == hipSuccess) {  // combined W_uv.W_o (CpuDecoder::prepare_projections, inference.cpp:28-46)
-            for (int h = 0; h < H; ++h)
-                for (int r = 0; r < kv; ++r) {
-                    float* row = proj.data() + ((size_t)h * kv + r) * d;
-                    std::memset(row, 0, (size_t)d * sizeof(float));
-                    for (int t = 0; t < dv; ++t) {
-                        const float a = P[P_W_UV][(size_t)r * H * dv + h * dv + t];
-                        const float* b = P[P_W_O] + (size_t)(h * dv + t) * d;
-                        for (int j = 0; j < d; ++j)
-                            row[j] += a * b[j];
-                    }
-                }
-            e = M->upload(w.w_out, pack(H * kv, d, m.ctx_pad, m.d_pad, [&](int k, int col) {
-                              return proj[(size_t)k * d + col];
-                          }));
-        }
-        if (e == hipSuccess)  // gate/up tiles interleaved: tile 2j gate, 2j+1 up, columns 16j..
-            e = M->upload(w.w_gate_up, pack(d, 2 * m.ff_pad, m.d_pad, 2 * m.ff_pad, [&](int k, int col) {
-                              const int t = col / 16, fcol = (t / 2) * 16 + col % 16;
-                              if (fcol >= ff)
-                                  return 0.0f;
-                              return (t % 2 ? P[P_W_UP] : P[P_W_GATE])[(size_t)k * ff + fcol];
-                          }));
-        if (e == hipSuccess)
-            e = M->upload(w.w_down, pack(ff, d, m.ff_pad, m.d_pad, [&](int k, int col) {
-                              return P[P_W_DOWN][(size_t)k * d + col];
-                          }));
-        M->layers.push_back(w);
-    }
+    e = upload_weights(M, params);
     const size_t rows = M->m_pad_max;
+    const int H = c.n_heads, kv = c.kv_lora_rank;
     if (e == hipSuccess) e = M->alloc(M->x, rows * m.d_pad);
     if (e == hipSuccess) e = M->alloc(M->res, rows * m.d_pad);
     if (e == hipSuccess) e = M->alloc(M->xw, rows * m.d_pad);
@@ -475,6 +511,29 @@ int mla_model_create(const mla_model_config* config, const float* params, int ma
 
 int mla_model_destroy(void* model) {
     delete static_cast<Model*>(model);
+    return MLA_OK;
+}
+
+int mla_model_update_weights(void* model, const float* params, uint64_t* revision) {
+    Model* M = static_cast<Model*>(model);
+    if (!M || !params)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_update_weights: null argument");
+    // Device work that may still read the weights finishes first; the copies below are
+    // synchronous.
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) {
+        M->updating = true;
+        M->slot_cursor = 0;
+        e = upload_weights(M, params);
+        M->updating = false;
+    }
+    if (e == hipSuccess && M->slot_cursor != M->weight_slots.size())
+        e = hipErrorInvalidValue;
+    if (e != hipSuccess)
+        return gpu_status(e, "mla_model_update_weights");
+    ++M->revision;
+    if (revision)
+        *revision = M->revision;
     return MLA_OK;
 }
 

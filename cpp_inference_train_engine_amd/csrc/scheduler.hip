@@ -60,6 +60,8 @@ struct Request {
     std::string pending;  // text streamed during the current step
     int failed = MLA_OK;
     std::string failure;
+    // This step's timings, published into prefill_s / decode_s under Scheduler::mu.
+    double step_prefill_s = -1, step_decode_s = 0;
     double queue_s = 0, prefill_s = 0, decode_s = 0, first_s = 0;
     // Shared with pollers, under Scheduler::mu.
     std::string outbox;
@@ -157,6 +159,10 @@ struct Scheduler {
 
     std::mutex mu;
     std::condition_variable wake, progress;
+    // API calls in progress on other threads (under mu); destroy waits for none.
+    int calls = 0;
+    std::condition_variable idle;
+    std::mutex join_mu;  // one thread joins the stepping thread
     std::deque<RequestPtr> queue;
     std::vector<RequestPtr> running;
     std::unordered_map<uint64_t, RequestPtr> live;  // submitted and not yet retired by poll
@@ -363,9 +369,9 @@ void Scheduler::run() {
             if (w.prompt) {
                 r->fed += w.count;
                 if (w.last)
-                    r->prefill_s = seconds(r->started, t1);
+                    r->step_prefill_s = seconds(r->started, t1);
             } else {
-                r->decode_s += seconds(t0, t1);
+                r->step_decode_s += seconds(t0, t1);
             }
             if (w.last)
                 picks.push_back(i);
@@ -399,11 +405,19 @@ void Scheduler::run() {
 
         lk.lock();
         ++steps;
-        for (const Row& w : rows)
-            if (!w.r->pending.empty()) {
-                w.r->outbox += w.r->pending;
-                w.r->pending.clear();
+        for (const Row& w : rows) {
+            Request* r = w.r;
+            if (!r->pending.empty()) {
+                r->outbox += r->pending;
+                r->pending.clear();
             }
+            if (r->step_prefill_s >= 0) {
+                r->prefill_s = r->step_prefill_s;
+                r->step_prefill_s = -1;
+            }
+            r->decode_s += r->step_decode_s;
+            r->step_decode_s = 0;
+        }
         for (size_t k = 0; k < running.size();) {
             const RequestPtr& r = running[k];
             if (r->failed || r->gen.finished()) {
@@ -431,6 +445,33 @@ void Scheduler::run() {
 }
 
 Scheduler* as_scheduler(void* p) { return static_cast<Scheduler*>(p); }
+
+// Counts an API call in progress.  Constructed and destroyed under S.mu (declare it after
+// the lock), so destroy can wait until no other thread is inside the scheduler.
+struct InCall {
+    Scheduler& S;
+    explicit InCall(Scheduler& s) : S(s) { ++S.calls; }
+    ~InCall() {
+        if (--S.calls == 0 && S.stopping)
+            S.idle.notify_all();
+    }
+    InCall(const InCall&) = delete;
+    InCall& operator=(const InCall&) = delete;
+};
+
+// Ends the stepping thread: what is queued never starts, what runs ends as cancelled.
+void stop(Scheduler* S) {
+    {
+        std::lock_guard<std::mutex> lk(S->mu);
+        S->stopping = true;
+        S->stop_flag = true;
+    }
+    S->wake.notify_all();
+    S->progress.notify_all();  // pollers waiting for text wake up
+    std::lock_guard<std::mutex> j(S->join_mu);
+    if (S->thread.joinable())
+        S->thread.join();
+}
 
 }  // namespace
 }  // namespace mla
@@ -491,18 +532,25 @@ int mla_scheduler_create(void* engine, void* tokenizer, const mla_scheduler_conf
     return MLA_OK;
 }
 
+int mla_scheduler_stop(void* scheduler) {
+    Scheduler* S = as_scheduler(scheduler);
+    if (!S)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_scheduler_stop: null scheduler");
+    stop(S);
+    return MLA_OK;
+}
+
 int mla_scheduler_destroy(void* scheduler) {
     Scheduler* S = as_scheduler(scheduler);
     if (!S)
         return MLA_OK;
+    stop(S);
     {
-        std::lock_guard<std::mutex> lk(S->mu);
-        S->stopping = true;
-        S->stop_flag = true;
+        // Calls already inside the scheduler on other threads (a poll that was waiting
+        // has been woken by stop) return before the memory goes.
+        std::unique_lock<std::mutex> lk(S->mu);
+        S->idle.wait(lk, [&] { return S->calls == 0; });
     }
-    S->wake.notify_all();
-    if (S->thread.joinable())
-        S->thread.join();
     delete S;
     return MLA_OK;
 }
@@ -517,6 +565,7 @@ int mla_scheduler_submit(void* scheduler, const uint16_t* prompt, size_t n,
         if (const int st = gen_config_from_c(config, c))
             return st;
     std::lock_guard<std::mutex> lk(S->mu);
+    const InCall in(*S);
     if (S->stopping)
         return fail(MLA_ERR_UNAVAILABLE, "Scheduler is stopping");
     if (S->queue.size() >= (size_t)S->cfg.max_queue) {  // server.cpp:213-219
@@ -566,6 +615,7 @@ int mla_scheduler_cancel(void* scheduler, uint64_t request) {
     if (!S)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_scheduler_cancel: null scheduler");
     std::lock_guard<std::mutex> lk(S->mu);
+    const InCall in(*S);
     auto it = S->live.find(request);
     if (it == S->live.end())
         return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown request");
@@ -581,13 +631,18 @@ int mla_scheduler_poll(void* scheduler, uint64_t request, int timeout_ms, char* 
     if (!S || !text_len || !status || (!text && text_capacity))
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_scheduler_poll: null argument");
     std::unique_lock<std::mutex> lk(S->mu);
+    const InCall in(*S);
     auto it = S->live.find(request);
     if (it == S->live.end())
         return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown request");
     const RequestPtr r = it->second;
     if (timeout_ms > 0)
         S->progress.wait_for(lk, std::chrono::milliseconds(timeout_ms),
-                             [&] { return r->done || !r->outbox.empty(); });
+                             [&] { return r->done || !r->outbox.empty() || S->stopping; });
+    // The request may have been retired by another poll while this one waited.
+    it = S->live.find(request);
+    if (it == S->live.end())
+        return fail(MLA_ERR_INVALID_ARGUMENT, "Unknown request");
     const size_t take = std::min(text_capacity, r->outbox.size());
     if (take)
         std::memcpy(text, r->outbox.data(), take);
@@ -620,6 +675,7 @@ int mla_scheduler_metrics_get(void* scheduler, mla_scheduler_metrics* m) {
     if (!S || !m)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_scheduler_metrics_get: null argument");
     std::lock_guard<std::mutex> lk(S->mu);
+    const InCall in(*S);
     m->requests = S->requests;
     m->completed = S->completed;
     m->rejected = S->rejected;

@@ -90,6 +90,33 @@ class HipEngine:
         ids = np.ascontiguousarray(ids, dtype=np.uint16).ravel()
         check(lib().mla_engine_set_banned(self.handle, ids.ctypes.data, ids.size))
 
+    def update_weights(self, params) -> None:
+        """mla_engine_update_weights: replace the weights (Model::mark_weights_changed);
+        sessions with cached tokens must prefill again before they decode."""
+        params = np.ascontiguousarray(params, dtype=np.float32)
+        if params.size != config_parameter_count(self.cfg):
+            raise ValueError(f"expected {config_parameter_count(self.cfg)} parameters, "
+                             f"got {params.size}")
+        check(lib().mla_engine_update_weights(self.handle, params.ctypes.data))
+
+    def stats(self) -> dict:
+        """mla_engine_stats: Execution::stats's counters (execution.hpp:25-27), engine-wide."""
+        v = (C.c_uint64 * 5)()
+        check(lib().mla_engine_stats(self.handle, v))
+        keys = ("graph_submissions", "host_waits", "kernel_submissions", "copies", "revision")
+        return dict(zip(keys, [int(x) for x in v]))
+
+    def forward(self, ids, batch: int, sequence: int) -> np.ndarray:
+        """mla_engine_forward: Execution::forward(ids, batch, sequence) (execution.hpp:
+        38-39), the logits of every position, [batch * sequence, vocab]."""
+        ids = np.ascontiguousarray(np.asarray(ids, np.uint16).ravel())
+        if ids.size != batch * sequence:
+            raise ValueError("ids must hold batch * sequence tokens")
+        out = np.empty((batch * sequence, self.cfg.vocab_size), np.float32)
+        check(lib().mla_engine_forward(self.handle, int(batch), int(sequence), ids.ctypes.data,
+                                       out.ctypes.data))
+        return out
+
     def step(self, sessions, token_lists, want_logits: bool = True):
         """One batched forward: ``sessions[i]`` appends ``token_lists[i]`` (one token =
         decode, several = chunked prefill).  Returns (logits [n, vocab] or None,
@@ -120,6 +147,14 @@ class HipExecution:
 
     def attention_name(self) -> str:
         return "paged-mla"
+
+    def stats(self) -> dict:
+        """Execution::stats: the engine's counters (its sessions share one stream)."""
+        return self.engine.stats()
+
+    def forward(self, ids, batch: int, sequence: int) -> np.ndarray:
+        """Execution::forward: every position's logits, [batch * sequence, vocab]."""
+        return self.engine.forward(ids, batch, sequence)
 
     def fork_inference(self) -> "HipExecution":
         """A new empty session on the same weights (execution.hpp:34-37)."""

@@ -62,7 +62,15 @@ class HipExecution final : public Execution {
     ~HipExecution() override { (void)mla_session_release(engine_->handle(), session_); }
     std::string device_name() const override { return "HIP / MI355X (gfx950)"; }
     std::string attention_name() const override { return "paged-mla"; }
+    ExecutionStats stats() const override { return engine_->stats(); }
     Result<std::unique_ptr<Execution>> fork_inference() override { return engine_->session(); }
+    Result<const Matrix*> forward(std::span<const std::uint16_t> ids, int batch,
+                                  int sequence) override {
+        const Status s = engine_->forward(ids, batch, sequence, output_);
+        if (!s)
+            return fail_as<const Matrix*>(s);
+        return Result<const Matrix*>::success(&output_);
+    }
     Result<std::span<const float>> prefill(std::span<const std::uint16_t> ids) override {
         const Status s = check(mla_session_prefill(engine_->handle(), session_, ids.data(),
                                                    (int)std::min<size_t>(ids.size(), 1u << 30),
@@ -84,6 +92,7 @@ class HipExecution final : public Execution {
     std::shared_ptr<HipEngine> engine_;
     int session_;
     std::vector<float> logits_;
+    Matrix output_;  // forward's logits, valid until the next forward
 };
 
 int text_callback(void* user, const char* text, size_t len) {
@@ -142,6 +151,30 @@ Status HipEngine::set_banned(std::span<const std::uint16_t> ids) {
     return check(mla_engine_set_banned(h_, ids.data(), ids.size()));
 }
 
+Status HipEngine::update_weights(std::span<const float> params) {
+    if (params.size() != mla_config_parameter_count(&config_))
+        return Status::failure(ErrorCode::invalid_argument, "Parameter count does not match the model");
+    return check(mla_engine_update_weights(h_, params.data()));
+}
+
+ExecutionStats HipEngine::stats() const {
+    std::uint64_t v[5] = {};
+    if (mla_engine_stats(h_, v) != MLA_OK)
+        return {};
+    return ExecutionStats{v[0], v[1], v[2]};
+}
+
+Status HipEngine::forward(std::span<const std::uint16_t> ids, int batch, int sequence,
+                          Matrix& out) {
+    if (batch < 1 || sequence < 1 || ids.size() != (std::size_t)batch * (std::size_t)sequence)
+        return Status::failure(ErrorCode::invalid_argument,
+                               "Forward requires batch * sequence token ids");
+    out.rows = batch * sequence;
+    out.cols = config_.vocab_size;
+    out.values.resize((std::size_t)out.rows * (std::size_t)out.cols);
+    return check(mla_engine_forward(h_, batch, sequence, ids.data(), out.values.data()));
+}
+
 Status HipEngine::step(std::span<Execution* const> sessions,
                        std::span<const std::vector<std::uint16_t>> tokens,
                        std::vector<float>* logits, std::vector<std::int32_t>* next_tokens) {
@@ -173,6 +206,18 @@ Result<std::unique_ptr<Execution>> make_hip_execution(const std::shared_ptr<HipE
         return Result<std::unique_ptr<Execution>>::failure(ErrorCode::invalid_argument,
                                                            "make_hip_execution: null engine");
     return engine->session();
+}
+
+Result<std::unique_ptr<Execution>> make_execution(const std::shared_ptr<HipEngine>& engine,
+                                                  std::string_view backend,
+                                                  std::string_view precision) {
+    if (backend != "hip")  // an unknown backend is unsupported, as in inference.cpp:320-322
+        return Result<std::unique_ptr<Execution>>::failure(ErrorCode::unsupported,
+                                                           "Select hip/fp32|fp16");
+    if (precision != "fp32" && precision != "fp16")
+        return Result<std::unique_ptr<Execution>>::failure(ErrorCode::unsupported,
+                                                           "HIP precision must be fp32 or fp16");
+    return make_hip_execution(engine);
 }
 
 // --------------------------------------------------------------- tokenizer ----

@@ -81,15 +81,39 @@ struct EngineLimits {
 
 class HipEngine;
 
+// ExecutionStats (execution.hpp:25-27), with the reference's field names.  On HIP:
+// model forwards submitted to the engine's stream, host waits on that stream, and
+// kernels launched (metal_kernel_submissions counts HIP kernel launches).
+struct ExecutionStats {
+    std::uint64_t graph_submissions = 0, host_waits = 0, metal_kernel_submissions = 0;
+};
+
+// The logits Execution::forward returns: rows x cols, row-major, read as m(r, c) like the
+// reference's Matrix.
+struct Matrix {
+    int rows = 0, cols = 0;
+    std::vector<float> values;
+    [[nodiscard]] float operator()(int r, int c) const { return values[(std::size_t)r * cols + c]; }
+    float& operator()(int r, int c) { return values[(std::size_t)r * cols + c]; }
+    [[nodiscard]] const float* data() const { return values.data(); }
+};
+
 // The inference part of mini_mla::Execution (execution.hpp:28-62).
 class Execution {
   public:
     virtual ~Execution() = default;
     [[nodiscard]] virtual std::string device_name() const = 0;
     [[nodiscard]] virtual std::string attention_name() const { return "reference"; }
+    [[nodiscard]] virtual ExecutionStats stats() const { return {}; }
     [[nodiscard]] virtual Result<std::unique_ptr<Execution>> fork_inference() {
         return Result<std::unique_ptr<Execution>>::failure(
             ErrorCode::unsupported, "Execution cannot fork inference sessions");
+    }
+    // Logits of every position of `batch` sequences of `sequence` ids (row-major); the
+    // matrix stays valid until the execution's next forward.
+    [[nodiscard]] virtual Result<const Matrix*> forward(std::span<const std::uint16_t>, int, int) {
+        return Result<const Matrix*>::failure(ErrorCode::unsupported,
+                                              "Execution has no forward pass");
     }
     [[nodiscard]] virtual Result<std::span<const float>> prefill(std::span<const std::uint16_t>) = 0;
     [[nodiscard]] virtual Result<std::span<const float>> decode(std::uint16_t) = 0;
@@ -111,6 +135,13 @@ class HipEngine : public std::enable_shared_from_this<HipEngine> {
     Result<std::unique_ptr<Execution>> session();
     // The ids the greedy token of batched steps skips (sample_token's banned list).
     Status set_banned(std::span<const std::uint16_t> ids);
+    // New weights (registry order), as Model::mark_weights_changed: sessions holding
+    // cached tokens must prefill again before they decode (inference.cpp:71-75).
+    Status update_weights(std::span<const float> params);
+    // Counters since creation, shared by every session of the engine.
+    [[nodiscard]] ExecutionStats stats() const;
+    // Every position's logits of `batch` sequences of `sequence` ids (mla_engine_forward).
+    Status forward(std::span<const std::uint16_t> ids, int batch, int sequence, Matrix& out);
     // One batched forward (continuous batching): sessions[i], a session of this engine,
     // appends tokens[i] (one token: a decode; several: a prompt chunk).  logits (may be
     // null) receives [n x vocab] of each session's last new token, next_tokens (may be
@@ -127,6 +158,14 @@ class HipEngine : public std::enable_shared_from_this<HipEngine> {
 
 // make_execution(model, nullptr, "hip") for an engine: a new session on it.
 Result<std::unique_ptr<Execution>> make_hip_execution(const std::shared_ptr<HipEngine>&);
+// make_execution(model, nullptr, backend, precision) (execution.hpp:63-66): backend "hip";
+// precision "fp32" (the reference's default) or "fp16".  Both keep fp16 weights and cache
+// with fp32 accumulation, so an "fp32" execution matches the CPU path to the fp16
+// tolerance of test_mps.cpp:140 (0.015), not to fp32's 1e-4.  Anything else is
+// unsupported, with the reference's message for an unknown backend.
+Result<std::unique_ptr<Execution>> make_execution(const std::shared_ptr<HipEngine>&,
+                                                  std::string_view backend,
+                                                  std::string_view precision = "fp32");
 
 // mini_mla::Tokenizer (src/infer/tokenizer.cpp) over mla_tokenizer_*.
 class Tokenizer {

@@ -102,6 +102,17 @@ class HipModel:
         self._h = h
         return self
 
+    def update_weights(self, params) -> int:
+        """mla_model_update_weights: new weights in place (Model::mark_weights_changed);
+        returns the revision count.  No step may be in flight."""
+        import numpy as np
+        params = np.ascontiguousarray(params, dtype=np.float32)
+        if params.size != config_parameter_count(self.cfg):
+            raise ValueError(f"expected {config_parameter_count(self.cfg)} parameters, got {params.size}")
+        rev = C.c_uint64()
+        check(lib().mla_model_update_weights(self._h, params.ctypes.data, C.byref(rev)))
+        return rev.value
+
     def close(self):
         if getattr(self, "_h", None):
             lib().mla_model_destroy(self._h)

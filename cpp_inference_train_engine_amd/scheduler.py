@@ -9,7 +9,9 @@ request limits and metrics.  The HTTP layer is the caller's.
 from __future__ import annotations
 
 import codecs
+import contextlib
 import ctypes as C
+import threading
 import time
 
 import numpy as np
@@ -47,15 +49,46 @@ class Scheduler:
                  max_queue: int = 16, request_timeout_seconds: int = 60):
         c = _SchedulerConfig(max_context, max_new_tokens, max_queue, request_timeout_seconds)
         h = C.c_void_p()
+        # Calls in progress on other threads, so close() never frees the scheduler under
+        # one of them (a server's handler threads poll while it shuts down).
+        self._cv = threading.Condition()
+        self._active, self._closing = 0, False
         check(lib().mla_scheduler_create(engine.handle, tokenizer._h, C.byref(c), C.byref(h)))
         self._h, self.engine, self.tokenizer = h, engine, tokenizer
         self.max_new_tokens = max_new_tokens
         engine._attach(self)  # closing the engine stops this scheduler first
 
+    @contextlib.contextmanager
+    def _use(self):
+        with self._cv:
+            if not getattr(self, "_h", None) or self._closing:
+                raise MlaError(7, "Scheduler is closed")
+            self._active += 1
+            h = self._h
+        try:
+            yield h
+        finally:
+            with self._cv:
+                self._active -= 1
+                self._cv.notify_all()
+
     def close(self):
-        if getattr(self, "_h", None):
-            lib().mla_scheduler_destroy(self._h)
+        """Stops the scheduler (queued requests never start, running ones end as
+        cancelled, waiting polls return), waits for calls in progress on other threads,
+        then frees it."""
+        cv = getattr(self, "_cv", None)
+        if cv is None:
+            return
+        with cv:
+            h = getattr(self, "_h", None)
+            if not h or self._closing:
+                return
+            self._closing = True
+        lib().mla_scheduler_stop(h)
+        with cv:
+            cv.wait_for(lambda: self._active == 0)
             self._h = None
+        lib().mla_scheduler_destroy(h)
 
     def __del__(self):
         self.close()
@@ -73,8 +106,9 @@ class Scheduler:
         ids = np.ascontiguousarray(prompt_ids, dtype=np.uint16).ravel()
         c, keep = c_config(config, max_new_tokens_default=not max_tokens_given)
         rid = C.c_uint64()
-        check(lib().mla_scheduler_submit(self._h, ids.ctypes.data, ids.size, C.byref(c),
-                                         int(stream), C.byref(rid)))
+        with self._use() as h:
+            check(lib().mla_scheduler_submit(h, ids.ctypes.data, ids.size, C.byref(c),
+                                             int(stream), C.byref(rid)))
         del keep
         return rid.value
 
@@ -85,7 +119,8 @@ class Scheduler:
         return self.submit(ids, config, stream, max_tokens_given)
 
     def cancel(self, rid: int) -> None:
-        check(lib().mla_scheduler_cancel(self._h, rid))
+        with self._use() as h:
+            check(lib().mla_scheduler_cancel(h, rid))
 
     def poll(self, rid: int, timeout: float = 0.0):
         """(new text bytes, status dict); status["done"] once the request has ended (it is
@@ -94,8 +129,10 @@ class Scheduler:
         n = C.c_size_t()
         tokens = np.empty(65536, np.uint16)
         st = _Status()
-        check(lib().mla_scheduler_poll(self._h, rid, int(timeout * 1000), buf, len(buf),
-                                       C.byref(n), tokens.ctypes.data, tokens.size, C.byref(st)))
+        with self._use() as h:
+            check(lib().mla_scheduler_poll(h, rid, int(timeout * 1000), buf, len(buf),
+                                           C.byref(n), tokens.ctypes.data, tokens.size,
+                                           C.byref(st)))
         status = {k: getattr(st, k) for k, _ in _Status._fields_}
         status["error_message"] = st.error_message.decode(errors="replace")
         status["finish_reason"] = st.finish_reason.decode()
@@ -134,14 +171,16 @@ class Scheduler:
 
     def metrics(self) -> dict:
         m = _Metrics()
-        check(lib().mla_scheduler_metrics_get(self._h, C.byref(m)))
+        with self._use() as h:
+            check(lib().mla_scheduler_metrics_get(h, C.byref(m)))
         return {k: getattr(m, k) for k, _ in _Metrics._fields_}
 
     def metrics_text(self) -> str:
         n = C.c_size_t()
-        check(lib().mla_scheduler_metrics_text(self._h, None, 0, C.byref(n)))
-        buf = C.create_string_buffer(n.value + 1)
-        check(lib().mla_scheduler_metrics_text(self._h, buf, len(buf), C.byref(n)))
+        with self._use() as h:
+            check(lib().mla_scheduler_metrics_text(h, None, 0, C.byref(n)))
+            buf = C.create_string_buffer(n.value + 1)
+            check(lib().mla_scheduler_metrics_text(h, buf, len(buf), C.byref(n)))
         return buf.raw[:n.value].decode()
 
 

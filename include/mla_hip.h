@@ -181,6 +181,7 @@ int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_
                      int max_work, float* out, float* lse, const void* workspace,
                      size_t workspace_bytes);
 
+
 /* ------------------------------------------------------------------ (c)
  * Absorbed MLA chunked-prefill attention over the paged cache, for every session
  * with q_len > 1 in the batch.  Session b appended q_len tokens at positions
@@ -240,6 +241,14 @@ size_t mla_config_parameter_count(const mla_model_config* config);
 int mla_model_create(const mla_model_config* config, const float* params, int max_batch,
                      int page_size, void** model);
 int mla_model_destroy(void* model);
+/* Model::mark_weights_changed (include/mini_mla/model.hpp) for an uploaded model: the
+ * weights are replaced in place by `params` (same configuration, registry order; rounded
+ * to fp16 and W_uv.W_o recombined, as at creation -- CpuDecoder::prepare_projections
+ * recomputes per revision, inference.cpp:28-46).  Waits for the device first; not
+ * stream-ordered, so no step may run concurrently.  *revision (may be NULL) receives the
+ * new revision count (0 at creation).  On a failed copy the weights are undefined until
+ * an update succeeds. */
+int mla_model_update_weights(void* model, const float* params, uint64_t* revision);
 
 /* One decode step for B sessions (B <= max_batch): tokens[b] (device int32, in
  * [0, vocab)) at position positions[b] (device int32: the tokens already cached,
@@ -307,8 +316,10 @@ const float* mla_model_logits(void* model);
  * inference.cpp:67).  Calls on one engine are serialised by an internal mutex, so
  * sessions may be driven from different threads (the reference's fork-per-thread
  * use, tests/inference_sessions.hpp:191-217); concurrent sessions are served best
- * through mla_engine_step.  Weights are immutable after creation, so the reference's
- * stale-weight error (inference.cpp:72) cannot arise. */
+ * through mla_engine_step.  The weights can be replaced (mla_engine_update_weights): a
+ * session whose cache predates the replacement is refused, as the reference's decode is
+ * after mark_weights_changed (inference.cpp:71-75; mps_backend.mm:943-944), until it is
+ * prefilled again. */
 
 /* An engine for up to max_sessions sessions: model upload as mla_model_create,
  * num_pages pages of page_size tokens per layer (fp16, the mla_append_latent format),
@@ -356,6 +367,29 @@ int mla_engine_step(void* engine, int n, const int* sessions, const int* counts,
 /* mla_model_set_banned for the engine's model: the ids next_tokens of mla_engine_step
  * skip (MLA_ERR_INVALID_ARGUMENT "All tokens are banned" when none is left). */
 int mla_engine_set_banned(void* engine, const uint16_t* ids, size_t n);
+/* New weights for the engine's model (mla_model_update_weights) after the engine's stream
+ * has drained.  From then on every session holding cached tokens is stale: its decode and
+ * its rows in mla_engine_step fail with MLA_ERR_INVALID_ARGUMENT "Decode requires
+ * current-weight prefill, available context, and a valid token" (CpuDecoder::decode,
+ * inference.cpp:71-75; tests/test_training.cpp:111-122) until mla_session_prefill
+ * restarts it.  Empty sessions and new prompts are unaffected. */
+int mla_engine_update_weights(void* engine, const float* params);
+/* Execution::stats (include/mini_mla/execution.hpp:25-27,33), engine-wide counters since
+ * creation: stats[5] = {model forwards submitted (graph_submissions), host waits on the
+ * engine's stream (host_waits), kernels launched (metal_kernel_submissions), copies
+ * issued, weight revision}. */
+int mla_engine_stats(void* engine, uint64_t* stats);
+/* Execution::forward(ids, batch, sequence) (execution.hpp:38-39) for inference: the
+ * logits of EVERY position of `batch` independent sequences of `sequence` tokens (ids
+ * row-major [batch x sequence]), as Model::forward returns them (src/model/model.cpp:
+ * 76-155): logits (host) [batch*sequence x vocab].  Runs through temporary sessions of
+ * the engine (whole sequences batched up to max_rows rows per step, longer ones in
+ * causal chunks), which are released afterwards; needs their cache pages and free session
+ * slots (else MLA_ERR_OUT_OF_MEMORY).  MLA_ERR_INVALID_ARGUMENT for an empty batch, a
+ * sequence beyond max_sequence_length or a token past the vocabulary; MLA_ERR_NUMERICAL
+ * when a logit is not finite. */
+int mla_engine_forward(void* engine, int batch, int sequence, const uint16_t* ids,
+                       float* logits);
 
 /* ------------------------------------------------------------ model exports
  * The reference's inference-side weight load, load_checkpoint(path, training =
@@ -511,7 +545,14 @@ void mla_scheduler_config_init(mla_scheduler_config* config);
  * (mla_engine_set_banned).  Engine and tokenizer must outlive the scheduler. */
 int mla_scheduler_create(void* engine, void* tokenizer, const mla_scheduler_config* config,
                          void** scheduler);
-/* Cancels what is queued or running and joins the thread. */
+/* Cancels what is queued or running and joins the stepping thread; idempotent.  Polls
+ * waiting on other threads wake up; later polls still hand out the (cancelled) results,
+ * later submits fail with MLA_ERR_UNAVAILABLE "Scheduler is stopping". */
+int mla_scheduler_stop(void* scheduler);
+/* mla_scheduler_stop, then waits until every call already inside the scheduler on other
+ * threads has returned, then frees it.  Calls that START after destroy are the caller's
+ * error (the handle is gone): a host shares the handle with a reference count or a lock,
+ * as the Python binding does. */
 int mla_scheduler_destroy(void* scheduler);
 /* Queues a generation of prompt (token ids, <|bos|> included).  config NULL or
  * max_new_tokens < 0: the server default min(max_new_tokens, max_context - n)

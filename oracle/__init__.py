@@ -81,6 +81,7 @@ def _declare(L):
         "orc_output_projection": (None, [vp, vp, vp]),
         "orc_decode": (i, [vp, vp, vp, vp, vp, i, C.c_uint16, i, i, vp]),
         "orc_set_threads": (None, [i]),
+        "orc_set_blas": (None, [vp, vp]),
         "orc_attention_paged": (i, [i, i, i, i, i, i, vp, vp, vp, i, vp, vp, vp, f, vp, vp]),
         "orc_build_metadata": (i, [i, vp, vp, vp, vp, i, i, i, i, i, i, i,
                                    vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
@@ -225,6 +226,37 @@ class Decoder:
             raise ValueError(f"decode failed ({st})")
         self.position += 1
         return logits
+
+
+# -------------------------------------------------------------- CBLAS ----
+_blas = None
+
+
+def use_blas(enable: bool = True):
+    """Route orc_forward / orc_decode's products through the CBLAS numpy ships (OpenBLAS,
+    64-bit indices) in place of the plain loops -- the portable stand-in for the
+    reference's Accelerate cblas calls, used to time the CPU baseline.  The library runs
+    single-threaded per call (one session per thread, as the reference's forks decode).
+    Returns a description of the library, or None when disabled or not found."""
+    global _blas
+    import glob
+    if not enable:
+        lib().orc_set_blas(None, None)
+        return None
+    if _blas is None:
+        libs = sorted(glob.glob(os.path.join(os.path.dirname(np.__file__) + ".libs",
+                                             "libscipy_openblas64_*.so")))
+        if not libs:
+            return None
+        B = C.CDLL(libs[0])
+        B.scipy_openblas_set_num_threads64_.argtypes = [C.c_int]
+        B.scipy_openblas_set_num_threads64_(1)
+        B.scipy_openblas_get_config64_.restype = C.c_char_p
+        _blas = (B, B.scipy_openblas_get_config64_().decode())
+    B, desc = _blas
+    lib().orc_set_blas(C.cast(B.scipy_cblas_sgemm64_, C.c_void_p),
+                       C.cast(B.scipy_cblas_sgemv64_, C.c_void_p))
+    return desc
 
 
 # --------------------------------------------------- paged attention ----

@@ -237,8 +237,34 @@ int orc_model_init(const orc_config* c, uint64_t seed, float* params) { /* model
 /* ------------------------------------------------------------------------ */
 /* ops (src/model/ops.cpp)                                                   */
 /* ------------------------------------------------------------------------ */
+/* Optional CBLAS for the CPU-baseline timing.  The reference's products are Accelerate
+   cblas_sgemm / cblas_sgemv calls (ops.cpp:15-17,119-122,138-140; inference.cpp:38-43,
+   107-113,122-132,146-152).  Accelerate does not exist on Linux, so orc_set_blas can hand
+   in a portable CBLAS with 64-bit indices (the OpenBLAS numpy ships); with none set, the
+   plain loops below run.  The parity tests use the loops; a BLAS only reorders sums. */
+typedef void (*orc_sgemm_fn)(int, int, int, int64_t, int64_t, int64_t, float, const float*,
+                             int64_t, const float*, int64_t, float, float*, int64_t);
+typedef void (*orc_sgemv_fn)(int, int, int64_t, int64_t, float, const float*, int64_t,
+                             const float*, int64_t, float, float*, int64_t);
+static orc_sgemm_fn g_sgemm = NULL;
+static orc_sgemv_fn g_sgemv = NULL;
+enum { CB_ROW_MAJOR = 101, CB_NO_TRANS = 111, CB_TRANS = 112 }; /* CBLAS enum values */
+
+void orc_set_blas(void* sgemm, void* sgemv) {
+    g_sgemm = (orc_sgemm_fn)sgemm;
+    g_sgemv = (orc_sgemv_fn)sgemv;
+}
+
 /* out[m x n] = a[m x k] . b[k x n]   (ops.cpp:8-18; sequential k sums) */
 static void matmul(const float* a, const float* b, float* out, int m, int k, int n) {
+    if (g_sgemv && g_sgemm) {
+        if (m == 1)
+            g_sgemv(CB_ROW_MAJOR, CB_TRANS, k, n, 1.0F, b, n, a, 1, 0.0F, out, 1);
+        else
+            g_sgemm(CB_ROW_MAJOR, CB_NO_TRANS, CB_NO_TRANS, m, n, k, 1.0F, a, k, b, n, 0.0F, out,
+                    n);
+        return;
+    }
     for (int i = 0; i < m; ++i) {
         float* o = out + (size_t)i * n;
         for (int j = 0; j < n; ++j)
@@ -253,6 +279,13 @@ static void matmul(const float* a, const float* b, float* out, int m, int k, int
 }
 /* out[m x n] = a[m x k] . b[n x k]^T  (tied logits, ops.cpp matmul with tb) */
 static void matmul_bt(const float* a, const float* b, float* out, int m, int k, int n) {
+    if (g_sgemv && g_sgemm) {
+        if (m == 1)
+            g_sgemv(CB_ROW_MAJOR, CB_NO_TRANS, n, k, 1.0F, b, k, a, 1, 0.0F, out, 1);
+        else
+            g_sgemm(CB_ROW_MAJOR, CB_NO_TRANS, CB_TRANS, m, n, k, 1.0F, a, k, b, k, 0.0F, out, n);
+        return;
+    }
     for (int i = 0; i < m; ++i)
         for (int j = 0; j < n; ++j) {
             float s = 0.0F;
@@ -496,7 +529,13 @@ int orc_decode(const orc_config* c, const float* params, const float* out_proj, 
         const float* uk = W(&v, l, P_W_UK);
         for (int hh = 0; hh < H; ++hh) { /* inference.cpp:116-153 */
             const float* qh = qv + hh * qk;
-            if (absorbed) {
+            if (absorbed && g_sgemv) { /* the same products as CBLAS gemv calls */
+                g_sgemv(CB_ROW_MAJOR, CB_NO_TRANS, kv, nope, 1.0F, uk + hh * nope, H * nope, qh, 1,
+                        0.0F, lq, 1);
+                g_sgemv(CB_ROW_MAJOR, CB_NO_TRANS, len, kv, 1.0F, cache, kv, lq, 1, 0.0F, scores, 1);
+                g_sgemv(CB_ROW_MAJOR, CB_NO_TRANS, len, rp, 1.0F, kc, rp, qh + nope, 1, 1.0F, scores,
+                        1);
+            } else if (absorbed) {
                 for (int r = 0; r < kv; ++r) {
                     float s = 0;
                     for (int n = 0; n < nope; ++n)
@@ -516,12 +555,13 @@ int orc_decode(const orc_config* c, const float* params, const float* out_proj, 
                         s += rk[(size_t)i * H * nope + hh * nope + n] * qh[n];
                     scores[i] = s;
                 }
-            for (int i = 0; i < len; ++i) {
-                float s = 0;
-                for (int j = 0; j < rp; ++j)
-                    s += kc[(size_t)i * rp + j] * qh[nope + j];
-                scores[i] = s + scores[i];
-            }
+            if (!(absorbed && g_sgemv))
+                for (int i = 0; i < len; ++i) {
+                    float s = 0;
+                    for (int j = 0; j < rp; ++j)
+                        s += kc[(size_t)i * rp + j] * qh[nope + j];
+                    scores[i] = s + scores[i];
+                }
             float mx = scores[0] * scale;
             for (int i = 0; i < len; ++i) {
                 scores[i] *= scale;
@@ -534,7 +574,10 @@ int orc_decode(const orc_config* c, const float* params, const float* out_proj, 
             }
             for (int i = 0; i < len; ++i)
                 scores[i] /= sum;
-            if (absorbed)
+            if (absorbed && g_sgemv)
+                g_sgemv(CB_ROW_MAJOR, CB_TRANS, len, kv, 1.0F, cache, kv, scores, 1, 0.0F,
+                        lctx + hh * kv, 1);
+            else if (absorbed)
                 for (int r = 0; r < kv; ++r) {
                     float s = 0;
                     for (int i = 0; i < len; ++i)

@@ -84,6 +84,11 @@ int orc_decode(const orc_config* c, const float* params, const float* out_proj, 
 
 /* Threads used by orc_attention_paged (default 1; sessions run in parallel). */
 void orc_set_threads(int n);
+/* A 64-bit-index CBLAS sgemm / sgemv (both, or both NULL) for the products of
+ * orc_forward / orc_decode, in place of the plain loops: the portable CBLAS standing in
+ * for Accelerate when the CPU baseline is timed.  Not thread-safe against running
+ * calls; set it before starting any. */
+void orc_set_blas(void* sgemm, void* sgemv);
 
 /* ---- Absorbed MLA attention over a paged cache (inference.cpp:116-153, fp32).
  * Page record layout (one per page, per layer): latent section

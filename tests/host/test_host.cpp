@@ -93,7 +93,8 @@ std::vector<float> tiny_params(const ModelConfig& m, uint64_t seed) {
     return p;
 }
 
-// CpuDecoder over the oracle: prefill = decode from position 0, one token at a time.
+// CpuDecoder over the oracle (inference.cpp:47-174): prefill runs the full forward and
+// keeps its cache rows (rounded to fp16, as the device cache holds them); decode appends.
 struct CpuDecoder {
     orc_config c;
     const std::vector<float>& params;
@@ -113,9 +114,21 @@ struct CpuDecoder {
         return logits;
     }
     const std::vector<float>& prefill(const std::vector<uint16_t>& ids) {
-        position = 0;
-        for (uint16_t t : ids)
-            decode(t);
+        const int T = (int)ids.size(), L = c.n_layers, kv = c.kv_lora_rank, rp = c.head_dim_rope;
+        const size_t S = (size_t)c.max_sequence_length;
+        std::vector<float> all((size_t)T * c.vocab_size), ckv((size_t)L * T * kv),
+            kr((size_t)L * T * rp);
+        orc_forward(&c, params.data(), ids.data(), T, all.data(), ckv.data(), kr.data());
+        auto h = [](float x) { return orc_f16_to_f32(orc_f32_to_f16(x)); };
+        for (int l = 0; l < L; ++l)
+            for (int t = 0; t < T; ++t) {
+                for (int j = 0; j < kv; ++j)
+                    latent[((size_t)l * S + t) * kv + j] = h(ckv[((size_t)l * T + t) * kv + j]);
+                for (int j = 0; j < rp; ++j)
+                    rope[((size_t)l * S + t) * rp + j] = h(kr[((size_t)l * T + t) * rp + j]);
+            }
+        std::copy(all.end() - c.vocab_size, all.end(), logits.begin());
+        position = T;
         return logits;
     }
 };
@@ -223,6 +236,62 @@ HOST_TEST(hip_execution_matches_cpu_decoder, true) {  // test_mps.cpp:126-166
     }
     std::printf("  max |hip - cpu| over prefill + 16 decodes: %.3g\n", worst);
     CHECK(worst < 5e-3F);
+}
+
+HOST_TEST(weight_changes_invalidate_decode_cache, true) {  // test_training.cpp:111-122
+    const ModelConfig m = tiny();
+    std::vector<float> params = tiny_params(m, 9);
+    auto engine = HipEngine::create(m, params, {4, 64, 32, 16});
+    REQUIRE(engine);
+    auto exec = make_execution(engine.value(), "hip");  // the reference's default, "fp32"
+    REQUIRE(exec);
+    Execution& x = *exec.value();
+    const std::vector<uint16_t> ids = {1, 2, 3};
+    REQUIRE(x.prefill(ids));
+    params[0] += 0.01F;
+    REQUIRE(engine.value()->update_weights(params));
+    auto stale = x.decode(4);
+    CHECK(!stale && stale.error().code == ErrorCode::invalid_argument);
+    REQUIRE(x.prefill(ids));
+    auto fresh = x.decode(4);
+    REQUIRE(fresh);
+    CpuDecoder cpu(m, params);
+    cpu.prefill(ids);
+    CHECK(max_abs_diff(fresh.value(), cpu.decode(4)) < 5e-3F);
+    auto bad = make_execution(engine.value(), "hip", "bf16");
+    CHECK(!bad && bad.error().code == ErrorCode::unsupported);
+    auto other = make_execution(engine.value(), "mps");
+    CHECK(!other && other.error().code == ErrorCode::unsupported);
+}
+
+HOST_TEST(forward_and_stats, true) {  // execution.hpp:25-39, bench_main.cpp:358-396
+    const ModelConfig m = tiny();
+    const std::vector<float> params = tiny_params(m, 4);
+    auto engine = HipEngine::create(m, params, {4, 64, 32, 16});
+    REQUIRE(engine);
+    auto exec = make_execution(engine.value(), "hip", "fp16");
+    REQUIRE(exec);
+    Execution& x = *exec.value();
+    std::vector<uint16_t> ids = prompt_ids(24, m.vocab_size, 11);
+    const ExecutionStats before = x.stats();
+    auto full = x.forward(ids, 2, 12);
+    REQUIRE(full);
+    const Matrix& f = *full.value();
+    CHECK(f.rows == 24 && f.cols == m.vocab_size);
+    // sequence 1 on its own: its prefill gives row 23 (the last of the second sequence)
+    auto out = x.prefill(std::span<const uint16_t>(ids).subspan(12, 11));
+    REQUIRE(out);
+    auto step = x.decode(ids[23]);
+    REQUIRE(step);
+    float worst = 0;
+    for (int j = 0; j < m.vocab_size; ++j)
+        worst = std::max(worst, std::abs(step.value()[(std::size_t)j] - f(23, j)));
+    std::printf("  decode vs forward row: %.3g\n", worst);
+    CHECK(worst < 5e-3F);
+    const ExecutionStats after = x.stats();
+    CHECK(after.graph_submissions - before.graph_submissions == 3);  // forward, prefill, decode
+    CHECK(after.host_waits - before.host_waits == 3);
+    CHECK(after.metal_kernel_submissions > before.metal_kernel_submissions);
 }
 
 HOST_TEST(forks_share_weights_and_reject_bad_input, true) {

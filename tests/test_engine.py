@@ -179,6 +179,89 @@ def test_shorter_reprefill_after_decoding(gpu, orc):
 
 
 @pytest.mark.gpu
+def test_weight_changes_invalidate_decode_cache(gpu, orc):
+    """tests/test_training.cpp:111-122 on the engine: after the weights change, a session
+    prefilled with the old ones cannot decode (invalid_argument, CpuDecoder's message,
+    inference.cpp:71-75), nor can its fork; after a new prefill it decodes with the new
+    weights, equal to the oracle on them."""
+    import cpp_inference_train_engine_amd as mla
+    cfg, params, _ = _models(TINY, seed=9)
+    eng = _engine(gpu, TINY, params, max_sessions=4, max_rows=64, num_pages=16, page_size=16)
+    a, empty = eng.session(), eng.session()
+    a.prefill([1, 2, 3])
+    a.decode(4)
+    fork = a.fork_prefix()
+    new = params.copy()
+    new[0] += 0.01  # token_embedding[0, 0], as the reference test changes it
+    new[1000:2000] *= 1.5
+    eng.update_weights(new)
+    assert eng.stats()["revision"] == 1
+    for s in (a, fork):
+        with pytest.raises(mla.MlaError) as e:
+            s.decode(4)
+        assert e.value.code == "invalid_argument"
+        assert "current-weight prefill" in str(e.value)
+        with pytest.raises(mla.MlaError):
+            eng.step([s], [[4]])
+    p16 = orc.bits_to_f32(orc.round_f16(new))
+    dec = orc.Decoder(cfg, p16, round_cache=True)
+    np.testing.assert_allclose(a.prefill([1, 2, 3]), dec.prefill([1, 2, 3]), rtol=0,
+                               atol=LOGIT_ATOL)
+    np.testing.assert_allclose(a.decode(4), dec.decode(4), rtol=0, atol=LOGIT_ATOL)
+    # a session that held nothing when the weights changed starts on the new ones
+    np.testing.assert_allclose(empty.prefill([1, 2, 3]), orc.Decoder(
+        cfg, p16, round_cache=True).prefill([1, 2, 3]), rtol=0, atol=LOGIT_ATOL)
+    eng.close()
+
+
+@pytest.mark.gpu
+def test_forward_returns_every_position(gpu, orc):
+    """Execution::forward(ids, batch, sequence) (execution.hpp:38-39): the logits of every
+    position of each sequence equal Model::forward's (the oracle's) rows; chunking by
+    max_rows changes nothing; and decode after prefill equals forward's last row, the check
+    the reference's decode bench records (apps/bench_main.cpp:378-396)."""
+    cfg, params, p16 = _models(MLA36M, seed=6)
+    rng = np.random.default_rng(6)
+    ids = rng.integers(0, MLA36M["vocab_size"], (3, 70)).astype(np.uint16)
+    eng = _engine(gpu, MLA36M, params, max_sessions=4, max_rows=256, num_pages=16)
+    got = eng.forward(ids, 3, 70)
+    assert got.shape == (210, MLA36M["vocab_size"])
+    for b in range(3):
+        want = orc.forward(cfg, p16, ids[b])
+        err = np.abs(got[b * 70:(b + 1) * 70] - want).max()
+        _say(f"forward sequence {b}: max |err| {err:.3e}")
+        assert err <= LOGIT_ATOL
+    assert eng.info()["active_sessions"] == 0 and eng.info()["free_pages"] == 16
+    ex = eng.session()
+    ex.prefill(ids[0, :69])
+    np.testing.assert_allclose(ex.decode(int(ids[0, 69])), got[69], rtol=0, atol=LOGIT_ATOL)
+    eng.close()
+    small = _engine(gpu, MLA36M, params, max_sessions=4, max_rows=50, num_pages=16)
+    np.testing.assert_allclose(small.forward(ids, 3, 70), got, rtol=0, atol=1e-5)
+    small.close()
+
+
+@pytest.mark.gpu
+def test_stats_count_submissions_waits_and_kernels(gpu):
+    """Execution::stats (execution.hpp:25-27, reported per update by bench_main.cpp:
+    358-368): one decode call is one forward submission and one host wait; its kernels are
+    the metadata build, the embedding, per layer the projections, the attention and its
+    split merge and the three FFN kernels, then the logits and the greedy token."""
+    _, params, _ = _models(MLA36M, seed=7)
+    eng = _engine(gpu, MLA36M, params, max_sessions=2, max_rows=64, num_pages=8)
+    ex = eng.session()
+    ex.prefill(list(range(1, 41)))
+    before = ex.stats()
+    ex.decode(5)
+    after = ex.stats()
+    L = MLA36M["n_layers"]
+    assert after["graph_submissions"] - before["graph_submissions"] == 1
+    assert after["host_waits"] - before["host_waits"] == 1
+    assert after["kernel_submissions"] - before["kernel_submissions"] == 1 + 1 + 6 * L + 2
+    eng.close()
+
+
+@pytest.mark.gpu
 def test_decode_equals_full_recomputation_on_gpu(gpu):
     """tests/test_training.cpp:52-76 on the engine: after prefill(prompt) and k decodes,
     the logits equal those of prefill(prompt + the k tokens) (one chunk and 3 chunks)."""

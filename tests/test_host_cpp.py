@@ -46,4 +46,4 @@ def test_host_api_gpu_tests(gpu, tiny_fixture, tmp_path):
     write_export(export, TINY, np.asarray(tiny_fixture["params"], np.float32), tok, "f16")
     res = _run(["--gpu", GOLDEN, export], 180)
     assert res.returncode == 0 and "0 failed checks" in res.stdout
-    assert res.stdout.count("PASS ") == 7
+    assert res.stdout.count("PASS ") == 9

@@ -357,3 +357,34 @@ def test_append_places_every_value_at_its_layout_word(orc, shape):
         seen[pg, lw[0]] = True
         seen[pg, rw[0]] = True
     assert np.all(vals[~seen] == 0)
+
+
+def test_blas_path_equals_the_loops(orc):
+    """The CPU baseline times the oracle with its products on a portable CBLAS (numpy's
+    OpenBLAS, standing in for the reference's Accelerate calls); that path must compute
+    what the pinned loops compute, up to summation order: the full forward and absorbed
+    decode agree within 1e-5 of the logits' scale on a small random model."""
+    from conftest import MLA36M
+    cfgd = dict(MLA36M, n_layers=2, vocab_size=2048, max_sequence_length=128)
+    cfg = orc.Config.from_dict(cfgd)
+    params = orc.model_init(cfg, 5)
+    ids = orc.Rng(5).bounded_many(cfg.vocab_size, 48).astype(np.uint16)
+
+    def run():
+        d = orc.Decoder(cfg, params, absorbed=True)
+        pre = d.prefill(ids[:40])
+        dec = [d.decode(int(t)) for t in ids[40:]]
+        return pre, np.stack(dec), orc.forward(cfg, params, ids)
+
+    loops = run()
+    desc = orc.use_blas(True)
+    try:
+        if desc is None:
+            pytest.skip("numpy ships no OpenBLAS here")
+        blas = run()
+    finally:
+        orc.use_blas(False)
+    for a, b in zip(loops, blas):
+        scale = float(np.abs(a).max())
+        assert np.abs(a - b).max() <= 1e-5 * max(scale, 1.0)
+    assert "OpenBLAS" in desc

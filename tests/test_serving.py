@@ -237,3 +237,47 @@ def test_scheduler_from_many_threads(gpu, tiny_fixture):
         assert (g["tokens"], g["text"], g["finish_reason"]) == \
             (alone["tokens"], want_text, alone["finish_reason"]), (p, c)
     eng.close()
+
+
+@pytest.mark.gpu
+def test_close_while_other_threads_poll(gpu, tiny_fixture):
+    """A server shutting down while its handler threads poll: close() stops the scheduler
+    (queued requests never start, running ones end as cancelled), wakes the waiting polls
+    and frees it only after every call in progress has returned.  Each poller ends with a
+    finished status or the scheduler's "closed" error, never a crash or a hang."""
+    import threading
+    eng = _engine(gpu, tiny_fixture, sessions=2)
+    t = gpu.HipTokenizer(TOK_TINY)
+    sch = gpu.Scheduler(eng, t, max_context=64, max_new_tokens=40, max_queue=16)
+    cfg = gpu.GenerationConfig(max_new_tokens=40, temperature=0.0)
+    rids = [sch.submit([t.special("<|bos|>")] + [5 + k] * 8, cfg, stream=True)
+            for k in range(6)]
+    outcomes, started = {}, threading.Barrier(len(rids) + 1)
+
+    def poller(rid):
+        started.wait()
+        try:
+            while True:
+                _, status = sch.poll(rid, 0.5)
+                if status["done"]:
+                    outcomes[rid] = ("done", status["finish_reason"])
+                    return
+        except gpu.MlaError as e:
+            outcomes[rid] = ("error", e.code)
+
+    threads = [threading.Thread(target=poller, args=(r,)) for r in rids]
+    for th in threads:
+        th.start()
+    started.wait()
+    sch.close()
+    for th in threads:
+        th.join(30)
+    assert not any(th.is_alive() for th in threads)
+    assert set(outcomes) == set(rids)
+    for kind, what in outcomes.values():
+        assert (kind == "done" and what in ("stop", "length", "cancelled")) or \
+            (kind == "error" and what == "unavailable"), (kind, what)
+    with pytest.raises(gpu.MlaError):
+        sch.submit([1, 2, 3], cfg)
+    sch.close()  # idempotent
+    eng.close()
