@@ -52,6 +52,10 @@ _SIGNATURES = {
                              C.c_int]),
     "mla_decode_merge": (C.c_int, [C.c_void_p] + [C.c_int] * 3 + [C.c_void_p] * 4 +
                          [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]),
+    "mla_noalloc_scratch_bytes": (C.c_size_t, []),
+    "mla_decode_attention_noalloc": (C.c_int, [C.c_void_p] + [C.c_int] * 6 + [C.c_float] +
+                                     [C.c_void_p] * 2 + [C.c_int] * 2 + [C.c_void_p] * 8 +
+                                     [C.c_int, C.c_void_p, C.c_void_p, C.c_int]),
     "mla_prefill_attention": (C.c_int, [C.c_void_p] + [C.c_int] * 6 + [C.c_float] +
                               [C.c_void_p] * 3 + [C.c_int] * 2 + [C.c_void_p] * 4 +
                               [C.c_int, C.c_void_p, C.c_void_p, C.c_int]),

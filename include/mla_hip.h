@@ -181,6 +181,28 @@ int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_
                      int max_work, float* out, float* lse, const void* workspace,
                      size_t workspace_bytes);
 
+/* mla_decode_attention without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  The split partials go to a file-scope device array of
+ * MLA_NOALLOC_SCRATCH_MIB MiB that each GPU the library runs on holds until the process
+ * ends; the call allocates nothing.  Arguments, kernels and results are those of
+ * mla_decode_attention.  MLA_ERR_INVALID_ARGUMENT when the partials would exceed the array
+ * (mla_decode_workspace_bytes(max_work, B, n_heads, kv_rank) > mla_noalloc_scratch_bytes(),
+ * e.g. above ~4,000 work items at H = 8, kv_rank = 128), or when `stream` belongs to a
+ * device other than the calling thread's current one.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, other threads) race and must
+ * be ordered by the caller. */
+#define MLA_NOALLOC_SCRATCH_MIB 16
+size_t mla_noalloc_scratch_bytes(void);
+int mla_decode_attention_noalloc(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
+                                 int page_size, int dtype, float scale,
+                                 const int32_t* cu_seqlens_q, const int32_t* page_table,
+                                 int max_pages, int num_pool_pages, const void* pages,
+                                 const void* q_latent, const void* q_rope,
+                                 const int32_t* num_splits, const int32_t* cu_splits,
+                                 const int32_t* work_desc, const int32_t* work_pages,
+                                 const int32_t* info, int max_work, float* out, float* lse,
+                                 int flags);
 
 /* ------------------------------------------------------------------ (c)
  * Absorbed MLA chunked-prefill attention over the paged cache, for every session
