@@ -125,19 +125,6 @@ int load_config(const std::string& path, mla_model_config& c) {  // ModelConfig:
     return st != MLA_OK ? st : config_from_json(j, c);
 }
 
-// ------------------------------------------------------------ tokenizer ----
-// Tokenizer::load's checks (tokenizer.cpp:70-127); the tokenizer's identity is the
-// SHA-256 of its file bytes.
-int check_tokenizer(const std::string& path, int& vocab, std::string& hash) {
-    Tokenizer t;
-    const int st = tokenizer_load(path, t);
-    if (st != MLA_OK)
-        return st;
-    vocab = t.vocab;
-    hash = t.hash;
-    return MLA_OK;
-}
-
 // ------------------------------------------------------------- registry ----
 struct Slot {
     size_t offset, rows, cols;
@@ -181,117 +168,252 @@ float half_to_float(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
-// load_checkpoint(path, training = false) (src/train/checkpoint.cpp:186-324).
-int read_export(const std::string& dir, mla_model_config& cfg, float* params, size_t count) {
-    std::string raw, err;
-    if (!read_file(join(dir, "manifest.json"), raw, err))
-        return fail(MLA_ERR_IO, err);
-    std::string complete;
-    if (!read_file(join(dir, "COMPLETE"), complete, err) || complete != sha256_hex(raw) + "\n")
-        return fail(MLA_ERR_IO, "Checkpoint is incomplete or manifest checksum failed");
+// ------------------------------------------------------------ validator ----
+// A directory check is a pipeline of stages over one ExportScan; each stage either
+// passes or names the failure (the reference's ErrorCode and message,
+// load_checkpoint(path, training = false), src/train/checkpoint.cpp:186-324).  The stage
+// order, and the rule order within a tensor entry, are the ones the failure-mode tests
+// pin: a defect is reported by the first rule it breaks.
+struct Failure {
+    int code = MLA_OK;
+    std::string message;
+    explicit operator bool() const { return code != MLA_OK; }
+};
+Failure io_failure(std::string m) { return {MLA_ERR_IO, std::move(m)}; }
+
+// One manifest tensor entry, as read from the manifest.
+struct TensorEntry {
+    std::string name, file, dtype, role;
+    size_t offset = 0, nbytes = 0;
+    uint32_t crc = 0;
+    std::vector<long long> shape;
+};
+
+struct ExportScan {
+    std::string dir;
+    std::string manifest_text;
     Json manifest;
+    bool training = false;  // a mini-mla-checkpoint (optimizer state may follow the weights)
+    mla_model_config cfg{};
+    size_t n_params = 0;
+    std::map<std::string, std::string> files;      // every listed file, hash-verified
+    std::map<std::string, size_t> cursor;          // next free byte of each tensor file
+    std::map<std::string, Slot> pending;           // registry tensors not yet seen
+    std::set<std::string> names;                   // entry names seen so far
+    float* params = nullptr;                       // may be null: checks only
+    size_t params_count = 0;
+};
+
+Failure seal_stage(ExportScan& x) {  // COMPLETE holds the manifest's SHA-256
+    std::string err, complete;
+    if (!read_file(join(x.dir, "manifest.json"), x.manifest_text, err))
+        return io_failure(err);
+    if (!read_file(join(x.dir, "COMPLETE"), complete, err) ||
+        complete != sha256_hex(x.manifest_text) + "\n")
+        return io_failure("Checkpoint is incomplete or manifest checksum failed");
     try {
-        manifest = JsonReader(raw).parse();
+        x.manifest = JsonReader(x.manifest_text).parse();
     } catch (const std::exception& e) {
-        return fail(MLA_ERR_INVALID_ARGUMENT, e.what());
+        return {MLA_ERR_INVALID_ARGUMENT, e.what()};
     }
-    try {
-        const std::string format = manifest.at("format").string();
-        if ((format != "mini-mla-checkpoint" && format != "mini-mla-model") ||
-            manifest.at("version").integer() != 1)
-            return fail(MLA_ERR_UNSUPPORTED,
-                        "Unsupported model format or inference export used for resume");
-        int st = load_config(join(dir, "config.json"), cfg);
-        if (st != MLA_OK)
-            return st;
-        const size_t n_params = mla_config_parameter_count(&cfg);
-        if (sha256_hex(config_dump(cfg)) != manifest.at("model_config_sha256").string() ||
-            n_params != manifest.at("parameter_count").size_integer())
-            return fail(MLA_ERR_INVALID_ARGUMENT, "Checkpoint model configuration mismatch");
-        int vocab = 0;
-        std::string tok_hash;
-        st = check_tokenizer(join(dir, "tokenizer.json"), vocab, tok_hash);
-        if (st != MLA_OK)
-            return st;
-        if (tok_hash != manifest.at("tokenizer_sha256").string() || vocab != cfg.vocab_size)
-            return fail(MLA_ERR_INVALID_ARGUMENT, "Checkpoint tokenizer mismatch");
-        if (params && count != n_params)
-            return fail(MLA_ERR_INVALID_ARGUMENT,
-                        "parameter buffer holds " + std::to_string(count) +
-                            " floats; the export has " + std::to_string(n_params));
-        std::map<std::string, std::string> files;
-        for (const auto& [name, hash] : manifest.at("sha256").object()) {
-            if (name != "weights.bin" && name != "optimizer.bin" && name != "trainer_state.json")
-                throw std::invalid_argument("Invalid checkpoint filename");
-            std::string bytes;
-            if (!read_file(join(dir, name.c_str()), bytes, err))
-                return fail(MLA_ERR_IO, err);
-            if (sha256_hex(bytes) != hash.string())
-                throw std::invalid_argument("Checkpoint file checksum failed: " + name);
-            files.emplace(name, std::move(bytes));
-        }
-        std::map<std::string, Slot> expected = registry(cfg);
-        std::set<std::string> seen;
-        std::map<std::string, size_t> ends;
-        for (const Json& entry : manifest.at("tensors").array()) {
-            const std::string name = entry.at("name").string(), file = entry.at("file").string(),
-                              dtype = entry.at("dtype").string();
-            if (file != "weights.bin" && file != "optimizer.bin")
-                throw std::invalid_argument("Invalid tensor filename");
-            if (!seen.insert(name).second)
-                throw std::invalid_argument("Duplicate named tensor");
-            const size_t offset = entry.at("offset").size_integer(),
-                         nbytes = entry.at("nbytes").size_integer();
-            auto fit = files.find(file);
-            if (fit == files.end() || offset != ends[file] || offset > fit->second.size() ||
-                nbytes > fit->second.size() - offset)
-                throw std::invalid_argument("Invalid tensor extent or missing tensor file");
-            const uint8_t* bytes = reinterpret_cast<const uint8_t*>(fit->second.data()) + offset;
-            ends[file] = offset + nbytes;
-            if (crc32(bytes, nbytes) != entry.at("crc32").size_integer())
-                throw std::invalid_argument("Tensor checksum failed: " + name);
-            auto it = expected.find(name);
-            if (it == expected.end()) {
-                if (file == "optimizer.bin" && format == "mini-mla-checkpoint")
-                    continue;  // training state: not needed for inference
-                throw std::invalid_argument("Unexpected tensor: " + name);
-            }
-            const Slot slot = it->second;
-            const Json::Array& shape = entry.at("shape").array();
-            const size_t item = dtype == "f32" ? 4 : dtype == "f16" ? 2 : 0;
-            if (!item || file != "weights.bin" || shape.size() != 2 ||
-                shape[0].integer() != (int)slot.rows || shape[1].integer() != (int)slot.cols ||
-                nbytes != slot.rows * slot.cols * item || entry.at("role").string() != slot.role)
-                throw std::invalid_argument("Tensor shape, dtype, role, or file mismatch: " +
-                                            name);
-            const size_t n = slot.rows * slot.cols;
-            bool finite = true;
-            for (size_t k = 0; k < n; ++k) {
-                float x;
-                if (item == 4) {
-                    std::memcpy(&x, bytes + 4 * k, 4);
-                } else {
-                    uint16_t h;
-                    std::memcpy(&h, bytes + 2 * k, 2);
-                    x = half_to_float(h);
-                }
-                finite = finite && std::isfinite(x);
-                if (params)
-                    params[slot.offset + k] = x;
-            }
-            if (!finite)
-                throw std::invalid_argument("Nonfinite checkpoint tensor: " + name);
-            expected.erase(it);
-        }
-        if (!expected.empty())
-            throw std::invalid_argument("Checkpoint is missing tensor: " + expected.begin()->first);
-        for (const auto& [file, end] : ends)
-            if (end != files.at(file).size())
-                throw std::invalid_argument("Unindexed trailing tensor data");
-        return MLA_OK;
-    } catch (const std::exception& e) {
-        return fail(MLA_ERR_IO, e.what());
+    return {};
+}
+
+Failure header_stage(ExportScan& x) {  // an inference export or a training checkpoint, v1
+    const std::string format = x.manifest.at("format").string();
+    x.training = format == "mini-mla-checkpoint";
+    if ((!x.training && format != "mini-mla-model") || x.manifest.at("version").integer() != 1)
+        return {MLA_ERR_UNSUPPORTED, "Unsupported model format or inference export used for resume"};
+    return {};
+}
+
+Failure architecture_stage(ExportScan& x) {  // config.json is the manifest's architecture
+    if (int st = load_config(join(x.dir, "config.json"), x.cfg))
+        return {st, mla_last_error()};
+    x.n_params = mla_config_parameter_count(&x.cfg);
+    if (sha256_hex(config_dump(x.cfg)) != x.manifest.at("model_config_sha256").string() ||
+        x.n_params != x.manifest.at("parameter_count").size_integer())
+        return {MLA_ERR_INVALID_ARGUMENT, "Checkpoint model configuration mismatch"};
+    return {};
+}
+
+Failure tokenizer_stage(ExportScan& x) {  // tokenizer.json is the manifest's, for this vocab
+    Tokenizer tok;
+    if (int st = tokenizer_load(join(x.dir, "tokenizer.json"), tok))
+        return {st, mla_last_error()};
+    if (tok.hash != x.manifest.at("tokenizer_sha256").string() || tok.vocab != x.cfg.vocab_size)
+        return {MLA_ERR_INVALID_ARGUMENT, "Checkpoint tokenizer mismatch"};
+    return {};
+}
+
+Failure files_stage(ExportScan& x) {  // every listed file exists and has its SHA-256
+    static const std::set<std::string> kKnown = {"weights.bin", "optimizer.bin",
+                                                 "trainer_state.json"};
+    for (const auto& [file, digest] : x.manifest.at("sha256").object()) {
+        if (!kKnown.count(file))
+            return io_failure("Invalid checkpoint filename");
+        std::string bytes, err;
+        if (!read_file(join(x.dir, file.c_str()), bytes, err))
+            return io_failure(err);
+        if (sha256_hex(bytes) != digest.string())
+            return io_failure("Checkpoint file checksum failed: " + file);
+        x.files[file] = std::move(bytes);
     }
+    x.pending = registry(x.cfg);
+    return {};
+}
+
+TensorEntry read_entry(const Json& e) {
+    TensorEntry t;
+    t.name = e.at("name").string();
+    t.file = e.at("file").string();
+    t.dtype = e.at("dtype").string();
+    t.role = e.at("role").string();
+    t.offset = e.at("offset").size_integer();
+    t.nbytes = e.at("nbytes").size_integer();
+    t.crc = (uint32_t)e.at("crc32").size_integer();
+    for (const Json& d : e.at("shape").array())
+        t.shape.push_back(d.integer());
+    return t;
+}
+
+size_t dtype_bytes(const std::string& dtype) { return dtype == "f32" ? 4 : dtype == "f16" ? 2 : 0; }
+
+const uint8_t* entry_bytes(const ExportScan& x, const TensorEntry& t) {
+    return reinterpret_cast<const uint8_t*>(x.files.at(t.file).data()) + t.offset;
+}
+
+// Widens the entry's values to fp32 (into params when given); false if one is not finite.
+bool widen(const ExportScan& x, const TensorEntry& t, const Slot& slot) {
+    const uint8_t* src = entry_bytes(x, t);
+    const size_t n = slot.rows * slot.cols;
+    bool finite = true;
+    for (size_t k = 0; k < n; ++k) {
+        float v;
+        if (t.dtype == "f32") {
+            std::memcpy(&v, src + 4 * k, 4);
+        } else {
+            uint16_t h;
+            std::memcpy(&h, src + 2 * k, 2);
+            v = half_to_float(h);
+        }
+        finite = finite && std::isfinite(v);
+        if (x.params)
+            x.params[slot.offset + k] = v;
+    }
+    return finite;
+}
+
+// What one manifest entry must satisfy, in the order the failure-mode tests pin.  A rule
+// returns true when the entry passes it; `named` rules append the tensor's name.
+enum class Verdict { pass, fail, skip };
+struct EntryRule {
+    const char* message;
+    bool named;
+    Verdict (*check)(ExportScan&, const TensorEntry&);
+};
+const EntryRule kEntryRules[] = {
+    {"Invalid tensor filename", false,
+     [](ExportScan&, const TensorEntry& t) {
+         return t.file == "weights.bin" || t.file == "optimizer.bin" ? Verdict::pass : Verdict::fail;
+     }},
+    {"Duplicate named tensor", false,
+     [](ExportScan& x, const TensorEntry& t) {
+         return x.names.insert(t.name).second ? Verdict::pass : Verdict::fail;
+     }},
+    {"Invalid tensor extent or missing tensor file", false,
+     [](ExportScan& x, const TensorEntry& t) {  // packed back to back, inside the file
+         const auto f = x.files.find(t.file);
+         if (f == x.files.end())
+             return Verdict::fail;
+         size_t& next = x.cursor[t.file];
+         const size_t size = f->second.size();
+         if (t.offset != next || t.offset > size || t.nbytes > size - t.offset)
+             return Verdict::fail;
+         next = t.offset + t.nbytes;
+         return Verdict::pass;
+     }},
+    {"Tensor checksum failed: ", true,
+     [](ExportScan& x, const TensorEntry& t) {
+         return crc32(entry_bytes(x, t), t.nbytes) == t.crc ? Verdict::pass : Verdict::fail;
+     }},
+    {"Unexpected tensor: ", true,
+     [](ExportScan& x, const TensorEntry& t) {
+         if (x.pending.count(t.name))
+             return Verdict::pass;
+         // a training checkpoint's optimizer moments: not needed for inference
+         return x.training && t.file == "optimizer.bin" ? Verdict::skip : Verdict::fail;
+     }},
+    {"Tensor shape, dtype, role, or file mismatch: ", true,
+     [](ExportScan& x, const TensorEntry& t) {
+         const Slot& s = x.pending.at(t.name);
+         const size_t item = dtype_bytes(t.dtype);
+         const bool ok = item && t.file == "weights.bin" && t.role == s.role &&
+                         t.shape.size() == 2 && t.shape[0] == (long long)s.rows &&
+                         t.shape[1] == (long long)s.cols && t.nbytes == s.rows * s.cols * item;
+         return ok ? Verdict::pass : Verdict::fail;
+     }},
+    {"Nonfinite checkpoint tensor: ", true,
+     [](ExportScan& x, const TensorEntry& t) {
+         const auto it = x.pending.find(t.name);
+         const bool finite = widen(x, t, it->second);
+         x.pending.erase(it);
+         return finite ? Verdict::pass : Verdict::fail;
+     }},
+};
+
+Failure tensors_stage(ExportScan& x) {
+    if (x.params && x.n_params != x.params_count)
+        return {MLA_ERR_INVALID_ARGUMENT, "parameter buffer holds " +
+                                              std::to_string(x.params_count) +
+                                              " floats; the export has " +
+                                              std::to_string(x.n_params)};
+    for (const Json& raw : x.manifest.at("tensors").array()) {
+        const TensorEntry t = read_entry(raw);
+        for (const EntryRule& rule : kEntryRules) {
+            const Verdict v = rule.check(x, t);
+            if (v == Verdict::fail)
+                return io_failure(rule.named ? rule.message + t.name : std::string(rule.message));
+            if (v == Verdict::skip)
+                break;
+        }
+    }
+    return {};
+}
+
+Failure coverage_stage(ExportScan& x) {  // nothing missing, nothing unindexed
+    if (!x.pending.empty())  // the first absent tensor in name order
+        return io_failure("Checkpoint is missing tensor: " + x.pending.begin()->first);
+    for (const auto& [file, end] : x.cursor)
+        if (end != x.files.at(file).size())
+            return io_failure("Unindexed trailing tensor data");
+    return {};
+}
+
+// Reads a model export or checkpoint directory: every check of load_checkpoint(path,
+// false) with its code and message; on success cfg is the architecture and params (when
+// not null) holds count = parameter_count fp32 values in registry order.
+int read_export(const std::string& dir, mla_model_config& cfg, float* params, size_t count) {
+    ExportScan x;
+    x.dir = dir;
+    x.params = params;
+    x.params_count = count;
+    using Stage = Failure (*)(ExportScan&);
+    static const Stage kStages[] = {seal_stage,  header_stage,   architecture_stage,
+                                    tokenizer_stage, files_stage, tensors_stage,
+                                    coverage_stage};
+    for (size_t k = 0; k < sizeof(kStages) / sizeof(kStages[0]); ++k) {
+        Failure f;
+        try {
+            f = kStages[k](x);
+        } catch (const std::exception& e) {  // a manifest field missing or of the wrong type
+            f = k == 0 ? Failure{MLA_ERR_INVALID_ARGUMENT, e.what()} : io_failure(e.what());
+        }
+        if (f)
+            return fail(f.code, f.message);
+    }
+    cfg = x.cfg;
+    return MLA_OK;
 }
 
 }  // namespace

@@ -14,63 +14,127 @@
 namespace mla {
 
 namespace {
+
+// The eight role tokens; they own the last eight ids of the vocabulary in this order
+// (docs/file_formats.md, "Tokenizer").
 const char* const kSpecialNames[8] = {"<|pad|>",       "<|bos|>",    "<|eos|>",  "<|user|>",
                                       "<|assistant|>", "<|system|>", "<|tool|>", "<|sep|>"};
+constexpr int kSpecials = 8;
+constexpr size_t kMaxTokenBytes = size_t(1) << 20;
+
+// A load failure: an ErrorCode status and the message the reference gives for it.
+struct Rejection {
+    int code = MLA_OK;
+    std::string message;
+    explicit operator bool() const { return code != MLA_OK; }
+};
+Rejection reject(int code, std::string message) { return {code, std::move(message)}; }
+Rejection invalid(std::string message) { return reject(MLA_ERR_INVALID_ARGUMENT, std::move(message)); }
+
+// The header fields a version-1 bytes tokenizer must carry, then its vocabulary size.
+Rejection read_header(const io::Json& j, int& vocab) {
+    struct Field {
+        const char* key;
+        const char* text;  // expected string, or null for the integer below
+        int number;
+    };
+    static const Field kAccepted[] = {{"format", "mini-mla-tokenizer", 0},
+                                      {"version", nullptr, 1},
+                                      {"pretokenizer", "bytes-v1", 0}};
+    for (const Field& f : kAccepted) {
+        const io::Json& v = j.at(f.key);
+        if (f.text ? v.string() != f.text : v.integer() != f.number)
+            return reject(MLA_ERR_UNSUPPORTED, "Unsupported tokenizer format or pretokenizer");
+    }
+    vocab = j.at("vocab_size").integer();
+    if (vocab < 256 + kSpecials || vocab > 65535)
+        return invalid("Tokenizer vocabulary must be in [264,65535]");
+    return {};
+}
+
+// Builds the id -> bytes table and the pair -> id map from the sequential merge list:
+// merge k creates id 256 + k, from two ids created before it, below the special range.
+class MergeBuilder {
+  public:
+    MergeBuilder(Tokenizer& t, int vocab) : t_(t), first_special_((size_t)vocab - kSpecials) {
+        t_.bytes.assign((size_t)vocab, std::string());
+        for (int b = 0; b < 256; ++b)
+            t_.bytes[(size_t)b].assign(1, (char)b);
+    }
+    Rejection add(const io::Json& merge) {
+        const io::Json::Array& triple = merge.array();
+        const size_t made = next_;
+        if (triple.size() != 3 || made >= first_special_ || triple[2].integer() != (int)made)
+            return invalid("Malformed BPE merge");
+        const int lhs = triple[0].integer(), rhs = triple[1].integer();
+        if (!earlier(lhs) || !earlier(rhs))
+            return invalid("BPE merge references a future token");
+        const uint32_t key = (uint32_t)lhs << 16 | (uint32_t)rhs;
+        if (t_.merges.count(key))
+            return invalid("Duplicate BPE pair");
+        t_.merges.emplace(key, (uint16_t)made);
+        std::string& text = t_.bytes[made];
+        text = t_.bytes[(size_t)lhs];
+        text += t_.bytes[(size_t)rhs];
+        if (text.size() > kMaxTokenBytes)
+            return invalid("BPE token exceeds size limit");
+        ++next_;
+        return {};
+    }
+
+  private:
+    bool earlier(int id) const { return id >= 0 && (size_t)id < next_; }
+    Tokenizer& t_;
+    size_t first_special_, next_ = 256;
+};
+
+// The specials object names exactly the eight role tokens, each at its fixed id.
+Rejection read_specials(const io::Json& j, int vocab, Tokenizer& t) {
+    const io::Json& specials = j.at("specials");
+    if (specials.object().size() != kSpecials)
+        return invalid("Tokenizer must define exactly eight special tokens");
+    for (int k = 0; k < kSpecials; ++k) {
+        const int want = vocab - kSpecials + k;
+        if (specials.at(kSpecialNames[k]).integer() != want)
+            return invalid("Special token IDs disagree with the native chat template");
+        t.specials.emplace_back(kSpecialNames[k], (uint16_t)want);
+        t.bytes[(size_t)want] = kSpecialNames[k];
+    }
+    return {};
+}
+
+Rejection build(const io::Json& j, Tokenizer& t) {
+    int vocab = 0;
+    if (Rejection r = read_header(j, vocab))
+        return r;
+    t.vocab = vocab;
+    MergeBuilder merges(t, vocab);
+    for (const io::Json& m : j.at("merges").array())
+        if (Rejection r = merges.add(m))
+            return r;
+    return read_specials(j, vocab, t);
+}
+
 }  // namespace
 
+// Tokenizer::load (tokenizer.cpp:70-127): the file's bytes are its identity; JSON that
+// does not parse, or lacks a field or has one of the wrong type, is invalid_argument.
 int tokenizer_load(const std::string& path, Tokenizer& t) {
     std::string text, err;
     if (!io::read_file(path, text, err))
         return fail(MLA_ERR_IO, err);
-    io::Json j;
+    Tokenizer built;
+    Rejection r;
     try {
-        j = io::JsonReader(text).parse();
+        r = build(io::JsonReader(text).parse(), built);
     } catch (const std::exception& e) {
-        return fail(MLA_ERR_INVALID_ARGUMENT, e.what());
+        r = invalid(e.what());
     }
-    try {
-        if (j.at("format").string() != "mini-mla-tokenizer" || j.at("version").integer() != 1 ||
-            j.at("pretokenizer").string() != "bytes-v1")
-            return fail(MLA_ERR_UNSUPPORTED, "Unsupported tokenizer format or pretokenizer");
-        const int vocab = j.at("vocab_size").integer();
-        if (vocab < 264 || vocab > 65535)
-            return fail(MLA_ERR_INVALID_ARGUMENT, "Tokenizer vocabulary must be in [264,65535]");
-        Tokenizer out;
-        out.vocab = vocab;
-        out.bytes.assign((size_t)vocab, std::string());
-        for (int i = 0; i < 256; ++i)
-            out.bytes[(size_t)i] = std::string(1, (char)i);
-        size_t id = 256;
-        for (const io::Json& m : j.at("merges").array()) {
-            const io::Json::Array& a = m.array();
-            if (a.size() != 3 || id >= (size_t)(vocab - 8) || a[2].integer() != (int)id)
-                throw std::invalid_argument("Malformed BPE merge");
-            const int left = a[0].integer(), right = a[1].integer();
-            if (left < 0 || right < 0 || (size_t)left >= id || (size_t)right >= id)
-                throw std::invalid_argument("BPE merge references a future token");
-            if (!out.merges.emplace((uint32_t)left << 16 | (uint32_t)right, (uint16_t)id).second)
-                throw std::invalid_argument("Duplicate BPE pair");
-            out.bytes[id] = out.bytes[(size_t)left] + out.bytes[(size_t)right];
-            if (out.bytes[id].size() > 1024 * 1024)
-                throw std::invalid_argument("BPE token exceeds size limit");
-            ++id;
-        }
-        if (j.at("specials").object().size() != 8)
-            throw std::invalid_argument("Tokenizer must define exactly eight special tokens");
-        for (int k = 0; k < 8; ++k) {
-            const int sid = j.at("specials").at(kSpecialNames[k]).integer();
-            if (sid != vocab - 8 + k)
-                throw std::invalid_argument(
-                    "Special token IDs disagree with the native chat template");
-            out.specials.emplace_back(kSpecialNames[k], (uint16_t)sid);
-            out.bytes[(size_t)sid] = kSpecialNames[k];
-        }
-        out.hash = io::sha256_hex(text);
-        t = std::move(out);
-        return MLA_OK;
-    } catch (const std::exception& e) {
-        return fail(MLA_ERR_INVALID_ARGUMENT, e.what());
-    }
+    if (r)
+        return fail(r.code, r.message);
+    built.hash = io::sha256_hex(text);
+    t = std::move(built);
+    return MLA_OK;
 }
 
 bool tokenizer_decode(const Tokenizer& t, const uint16_t* ids, size_t n, bool skip_special,
