@@ -291,6 +291,202 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
     }
 }
 
+// The build for batches whose session arrays and padded page table fit in LDS
+// (B <= kMetaLdsCap, B * max_pages <= kMetaSmallPt).  All waves stage the inputs and the
+// page ids in LDS (one load round trip each); wave 0 alone runs both scans, 64 sessions
+// per pass with the running total carried between passes (a 6-step wave scan instead of
+// a 1024-thread block scan, whose 64-bit shuffles and barriers cost microseconds); then
+// all waves write every output, with no global store before the last barrier.  Outputs
+// are bit-identical to build_metadata_kernel's.
+constexpr int kMetaSmallPt = 8192;
+
+// One DPP move of a 64-bit value (both halves with the same control); lanes the
+// control gives no source, and rows outside row_mask, receive 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ long long dpp64(long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf,
+                                               true);
+    return (long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// Inclusive scan over the 64 lanes of a wave on DPP moves (no LDS round trips): shifts
+// of 1, 2, 4, 8 lanes within each row of 16, then lane 15 of each row broadcast into
+// the next row (rows 1, 3) and lane 31 into the upper half (rows 2, 3).
+__device__ __forceinline__ long long wave_scan_incl(long long v) {
+    v += dpp64<0x111, 0xf>(v);  // row_shr:1
+    v += dpp64<0x112, 0xf>(v);  // row_shr:2
+    v += dpp64<0x114, 0xf>(v);  // row_shr:4
+    v += dpp64<0x118, 0xf>(v);  // row_shr:8
+    v += dpp64<0x142, 0xa>(v);  // row_bcast:15
+    v += dpp64<0x143, 0xc>(v);  // row_bcast:31
+    return v;
+}
+
+__global__ __launch_bounds__(kMetaThreads) void build_metadata_lds_kernel(MetadataArgs a) {
+    __shared__ int32_t s_cup[kMetaLdsCap + 1], s_q[kMetaLdsCap], s_ctx[kMetaLdsCap];
+    __shared__ int32_t s_cuq[kMetaLdsCap + 1], s_cuk[kMetaLdsCap + 1], s_cus[kMetaLdsCap + 1];
+    __shared__ int32_t s_pt[kMetaSmallPt];
+    __shared__ int err;
+    __shared__ long long s_tot[4];  // total_q, total_k, split, W
+    const int tid = threadIdx.x, lane = tid & 63, B = a.B, mp = a.max_pages;
+    const int entries = B * mp;  // <= kMetaSmallPt
+    // ---- inputs to LDS ----
+    for (int b = tid; b <= B; b += kMetaThreads) {
+        s_cup[b] = a.cu_pages[b];
+        if (b < B) {
+            s_q[b] = a.q_len[b];
+            s_ctx[b] = a.ctx_len[b];
+        }
+    }
+    if (tid == 0) {
+        err = INT_MAX;
+        s_cuq[0] = s_cuk[0] = s_cus[0] = 0;
+    }
+    __syncthreads();
+    // ---- padded page table in LDS; ids out of the pool name their session ----
+    {
+        constexpr int U = kMetaSmallPt / kMetaThreads;
+        int32_t pid[U];
+        int bad_b = INT_MAX;
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int e = tid + k * kMetaThreads;
+            const int b = e < entries ? (int)((uint32_t)e / (uint32_t)mp) : 0;
+            const int j = e - b * mp;
+            const int p0 = s_cup[b], np = s_cup[b + 1] - p0;
+            const bool listed = e < entries && j < np;
+            pid[k] = listed ? a.page_ids[p0 + j] : -1;
+            if (listed && (pid[k] < 0 || pid[k] >= a.num_pool_pages))
+                bad_b = min(bad_b, b);
+        }
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const int e = tid + k * kMetaThreads;
+            if (e < entries)
+                s_pt[e] = pid[k];
+        }
+        if (bad_b != INT_MAX)
+            atomicMin(&err, bad_b);
+    }
+    __syncthreads();
+    // ---- wave 0: cumulative rows / keys / pages, then work items per session ----
+    if (tid < 64) {
+        long long cq = 0, ck = 0, cp = 0;
+        int bad = INT_MAX;
+        for (int base = 0; base < B; base += 64) {
+            const int b = base + lane;
+            long long q = 0, kl = 0, pages = 0;
+            if (b < B) {
+                q = s_q[b];
+                const long long ctx = s_ctx[b];
+                const long long npages = (long long)s_cup[b + 1] - s_cup[b];
+                kl = ctx + q;
+                const long long need = kl < 0 ? 0 : ceil_div_nn(kl, a.page_size);
+                if (q < 0 || ctx < 0 || npages < 0 || npages > mp || need > npages)
+                    bad = min(bad, b);
+                pages = q > 0 ? need : 0;
+            }
+            const long long iq = cq + wave_scan_incl(q), ik = ck + wave_scan_incl(kl);
+            const long long ip = cp + wave_scan_incl(pages);
+            if (b < B) {
+                if (iq > INT_MAX || ik > INT_MAX || iq > a.max_rows)
+                    bad = min(bad, b);
+                s_cuq[b + 1] = (int32_t)iq;
+                s_cuk[b + 1] = (int32_t)ik;
+            }
+            cq = __shfl(iq, 63, 64);
+            ck = __shfl(ik, 63, 64);
+            cp = __shfl(ip, 63, 64);
+        }
+        long long split = a.split_pages;
+        if (split == 0) {
+            split = (cp + a.target_blocks - 1) / a.target_blocks;
+            if (split < 1)
+                split = 1;
+        }
+        long long cw = 0;
+        for (int base = 0; base < B; base += 64) {
+            const int b = base + lane;
+            long long ns = 0;
+            if (b < B && s_q[b] > 0)
+                ns = ceil_div_nn(ceil_div_nn((long long)s_ctx[b] + s_q[b], a.page_size), split);
+            const long long iw = cw + wave_scan_incl(ns);
+            if (b < B) {
+                if (iw > a.max_work)
+                    bad = min(bad, B + b);  // reported only when the first scan found nothing
+                s_cus[b + 1] = (int32_t)iw;
+            }
+            cw = __shfl(iw, 63, 64);
+        }
+        // First offending session: the row/key/page checks outrank the work-item one.
+        for (int off = 32; off > 0; off >>= 1)
+            bad = min(bad, __shfl_xor(bad, off, 64));
+        if (lane == 0) {
+            if (bad != INT_MAX)
+                atomicMin(&err, bad >= B ? bad - B + (1 << 30) : bad);
+            s_tot[0] = cq;
+            s_tot[1] = ck;
+            s_tot[2] = split;
+            s_tot[3] = cw;
+        }
+    }
+    __syncthreads();
+    if (err != INT_MAX) {
+        write_error(a, err >= (1 << 30) ? err - (1 << 30) : err);
+        return;
+    }
+    const long long total_q = s_tot[0], total_k = s_tot[1], split = s_tot[2];
+    const int W = (int)s_tot[3];
+    // ---- outputs: global stores only from here on ----
+    for (int b = tid; b <= B; b += kMetaThreads) {
+        a.cu_seqlens_q[b] = s_cuq[b];
+        a.cu_seqlens_k[b] = s_cuk[b];
+        a.cu_splits[b] = s_cus[b];
+        if (b < B)
+            a.num_splits[b] = s_cus[b + 1] - s_cus[b];
+    }
+    for (int e = tid; e < entries; e += kMetaThreads)
+        a.page_table[e] = s_pt[e];
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    for (int w = tid; w < a.max_work; w += kMetaThreads) {
+        if (w >= W) {
+            a.work_desc[(long long)w * kWorkDescInts] = -1;
+            continue;
+        }
+        const int b = upper_index(s_cus, B, w);
+        const int sp = w - s_cus[b];
+        const int q = s_q[b], kl = s_ctx[b] + q;
+        const int need = (kl + a.page_size - 1) / a.page_size;
+        const int p0 = (int)(sp * split);
+        const int p1 = (int)(p0 + split < need ? p0 + split : need);
+        a.work_session[w] = b;
+        a.work_split[w] = sp;
+        i32x4* d = reinterpret_cast<i32x4*>(a.work_desc + (long long)w * kWorkDescInts);
+        d[0] = i32x4{b, s_cuq[b], kl, p0};
+        d[1] = i32x4{p1, s_cus[b + 1] - s_cus[b], s_cus[b], q};
+        int32_t pg[kWorkPages];
+#pragma unroll
+        for (int j = 0; j < kWorkPages; ++j)
+            pg[j] = p0 + j < p1 ? s_pt[b * mp + p0 + j] : -1;
+        i32x4* dp = reinterpret_cast<i32x4*>(a.work_pages + (long long)w * kWorkPages);
+        dp[0] = i32x4{pg[0], pg[1], pg[2], pg[3]};
+        dp[1] = i32x4{pg[4], pg[5], pg[6], pg[7]};
+    }
+    for (int i = tid; i < (int)total_q; i += kMetaThreads) {
+        const int b = upper_index(s_cuq, B, i);
+        const int pos = s_ctx[b] + (i - s_cuq[b]);
+        const int page = s_pt[b * mp + pos / a.page_size];
+        a.slot_mapping[i] = (int32_t)(page * (long long)a.page_size + pos % a.page_size);
+    }
+    if (tid == 0) {
+        a.info[0] = W;
+        a.info[1] = (int32_t)split;
+        a.info[2] = (int32_t)total_q;
+        a.info[3] = (int32_t)total_k;
+    }
+}
+
 // One thread per element of the appended rows; RNE rounding to 16 bits.
 template <typename T>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
@@ -319,7 +515,9 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 }  // namespace
 
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream) {
-    if (a.B <= kMetaLdsCap)
+    if (a.B <= kMetaLdsCap && (long long)a.B * a.max_pages <= kMetaSmallPt)
+        hipLaunchKernelGGL(build_metadata_lds_kernel, dim3(1), dim3(kMetaThreads), 0, stream, a);
+    else if (a.B <= kMetaLdsCap)
         hipLaunchKernelGGL(build_metadata_kernel<true>, dim3(1), dim3(kMetaThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(build_metadata_kernel<false>, dim3(1), dim3(kMetaThreads), 0, stream,
