@@ -662,11 +662,39 @@ __global__ __launch_bounds__(64 * kWaves) void g5_kernel(StepArgs s, LayerWeight
 
 // --------------------------------------------------------------------- g7 ----
 // Final RMSNorm + tied logits h . E^T for 64 rows and four 16-column tiles per
-// workgroup (the waves split K four ways and the tiles two ways); each workgroup also
-// leaves, per row, the greedy winner of its 64 columns (strict >, so the lowest index
-// wins ties; banned ids never win) and whether all of them were finite (banned or not:
-// sample_token checks every logit, inference.cpp:352-353).
-constexpr int kG7Tiles = 4, kG7KG = 4;
+// workgroup (the waves split K eight ways: measured 11.7 us at config 3 against 13.1 us
+// for four ways times two tile groups, whose waves each loaded twice the activation
+// rows); each workgroup also leaves, per row, the greedy winner of its 64 columns
+// (strict >, so the lowest index wins ties; banned ids never win) and whether all of
+// them were finite (banned or not: sample_token checks every logit,
+// inference.cpp:352-353).
+constexpr int kG7Tiles = 4, kG7KG = 8;
+
+// Greedy key of a logit: larger value first, then lower column.  The value's bits are
+// mapped to an order-preserving unsigned (after -0 -> +0, which compares equal to it),
+// the column to its complement; 0 marks "no candidate" (every real key is larger).
+__device__ __forceinline__ uint64_t greedy_key(float y, int col) {
+    const uint32_t b = __float_as_uint(y + 0.0f);
+    const uint32_t ord = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint32_t)~(uint32_t)col;
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_shr64(uint64_t v) {  // lanes without a source get 0
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, true);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+// Running maximum along each row of 16 lanes: lane 15 of the row ends with the row's max.
+__device__ __forceinline__ uint64_t row_max16(uint64_t v) {
+    uint64_t t = dpp_shr64<0x111>(v);
+    v = t > v ? t : v;
+    t = dpp_shr64<0x112>(v);
+    v = t > v ? t : v;
+    t = dpp_shr64<0x114>(v);
+    v = t > v ? t : v;
+    t = dpp_shr64<0x118>(v);
+    return t > v ? t : v;
+}
 
 template <int KW>
 __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
@@ -692,16 +720,10 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
     floatx4 v[kG7Tiles];
     if (!splitk_reduce<4, NTW, kG7KG>(acc, part, mt, v))
         return;
-    float bv[4], fin[4];
-    int bc[4];
+    uint64_t best[4] = {0, 0, 0, 0};
+    uint64_t nonfinite[4] = {0, 0, 0, 0};  // 1 when some logit of the row is not finite
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        bv[i] = -INFINITY;
-        bc[i] = 0x7fffffff;
-        fin[i] = 1.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < kG7Tiles; ++j) {  // tiles in increasing column order
+    for (int j = 0; j < kG7Tiles; ++j) {
         const int col = (nt0 + j) * 16 + n;
         const bool valid = nt0 + j < n_tiles && col < m.vocab;
         const bool open = valid && !(s.ban && ((s.ban[col >> 5] >> (col & 31)) & 1u));
@@ -712,31 +734,23 @@ __global__ __launch_bounds__(64 * kWaves) void g7_kernel(StepArgs s) {
             if (valid && row < s.B)
                 s.logits[(long long)row * m.vocab + col] = y;
             if (valid && !isfinite(y))
-                fin[i] = 0.0f;
-            if (open && (bc[i] == 0x7fffffff || y > bv[i])) {  // strict >: lowest column
-                bv[i] = y;
-                bc[i] = col;
-            }
+                nonfinite[i] = 1;
+            const uint64_t k = open ? greedy_key(y, col) : 0;
+            best[i] = k > best[i] ? k : best[i];
         }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        // the 16 lanes of a row hold 16 columns each: larger value, then lower column
-        for (int off = 8; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv[i], off, 16);
-            const int oc = __shfl_xor(bc[i], off, 16);
-            fin[i] = fminf(fin[i], __shfl_xor(fin[i], off, 16));
-            if (oc != 0x7fffffff &&
-                (bc[i] == 0x7fffffff || ov > bv[i] || (ov == bv[i] && oc < bc[i]))) {
-                bv[i] = ov;
-                bc[i] = oc;
-            }
-        }
+        // the 16 lanes of a row hold 16 columns each; lane 15 gathers the row's winner
+        const uint64_t k = row_max16(best[i]);
+        const uint64_t bad = row_max16(nonfinite[i]);
         const int row = row0 + 16 * mt + 4 * g + i;
-        if (n == 0 && row < s.B) {
+        if (n == 15 && row < s.B) {
             const long long idx = (long long)row * gridDim.x + blockIdx.x;
-            s.arg_v[idx] = bv[i];
-            s.arg_c[idx] = fin[i] > 0.0f ? bc[i] : -1;
+            const uint32_t ord = (uint32_t)(k >> 32);
+            const uint32_t b = ord & 0x80000000u ? ord ^ 0x80000000u : ~ord;
+            s.arg_v[idx] = k ? __uint_as_float(b) : -INFINITY;
+            s.arg_c[idx] = bad ? -1 : k ? (int)~(uint32_t)k : 0x7fffffff;
         }
     }
 }
