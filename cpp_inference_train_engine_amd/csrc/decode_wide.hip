@@ -61,7 +61,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     constexpr int CHUNKS = REC / 8;      // 16-byte chunks of a record
     constexpr int LAT_BLOCKS = PS * KV / 512;  // latent 1 KB blocks (the rest is rope)
     constexpr int THREADS = 64 * WAVES;
-    static_assert(REC % 512 == 0, "record blocks");
+    constexpr int kBlocksPerWave = BLOCKS / WAVES;  // page-copy blocks each wave issues
+    static_assert(REC % 512 == 0 && BLOCKS % WAVES == 0, "record blocks");
+    static_assert(kBlocksPerWave <= KS + RS, "a wave's copy blocks fit the first unit's k-steps");
     using V8 = typename T::vec8;
     __shared__ __attribute__((aligned(16))) uint16_t buf0[REC];
     __shared__ __attribute__((aligned(16))) uint16_t buf1[REC];
@@ -83,19 +85,31 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     // reads of two adjacent sub-chunks then hit disjoint banks.  Rope blocks are copied
     // as stored.
     const int lat_src = (lane >> 4) * 128 + ((lane & 15) ^ (((lane >> 4) & 1) << 3)) * 8;
-    auto issue_page_id = [&](int page, uint16_t* dst) {
-        const uint16_t* base =
-            a.pages + (long long)((unsigned)page < (unsigned)a.num_pool_pages ? page : 0) * REC;
-        for (int bk = wave; bk < BLOCKS; bk += WAVES)
-            copy_block_to_lds(base + bk * 512 + (bk < LAT_BLOCKS ? lat_src : lane * 8),
-                              dst + bk * 512);
+    auto page_src = [&](int page) {
+        return a.pages + (long long)((unsigned)page < (unsigned)a.num_pool_pages ? page : 0) * REC;
     };
-    // Page ids come from LDS (staged below), so issuing a page never waits on memory.
-    auto issue_page = [&](int p, uint16_t* dst) {
+    // Block k of this wave's share of a page copy: record block wave + WAVES * k.
+    auto issue_block = [&](const uint16_t* base, uint16_t* dst, int k) {
+        const int bk = wave + WAVES * k;
+        copy_block_to_lds(base + bk * 512 + (bk < LAT_BLOCKS ? lat_src : lane * 8),
+                          dst + bk * 512);
+    };
+    // Page ids come from LDS (staged below) for the item's first kWideMaxItemPages pages.
+    auto page_id = [&](int p) {
         const int i = p - p_begin;
-        issue_page_id(i < kWideMaxItemPages ? pids[i] : ptab[p], dst);
+        int id;
+        if (i < kWideMaxItemPages)
+            id = pids[i];
+        else
+            id = ptab[p];
+        return __builtin_amdgcn_readfirstlane(id);
     };
-    issue_page_id(ptab[p_begin], buf0);  // first page in flight while q and the ids load
+    {  // the first page in flight while q and the ids load
+        const uint16_t* base = page_src(__builtin_amdgcn_readfirstlane(ptab[p_begin]));
+#pragma unroll
+        for (int k = 0; k < kBlocksPerWave; ++k)
+            issue_block(base, buf0, k);
+    }
     for (int i = tid; i < min(p_end - p_begin, kWideMaxItemPages); i += THREADS)
         pids[i] = ptab[p_begin + i];
 
@@ -133,7 +147,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
             acc[rt][ht] = floatx4{0, 0, 0, 0};
     }
 
-    auto compute_page = [&](const uint16_t* pg, int p) {
+    // With has_next, the page after p (record `next`) is copied into `next_dst` one block
+    // per k-step of the first unit's scores, so the copies go out while the wave
+    // computes instead of ahead of it.
+    auto compute_page = [&](const uint16_t* pg, int p, bool has_next, const uint16_t* next,
+                            uint16_t* next_dst) {
         const int valid = min(PS, kl - p * PS);  // >= 1 inside [p_begin, p_end)
         if (valid < PS) {
             // the session's last page: zero the slots past its end (they may hold any bits)
@@ -165,8 +183,16 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
                                     pg + PS * KV + (t * (RP / 8) + 4 * (j - KS)) * 128 + lane * 8);
             };
             V8 kn[2] = {k_operand(0, 0), k_operand(1, 0)};
+            const uint16_t* nsrc = next + wave * 512 + lat_src;
 #pragma unroll
             for (int j = 0; j < KS + RS; ++j) {
+                if (u == 0 && j < kBlocksPerWave && has_next) {
+                    // block wave + WAVES j: latent blocks first, then the rope ones
+                    const int bk = wave + WAVES * j;
+                    copy_block_to_lds(bk < LAT_BLOCKS ? nsrc : nsrc - lat_src + lane * 8,
+                                      next_dst + bk * 512);
+                    nsrc += WAVES * 512;
+                }
                 const V8 k0 = kn[0], k1 = kn[1];
                 if (j + 1 < KS + RS) {
                     kn[0] = k_operand(0, j + 1);
@@ -191,8 +217,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
                         sc[tt][ht][i] = x;
                         mp = fmaxf(mp, x);
                     }
-                mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
-                mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+                mp = rows_max(mp);
                 const float m_new = fmaxf(m_run[ht], mp);
                 if (__ballot(m_new > m_run[ht])) {  // some head's maximum rose
                     const float alpha =
@@ -257,24 +282,23 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     };
 
     // Page p of the item lives in buf0 when (p - p_begin) is even, buf1 when odd.  Each
-    // round: wait for this page's loads, barrier, issue the next page into the other
-    // buffer (its readers finished before the previous barrier), consume, barrier.
+    // round: wait for this wave's copies of page p, barrier (every wave's copies landed,
+    // and every wave is done with page p - 1, whose buffer the copies of page p + 1 now
+    // overwrite), consume page p while issuing page p + 1.
     for (int p = p_begin; p < p_end; ++p) {
         const bool odd = (p - p_begin) & 1;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of page p landed
         __syncthreads();
-        if (p + 1 < p_end)
-            issue_page(p + 1, odd ? buf0 : buf1);
-        compute_page(odd ? buf1 : buf0, p);
-        __syncthreads();
+        const bool has_next = p + 1 < p_end;
+        const uint16_t* next = has_next ? page_src(page_id(p + 1)) : a.pages;
+        compute_page(odd ? buf1 : buf0, p, has_next, next, odd ? buf0 : buf1);
     }
 
     // ---- this wave's heads: final rows (one-item sessions) or split partials ----
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
         float l = l_run[ht];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        l = rows_sum(l);
         const int head = 16 * (HT * wave + ht) + n;
         if (head >= H)
             continue;

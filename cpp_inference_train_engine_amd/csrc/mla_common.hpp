@@ -79,6 +79,41 @@ __device__ inline float wave_sum(float v) {
     return v;
 }
 
+// Max / sum over lanes n, n+16, n+32, n+48 of a wave (its four 16-lane rows), left in
+// every lane.  gfx950's v_permlane16_swap exchanges rows between the row pairs {0,1} and
+// {2,3}, v_permlane32_swap the two 32-lane halves: two VALU swaps instead of two LDS
+// permute round trips.  Each stage combines the two rows of a pair, so the result is
+// the one __shfl_xor(., 16) then __shfl_xor(., 32) gives (max and + are commutative).
+// Every lane of the wave must be active.
+// (The swap results are copied out element by element: a __builtin_bit_cast of an
+// element of the returned vector reads element 0 in this toolchain.)
+__device__ __forceinline__ void swap_rows16(float x, float& a, float& b) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    a = __uint_as_float(r0);
+    b = __uint_as_float(r1);
+}
+__device__ __forceinline__ void swap_halves32(float x, float& a, float& b) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const unsigned r0 = r[0], r1 = r[1];
+    a = __uint_as_float(r0);
+    b = __uint_as_float(r1);
+}
+__device__ __forceinline__ float rows_max(float x) {
+    float a, b;
+    swap_rows16(x, a, b);
+    swap_halves32(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    float a, b;
+    swap_rows16(x, a, b);
+    swap_halves32(a + b, a, b);
+    return a + b;
+}
+
 }  // namespace mla
 
 namespace mla {
