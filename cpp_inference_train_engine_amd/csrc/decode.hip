@@ -212,8 +212,7 @@ void decode_page_kernel(DecodeArgs a) {
                 sc[t][i] = x;
                 mp = fmaxf(mp, x);
             }
-        mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
-        mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+        mp = rows_max(mp);
         if (m_run == -INFINITY) {
             m_run = mp;  // first page of this wave: nothing accumulated yet
         } else if (__ballot(mp > m_run)) {
@@ -296,8 +295,7 @@ void decode_page_kernel(DecodeArgs a) {
         }
     }
     __builtin_amdgcn_s_setprio(0);
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = rows_sum(l_run);
 
     // ---- merge the WAVES softmax states of this work item in LDS ----
     // Each wave parks its unscaled state in its own unit tile (its 16 x MSTRIDE floats fit

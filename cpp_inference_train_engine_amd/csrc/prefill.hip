@@ -229,8 +229,7 @@ void prefill_page_kernel(PrefillArgs a) {
             // sum.  Each lane checks its own scores, so the row max (a cross-lane
             // reduction) is formed only on the rare pages that raise the reference.
             if (__builtin_amdgcn_ballot_w64(mp * a.scale_log2 > m_run[q] + kPfRescale)) {
-                mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
-                mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+                mp = rows_max(mp);
                 const float m_new = fmaxf(m_run[q], mp * a.scale_log2);
                 const float alpha = exp2_fast(m_run[q] - m_new);
                 l_run[q] *= alpha;
@@ -291,8 +290,7 @@ void prefill_page_kernel(PrefillArgs a) {
     // ---- the two token halves of each q-group meet in LDS; normalise and store ----
 #pragma unroll
     for (int q = 0; q < QT; ++q) {
-        l_run[q] += __shfl_xor(l_run[q], 16, 64);
-        l_run[q] += __shfl_xor(l_run[q], 32, 64);
+        l_run[q] = rows_sum(l_run[q]);
     }
     __syncthreads();  // every wave is done with the page buffers
     static_assert((QT * RT * 256 + QT * 128) * 4 <= REC * 2, "exchange fits a page buffer");
