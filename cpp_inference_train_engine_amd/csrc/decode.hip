@@ -61,12 +61,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
-__device__ __forceinline__ void wave_lds_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // decode_page_kernel -- one workgroup of WAVES waves per work item (session, split);
 // wave v owns pages p_begin+v, p_begin+v+WAVES, ... of the item and issues ALL loads
 // of a page (PS tokens, TILED record: every 16-byte lane load reads 1 KB

@@ -40,15 +40,6 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
-// One wave copies 1 KB from global to LDS: lane l's 16 bytes (from its own `src`)
-// land at dst + 16 l bytes.
-__device__ __forceinline__ void copy_block_to_lds(const uint16_t* src, uint16_t* dst) {
-    __builtin_amdgcn_global_load_lds(
-        (const void*)src,
-        (__attribute__((address_space(3))) void*)((__attribute__((address_space(3))) char*)dst),
-        16, 0, 0);
-}
-
 template <typename T, int KV, int RP, int PS, int HT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     static_assert(KV % 32 == 0 && RP % 32 == 0 && PS % 32 == 0, "tile shape");
@@ -77,7 +68,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
     const int H = a.H;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int32_t* ptab = a.page_table + (long long)s * a.max_pages;
 
     // Latent blocks land in LDS with odd 256-byte sub-chunks rotated by 8 token rows
@@ -89,9 +80,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
         return a.pages + (long long)((unsigned)page < (unsigned)a.num_pool_pages ? page : 0) * REC;
     };
     // Block k of this wave's share of a page copy: record block wave + WAVES * k.
+    const uint32_t lat_off = 2 * lat_src, rope_off_b = 16 * lane;  // lane byte offsets
     auto issue_block = [&](const uint16_t* base, uint16_t* dst, int k) {
         const int bk = wave + WAVES * k;
-        copy_block_to_lds(base + bk * 512 + (bk < LAT_BLOCKS ? lat_src : lane * 8),
+        copy_block_to_lds(base + bk * 512, bk < LAT_BLOCKS ? lat_off : rope_off_b,
                           dst + bk * 512);
     };
     // Page ids come from LDS (staged below) for the item's first kWideMaxItemPages pages.
@@ -183,16 +175,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
                                     pg + PS * KV + (t * (RP / 8) + 4 * (j - KS)) * 128 + lane * 8);
             };
             V8 kn[2] = {k_operand(0, 0), k_operand(1, 0)};
-            const uint16_t* nsrc = next + wave * 512 + lat_src;
 #pragma unroll
             for (int j = 0; j < KS + RS; ++j) {
-                if (u == 0 && j < kBlocksPerWave && has_next) {
-                    // block wave + WAVES j: latent blocks first, then the rope ones
-                    const int bk = wave + WAVES * j;
-                    copy_block_to_lds(bk < LAT_BLOCKS ? nsrc : nsrc - lat_src + lane * 8,
-                                      next_dst + bk * 512);
-                    nsrc += WAVES * 512;
-                }
+                if (u == 0 && j < kBlocksPerWave && has_next)
+                    issue_block(next, next_dst, j);
                 const V8 k0 = kn[0], k1 = kn[1];
                 if (j + 1 < KS + RS) {
                     kn[0] = k_operand(0, j + 1);

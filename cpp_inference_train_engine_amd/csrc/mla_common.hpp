@@ -114,6 +114,41 @@ __device__ __forceinline__ float rows_sum(float x) {
     return a + b;
 }
 
+// One wave copies 1 KB from global memory to LDS: lane l's 16 bytes, read at
+// base + off bytes (base uniform, off the lane's own), land at dst + 16 l bytes (gfx950
+// global_load_lds_dwordx4 in its scalar-base form; the LDS address goes in M0, which no
+// other code here uses).  Written as inline assembly so that the compiler, which cannot
+// tell which LDS bytes such a copy writes, does not wait for every copy in flight before
+// each later LDS access (it did, before the first transpose read after a prefetch).
+// The copy counts in vmcnt: the caller waits for it (s_waitcnt vmcnt) and orders its
+// LDS reads after the wait (wave_lds_fence or a barrier) before reading what it wrote.
+// Any vmcnt wait of the compiler's own (for a global load, or a register reload) also
+// waits for the copies issued before it, so the copies go out after such loads.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void copy_block_to_lds(const void* base, uint32_t off, void* dst) {
+    // readfirstlane returns int: each half goes through uint32_t before widening (a
+    // sign-extended low half would set the upper 32 bits of the address).
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane((uint32_t)b));
+    const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
+    const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)dst));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(m0), "v"(off), "s"(reinterpret_cast<const void*>(sb))
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Orders this wave's LDS accesses: nothing before it moves after it, or after it before.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace mla
 
 namespace mla {

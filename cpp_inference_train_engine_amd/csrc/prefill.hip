@@ -53,26 +53,30 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
 
 constexpr float kPfNoMax = -1.0e30f;  // running-max floor: below every real score
 constexpr float kPfRescale = 8.0f;    // log2 headroom before the running max is raised
-constexpr int kPfQG = 2;        // q-groups per workgroup (QT 16-row tiles each)
-constexpr int kPfKH = 2;        // token halves: the two waves of a q-group split each page
-constexpr int kPfWaves = kPfQG * kPfKH;
-constexpr int kPfMaxIds = 2048;  // page ids staged in LDS: sessions up to 2048 pages
+constexpr int kPfWaves = 4;           // waves per workgroup, each streaming its own units
+constexpr int kPfQT = 2;              // 16-row q-tiles per workgroup (shared by its waves)
+constexpr int kPfUnit = 32;           // tokens per unit (two 16-token tiles)
+constexpr int kPfMaxIds = 512;        // page ids staged in LDS (later pages: page table)
 
-template <typename T, int KV, int RP, int PS, int QT>
+template <typename T, int KV, int RP, int PS>
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void prefill_page_kernel(PrefillArgs a) {
-    static_assert(KV % 32 == 0 && RP % 8 == 0 && RP <= 32 && PS == 64, "tile shape");
-    constexpr int KS = KV / 32;               // latent k-steps of the score MFMAs
-    constexpr int RT = KV / 16;               // 16-row (latent) tiles of O^T
-    constexpr int REC = PS * (KV + RP);       // words of a page record
-    constexpr int CHUNKS = REC / 8;           // 16-byte chunks of a record
-    constexpr int THREADS = 64 * kPfWaves;
-    constexpr int CPT = (CHUNKS + THREADS - 1) / THREADS;  // chunks per thread and page
-    constexpr int WG_ROWS = kPfQG * QT * 16;
+    static_assert(KV % 32 == 0 && RP % 8 == 0 && RP <= 32 && PS % kPfUnit == 0, "tile shape");
+    constexpr int QT = kPfQT;
+    constexpr int KS = KV / 32;                // latent k-steps of the score MFMAs
+    constexpr int RT = KV / 16;                // 16-row (latent) tiles of O^T
+    constexpr int LAT_BLOCKS = 2 * KS;         // 1 KB latent blocks of a unit (two tiles)
+    constexpr int ROPE_WORDS = 2 * 16 * RP;    // rope words of a unit
+    static_assert(ROPE_WORDS == 512, "a unit's rope keys fill one 1 KB block");
+    constexpr int UBLOCKS = LAT_BLOCKS + 1;    // 1 KB blocks of a unit
+    constexpr int UREC = UBLOCKS * 512;        // words of a unit
+    constexpr int UPP = PS / kPfUnit;          // units per page
+    constexpr int WG_ROWS = QT * 16;
     using V8 = typename T::vec8;
-    __shared__ __attribute__((aligned(16))) uint16_t buf0[REC];
-    __shared__ __attribute__((aligned(16))) uint16_t buf1[REC];
-    __shared__ int32_t pids[kPfMaxIds];
+    // Unit ring of each wave: even units of its stream in slot0, odd ones in slot1.
+    __shared__ __attribute__((aligned(16))) uint16_t slot0[kPfWaves][UREC];
+    __shared__ __attribute__((aligned(16))) uint16_t slot1[kPfWaves][UREC];
+    __shared__ int32_t pids[kPfMaxIds];  // the session's first page ids
 
     const int b = blockIdx.y;
     if (a.info[0] <= 0)
@@ -87,67 +91,53 @@ void prefill_page_kernel(PrefillArgs a) {
         return;
     const int ctx = k_len - q_len;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
-    const int wave = tid >> 6, qg = wave >> 1, kh = wave & 1;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // keys [0, k_hi) are visible to some q-row of this workgroup
     const int last_q = min(n_rows - 1, rb + WG_ROWS - 1) / H;
     const int k_hi = ctx + last_q + 1;
-    const int n_pages = (k_hi + PS - 1) / PS;
+    const int n_units = (k_hi + kPfUnit - 1) / kPfUnit;
     const int32_t* ptab = a.page_table + (long long)b * a.max_pages;
+    const long long rec = (long long)PS * (KV + RP);
 
-    // ---- page staging: 16-byte chunks through registers, slots at or past k_len zeroed.
-    // One register set holds page p+1 while page p is consumed from LDS (a second set
-    // holding p+2 as well measured no faster and cost 20 VGPRs).
-    // Raw buffer loads over the page record: a chunk that must read as zero (slot at or
-    // past k_len, an invalid page id, or p >= n_pages) gets an offset outside the record,
-    // which the hardware returns as zero.  Every load is issued unconditionally, so no
-    // register merges (and no early waits) appear between the loads and their use.
-    auto load_page = [&](u32x4 (&st)[CPT], int page_id, int p) {
-        const int page = __builtin_amdgcn_readfirstlane(page_id);  // uniform: scalar rsrc
-        const bool ok = (unsigned)page < (unsigned)a.num_pool_pages && p < n_pages;
-        const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(a.pages + (long long)(ok ? page : 0) * REC), 0, REC * 2,
-            0x00020000);
-        const int valid = ok ? k_len - p * PS : 0;  // slots of the page that hold keys
-#pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int c = tid + k * THREADS;
-            bool live = c < CHUNKS && valid > 0;
-            if (valid < PS) {  // the session's last page (or nothing to load)
-                // slot of chunk c: latent chunks run (t, j, g, n), rope chunks (t, ch, n)
-                const int slot = c < PS * KV / 8 ? (c / (16 * 4 * KS)) * 16 + (c & 15)
-                                                 : ((c - PS * KV / 8) / (16 * (RP / 8))) * 16 +
-                                                       (c & 15);
-                live = live && slot < valid;
-            }
-            st[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  rsrc, live ? c * 16 : 0x40000000, 0, 0));
-        }
+    // The wave's units: wave, wave + kPfWaves, ...  Unit u is half u % UPP of page u / UPP:
+    // its latent is the LAT_BLOCKS contiguous blocks from block LAT_BLOCKS * (u % UPP) of
+    // the record, its rope keys the 1 KB at PS*KV + ROPE_WORDS * (u % UPP).  A unit of an
+    // invalid page id is not copied (it is zeroed in LDS instead).
+    const int n_pages = (n_units + UPP - 1) / UPP;
+    auto page_of = [&](int u) {
+        const int pg = u / UPP;
+        int id;
+        if (pg < kPfMaxIds)
+            id = pids[pg];
+        else
+            id = ptab[pg];
+        return __builtin_amdgcn_readfirstlane(id);
     };
-    auto store_page = [&](const u32x4 (&st)[CPT], uint16_t* dst) {
+    auto issue_unit = [&](int u, int page, uint16_t* dst) {
+        if ((unsigned)page >= (unsigned)a.num_pool_pages)
+            return false;
+        const uint16_t* base = a.pages + page * rec;
+        const int h = u % UPP;
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int c = tid + k * THREADS;
-            if (c < CHUNKS)
-                *reinterpret_cast<u32x4*>(dst + c * 8) = st[k];
-        }
+        for (int k = 0; k < LAT_BLOCKS; ++k)
+            copy_block_to_lds(base + (LAT_BLOCKS * h + k) * 512, 16 * lane, dst + k * 512);
+        copy_block_to_lds(base + PS * KV + ROPE_WORDS * h, 16 * lane, dst + LAT_BLOCKS * 512);
+        return true;
     };
-    // Prologue, in issue order: the page ids (staged in LDS, so issuing a later page
-    // never waits on memory), the Q operands, then the first two pages.
-    const int id0 = ptab[0];
-    constexpr int IDS_PT = kPfMaxIds / THREADS;
-    int ids[IDS_PT];
-#pragma unroll
-    for (int k = 0; k < IDS_PT; ++k) {
-        const int i = tid + k * THREADS;
-        ids[k] = i < n_pages ? ptab[i] : 0;
-    }
-    const int wr0 = rb + qg * QT * 16;  // first session q-row of the wave
+
+    // ---- Q^T operands of the workgroup's q-rows (every wave holds all of them) ----
     V8 qv[QT][KS + 1];
     int lim[QT];  // lane's q-row n sees keys [0, lim]; -1 = no such row
     const bool rope_lane = 8 * g < RP;
+    int u = wave;  // this wave's current unit
+    int page_cur = u < n_units ? __builtin_amdgcn_readfirstlane(ptab[u / UPP]) : 0;
+    if (u < n_units)
+        issue_unit(u, page_cur, slot0[wave]);
+    for (int i = tid; i < min(n_pages, kPfMaxIds); i += 64 * kPfWaves)
+        pids[i] = ptab[i];
 #pragma unroll
     for (int q = 0; q < QT; ++q) {
-        const int r = wr0 + q * 16 + n;
+        const int r = rb + q * 16 + n;
         const bool valid = r < n_rows;
         lim[q] = valid ? ctx + r / H : -1;
         const long long fr = (long long)q0 * H + r;  // flat (row, head) index
@@ -159,20 +149,19 @@ void prefill_page_kernel(PrefillArgs a) {
                         ? *reinterpret_cast<const V8*>(a.q_rope + fr * RP + 8 * g)
                         : V8{};
     }
-    u32x4 st0[CPT];
-    load_page(st0, id0, 0);
-#pragma unroll
-    for (int k = 0; k < IDS_PT; ++k)
-        pids[tid + k * THREADS] = ids[k];
-    store_page(st0, buf0);
-    __syncthreads();
+    // The first unit and the q operands landed (an explicit wait: the compiler does not
+    // see the unit copies, and would otherwise wait for the q loads inside the loop,
+    // where that wait would also hold back on the next unit's copies).
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();                     // the staged page ids
+    int page_nxt = u + kPfWaves < n_units ? page_of(u + kPfWaves) : 0;
     const int rope_off = (16 * (rope_lane ? g : g % (RP / 8)) + n) * 8;
     // transpose-read address of lane (g, j=n) inside a token tile: token 4g + n/4,
     // latent 4*(n%4) + (row-tile offset)
     const int tr_lane = (((n & 3) >> 1) * 128) + (4 * g + (n >> 2)) * 8 + 4 * (n & 1);
+    // The lowest causal limit of the workgroup's rows (-1 when some row is past the chunk).
+    const int lim_min = rb + WG_ROWS <= n_rows ? ctx + rb / H : -1;
 
-    // The lowest causal limit of the wave's rows (-1 when some row is past the chunk).
-    const int lim_min = wr0 + QT * 16 <= n_rows ? ctx + wr0 / H : -1;
     float m_run[QT], l_run[QT];
     floatx4 acc[QT][RT];
 #pragma unroll
@@ -184,50 +173,52 @@ void prefill_page_kernel(PrefillArgs a) {
             acc[q][rt] = floatx4{0, 0, 0, 0};
     }
 
-    // Scores, mask, online softmax and PV of this wave's token half of page p.
-    auto compute = [&](const uint16_t* pg, int p) {
-        const int tok0 = p * PS + 32 * kh;
+    // Scores, mask, online softmax and PV of unit u (in LDS at sp).
+    auto compute = [&](const uint16_t* sp, int uu) {
+        const int tok0 = uu * kPfUnit;
         floatx4 sc[2][QT];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            const int t = 2 * kh + tt;
 #pragma unroll
             for (int q = 0; q < QT; ++q)
                 sc[tt][q] = floatx4{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
-                const V8 ka = *reinterpret_cast<const V8*>(pg + (t * KS + j) * 512 + lane * 8);
+                const V8 ka = *reinterpret_cast<const V8*>(sp + (tt * KS + j) * 512 + lane * 8);
 #pragma unroll
                 for (int q = 0; q < QT; ++q)
                     sc[tt][q] = T::mma32(ka, qv[q][j], sc[tt][q]);
             }
-            const V8 kr =
-                *reinterpret_cast<const V8*>(pg + PS * KV + t * (RP / 8) * 128 + rope_off);
+            const V8 kr = *reinterpret_cast<const V8*>(sp + LAT_BLOCKS * 512 + tt * 16 * RP +
+                                                        rope_off);
 #pragma unroll
             for (int q = 0; q < QT; ++q)
                 sc[tt][q] = T::mma32(kr, qv[q][KS], sc[tt][q]);
         }
-        V8 pb[QT], pl[QT];  // P^T operands (pl: the low part, bf16 only)
-        // Every row of the wave sees all 32 tokens of this half unless it holds the
+        // Every row of the workgroup sees all 32 tokens of this unit unless it holds the
         // causal edge (or rows past the chunk): only then are tokens masked.
-        const bool full = tok0 + 31 <= lim_min;
+        if (!(tok0 + kPfUnit - 1 <= lim_min)) {
+#pragma unroll
+            for (int q = 0; q < QT; ++q)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (tok0 + 16 * tt + 4 * g + i > lim[q])
+                            sc[tt][q][i] = -INFINITY;
+        }
+        V8 pb[QT], pl[QT];  // P^T operands (pl: the low part, bf16 only)
 #pragma unroll
         for (int q = 0; q < QT; ++q) {
-            float mp = -INFINITY;  // this lane's max, raw score units (the scale is > 0)
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (!full && tok0 + 16 * tt + 4 * g + i > lim[q])
-                        sc[tt][q][i] = -INFINITY;
-                    mp = fmaxf(mp, sc[tt][q][i]);
-                }
+            // this lane's max, raw score units (the scale is > 0)
+            float mp = fmaxf(fmaxf(fmaxf(sc[0][q][0], sc[0][q][1]), fmaxf(sc[0][q][2], sc[0][q][3])),
+                             fmaxf(fmaxf(sc[1][q][0], sc[1][q][1]), fmaxf(sc[1][q][2], sc[1][q][3])));
             // log2 units; m_run starts at a finite floor, so exp2 never sees inf - inf.
             // The reference max m_run is raised only when a score exceeds it by more than
             // kPfRescale; below that the probabilities are exp2(x - m_run) <= 2^kPfRescale,
             // exact in fp32 and fp16, and the final normalisation divides by the same-based
             // sum.  Each lane checks its own scores, so the row max (a cross-lane
-            // reduction) is formed only on the rare pages that raise the reference.
+            // reduction) is formed only on the rare units that raise the reference.
             if (__builtin_amdgcn_ballot_w64(mp * a.scale_log2 > m_run[q] + kPfRescale)) {
                 mp = rows_max(mp);
                 const float m_new = fmaxf(m_run[q], mp * a.scale_log2);
@@ -254,12 +245,12 @@ void prefill_page_kernel(PrefillArgs a) {
                 }
             l_run[q] += psum;  // per lane; summed over the 4 lane groups at the end
         }
-        // O^T += C^T . P^T over the 32 tokens of this half (one K-step)
+        // O^T += C^T . P^T over the unit's 32 tokens (one K-step per 16 latent rows)
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
             const int blk = ((rt >> 1) * 4 + 2 * (rt & 1)) * 128;  // latent rows 16rt..
-            const u32x2 lo = lds_read_tr16(pg + (2 * kh) * KS * 512 + blk + tr_lane);
-            const u32x2 hi = lds_read_tr16(pg + (2 * kh + 1) * KS * 512 + blk + tr_lane);
+            const u32x2 lo = lds_read_tr16(sp + blk + tr_lane);
+            const u32x2 hi = lds_read_tr16(sp + KS * 512 + blk + tr_lane);
             const V8 ca = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
             for (int q = 0; q < QT; ++q) {
@@ -269,69 +260,99 @@ void prefill_page_kernel(PrefillArgs a) {
             }
         }
     };
-    // Page p lives in buf[p % 2]; its successor waits in the registers st0.  One step:
-    // load page p+1 into the registers, consume page p, store page p+1 into the other
-    // buffer (its last readers finished before the previous barrier), barrier.  Steps
-    // are unrolled in pairs so every buffer is named statically.
-    auto step = [&](const uint16_t* cur, uint16_t* nx, int p) {
-        load_page(st0, pids[min(p + 1, n_pages - 1)], p + 1);
-        compute(cur, p);
-        if (p + 1 < n_pages)
-            store_page(st0, nx);
-        __syncthreads();
+    // Tokens of unit uu at or past k_len, or the whole unit when its page id is invalid,
+    // read as zero: the unit's chunks are cleared in LDS (chunk c of block k holds token
+    // 16 * (k / KS) + c % 16 of a latent block, 16 * (c / 32) + c % 16 of the rope block).
+    auto clear_tail = [&](uint16_t* sp, int uu, int page) {
+        const int valid = (unsigned)page < (unsigned)a.num_pool_pages ? k_len - uu * kPfUnit : 0;
+        if (valid >= kPfUnit)
+            return;
+#pragma unroll
+        for (int k = 0; k < UBLOCKS; ++k) {
+            const int tok = k < LAT_BLOCKS ? 16 * (k / KS) + n : 16 * (lane >> 5) + n;
+            if (tok >= valid)
+                *reinterpret_cast<u32x4*>(sp + k * 512 + lane * 8) = u32x4{0, 0, 0, 0};
+        }
+        wave_lds_fence();
     };
-    for (int p = 0; p < n_pages; p += 2) {
-        step(buf0, buf1, p);
-        if (p + 1 >= n_pages)
-            break;
-        step(buf1, buf0, p + 1);
+
+    // The wave's stream: unit u sits in slot (i & 1) for its i-th unit; the copy of the
+    // next unit goes out before this one is consumed.  Only this wave touches its slots,
+    // so no workgroup barrier is needed until the final merge.
+    for (int i = 0; u < n_units; ++i, u += kPfWaves) {
+        uint16_t* cur = (i & 1) ? slot1[wave] : slot0[wave];
+        uint16_t* nxt = (i & 1) ? slot0[wave] : slot1[wave];
+        const bool more = u + kPfWaves < n_units;
+        const int page_after = u + 2 * kPfWaves < n_units ? page_of(u + 2 * kPfWaves) : 0;
+        if (more && issue_unit(u + kPfWaves, page_nxt, nxt))
+            __builtin_amdgcn_s_waitcnt(0x0F70 | UBLOCKS);  // vmcnt(UBLOCKS): the next unit's
+                                                           // copies may still be in flight
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        wave_lds_fence();
+        clear_tail(cur, u, page_cur);
+        compute(cur, u);
+        page_cur = page_nxt;
+        page_nxt = page_after;
+        wave_lds_fence();  // this slot's reads are done before the next copy into it
     }
 
-    // ---- the two token halves of each q-group meet in LDS; normalise and store ----
+    // ---- the waves' softmax states meet in LDS; normalise and store ----
 #pragma unroll
-    for (int q = 0; q < QT; ++q) {
+    for (int q = 0; q < QT; ++q)
         l_run[q] = rows_sum(l_run[q]);
-    }
-    __syncthreads();  // every wave is done with the page buffers
-    static_assert((QT * RT * 256 + QT * 128) * 4 <= REC * 2, "exchange fits a page buffer");
-    float* xo = reinterpret_cast<float*>(qg == 0 ? buf0 : buf1);
-    if (kh == 1) {
+    __syncthreads();  // every wave is done with its slots
+    // per wave: acc [QT][RT][64 lanes] floatx4, then m and l of its 32 rows
+    constexpr int XO = QT * RT * 64 * 4;
+    static_assert((XO + 2 * WG_ROWS) * 4 <= UREC * 2 * 2, "a wave's state fits its two slots");
+    auto xo_of = [&](int v) {
+        return reinterpret_cast<float*>(v < 2 ? &slot0[2 * v][0] : &slot1[2 * (v - 2)][0]);
+    };
+    {
+        float* xo = xo_of(wave);
 #pragma unroll
         for (int q = 0; q < QT; ++q) {
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
                 *reinterpret_cast<floatx4*>(xo + ((q * RT + rt) * 64 + lane) * 4) = acc[q][rt];
             if (g == 0) {
-                xo[QT * RT * 256 + q * 128 + n] = m_run[q];
-                xo[QT * RT * 256 + q * 128 + 64 + n] = l_run[q];
+                xo[XO + q * 16 + n] = m_run[q];
+                xo[XO + WG_ROWS + q * 16 + n] = l_run[q];
             }
         }
     }
     __syncthreads();
-    if (kh == 1)
-        return;
+    // thread t: q-row r = t / RT (of the workgroup's 32), latent rows 16 rt .. 16 rt + 15
+    static_assert(WG_ROWS * RT == 64 * kPfWaves, "one thread per (row, latent tile)");
+    const int r = tid / RT, rt = tid % RT;
+    const int q = r / 16, rn = r % 16;
+    float mv[kPfWaves], M = kPfNoMax;
 #pragma unroll
-    for (int q = 0; q < QT; ++q) {
-        const float m1 = xo[QT * RT * 256 + q * 128 + n];
-        const float l1 = xo[QT * RT * 256 + q * 128 + 64 + n];
-        const float M = fmaxf(m_run[q], m1);
-        const float f0 = exp2_fast(m_run[q] - M), f1 = exp2_fast(m1 - M);
-        const float l = l_run[q] * f0 + l1 * f1;
-        const int r = wr0 + q * 16 + n;
-        if (r >= n_rows)
-            continue;
-        const long long fr = (long long)q0 * H + r;
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            const floatx4 o1 =
-                *reinterpret_cast<const floatx4*>(xo + ((q * RT + rt) * 64 + lane) * 4);
-            *reinterpret_cast<floatx4*>(a.out + fr * KV + 16 * rt + 4 * g) =
-                (acc[q][rt] * f0 + o1 * f1) * inv;
-        }
-        if (a.lse && g == 0)
-            a.lse[fr] = (M + __log2f(l)) * kLn2;
+    for (int v = 0; v < kPfWaves; ++v) {
+        mv[v] = xo_of(v)[XO + r];
+        M = fmaxf(M, mv[v]);
     }
+    float L = 0.0f;
+    floatx4 o[4] = {};
+#pragma unroll
+    for (int v = 0; v < kPfWaves; ++v) {
+        const float* xo = xo_of(v);
+        const float f = exp2_fast(mv[v] - M);
+        L += xo[XO + WG_ROWS + r] * f;
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+            o[gg] += *reinterpret_cast<const floatx4*>(xo + ((q * RT + rt) * 64 + gg * 16 + rn) * 4) * f;
+    }
+    const int row = rb + r;
+    if (row >= n_rows)
+        return;
+    const long long fr = (long long)q0 * H + row;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg)
+        *reinterpret_cast<floatx4*>(a.out + fr * KV + 16 * rt + 4 * gg) = o[gg] * inv;
+    if (a.lse && rt == 0)
+        a.lse[fr] = (M + __log2f(L)) * kLn2;
 }
 
 // ------------------------------------------------------------- generic ----
@@ -438,16 +459,11 @@ __global__ __launch_bounds__(kPgThreads) void prefill_generic_kernel(PrefillArgs
         a.lse[fr] = (m_run + __log2f(l_run)) * kLn2;
 }
 
-// One 16-row tile per q-group: 32 q-rows per workgroup, 138 VGPRs, three workgroups per
-// CU (four, at 124 VGPRs and 1024 staged page ids, measured slower: 62.3 us).  Twice as many workgroups as two tiles would give (measured on config 4: 55.7 us
-// against 62.4 us), so the dispatcher can even out the sessions' unequal key ranges.
-constexpr int kPfQT = 1;
-
 template <typename T>
 hipError_t launch_prefill_page(const PrefillArgs& a, int max_q_len, hipStream_t stream) {
-    constexpr int rows = kPfQG * kPfQT * 16;
+    constexpr int rows = kPfQT * 16;
     const long long gx = ((long long)max_q_len * a.H + rows - 1) / rows;
-    hipLaunchKernelGGL((prefill_page_kernel<T, 128, 16, 64, kPfQT>), dim3((unsigned)gx, a.B),
+    hipLaunchKernelGGL((prefill_page_kernel<T, 128, 16, 64>), dim3((unsigned)gx, a.B),
                        dim3(64 * kPfWaves), 0, stream, a);
     return hipGetLastError();
 }
@@ -458,17 +474,12 @@ bool prefill_mfma_supported(int H, int kv_rank, int rope_dim, int page_size) {
     return H <= 16 && page_size == 64 && kv_rank == 128 && rope_dim == 16;
 }
 
-// The MFMA kernel stages a session's page ids in LDS (at most kPfMaxIds pages).
-static bool prefill_mfma_fits(const PrefillArgs& a) {
-    return prefill_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size) &&
-           a.max_pages <= kPfMaxIds;
-}
 
 hipError_t launch_prefill(const PrefillArgs& a, int max_q_len, int dtype, bool force_generic,
                           hipStream_t stream) {
     if (a.B <= 0 || max_q_len < 2)
         return hipSuccess;
-    if (!force_generic && prefill_mfma_fits(a))
+    if (!force_generic && prefill_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size))
         return dtype == 0 ? launch_prefill_page<F16>(a, max_q_len, stream)
                           : launch_prefill_page<BF16>(a, max_q_len, stream);
     const size_t shmem = (a.kv_rank + a.rope_dim + kPgChunk + 8) * sizeof(float);
