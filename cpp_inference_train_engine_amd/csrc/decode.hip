@@ -468,10 +468,11 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
 }
 
 // --------------------------------------------------------------- merge ----
-// Log-sum-exp combine of a session's split partials (log2 domain), one workgroup per
-// session.  The session's metadata comes in one batch of loads; each thread then owns
-// V consecutive columns of one head and keeps kMergeUnroll splits' partials in flight,
-// folding them into a running (max, sum, o) so nothing waits on a global reduction.
+// Log-sum-exp combine of a session's split partials (log2 domain).  Workgroup (s, y)
+// owns kMergeThreads consecutive (head, V-column) elements of session s, one per
+// thread.  The session's metadata comes in one batch of loads; each thread then folds
+// the splits in order into a running (max, sum, o), kMergeUnroll splits per round, the
+// next round's partials in flight while this round is folded.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeUnroll = 8;
 
@@ -484,37 +485,53 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
     if (built <= 0 || row_end - row != 1 || ns <= 1 || w0 < 0 || w0 + ns > a.max_work)
         return;  // failed build, not a decode row, or nothing to combine
     const int H = a.H, KV = a.kv_rank, per_head = KV / V;
-    for (int e = threadIdx.x; e < H * per_head; e += kMergeThreads) {
-        const int h = e / per_head, c = (e % per_head) * V;
-        float M = -INFINITY, L = 0.0f;
-        vecV O = {};
-        for (int i0 = 0; i0 < ns; i0 += kMergeUnroll) {
-            float mi[kMergeUnroll], li[kMergeUnroll];
-            vecV oi[kMergeUnroll];
+    const int e = blockIdx.y * kMergeThreads + threadIdx.x;
+    if (e >= H * per_head)
+        return;
+    const int h = e / per_head, c = (e % per_head) * V;
+    float M = -INFINITY, L = 0.0f;
+    vecV O = {};
+    auto load = [&](int i0, float (&mi)[kMergeUnroll], float (&li)[kMergeUnroll],
+                    vecV (&oi)[kMergeUnroll]) {
 #pragma unroll
-            for (int k = 0; k < kMergeUnroll; ++k) {
-                const long long idx = (long long)(w0 + min(i0 + k, ns - 1)) * H + h;
-                mi[k] = a.part_ml[idx * 2];
-                li[k] = a.part_ml[idx * 2 + 1];
-                oi[k] = *reinterpret_cast<const vecV*>(a.part_o + idx * KV + c);
-            }
-#pragma unroll
-            for (int k = 0; k < kMergeUnroll; ++k) {
-                if (i0 + k >= ns || mi[k] == -INFINITY)
-                    continue;  // past the last split, or a split with no tokens
-                const float Mn = fmaxf(M, mi[k]);
-                const float sa = M == -INFINITY ? 0.0f : exp2_fast(M - Mn);
-                const float sb = exp2_fast(mi[k] - Mn);
-                L = L * sa + li[k] * sb;
-                O = O * sa + oi[k] * sb;
-                M = Mn;
-            }
+        for (int k = 0; k < kMergeUnroll; ++k) {
+            const long long idx = (long long)(w0 + min(i0 + k, ns - 1)) * H + h;
+            mi[k] = a.part_ml[idx * 2];
+            li[k] = a.part_ml[idx * 2 + 1];
+            oi[k] = *reinterpret_cast<const vecV*>(a.part_o + idx * KV + c);
         }
-        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-        *reinterpret_cast<vecV*>(a.out + ((long long)row * H + h) * KV + c) = O * inv;
-        if (a.lse && c == 0)
-            a.lse[(long long)row * H + h] = (M + __log2f(L)) * kLn2;
+    };
+    auto fold = [&](int i0, const float (&mi)[kMergeUnroll], const float (&li)[kMergeUnroll],
+                    const vecV (&oi)[kMergeUnroll]) {
+#pragma unroll
+        for (int k = 0; k < kMergeUnroll; ++k) {
+            if (i0 + k >= ns || mi[k] == -INFINITY)
+                continue;  // past the last split, or a split with no tokens
+            const float Mn = fmaxf(M, mi[k]);
+            const float sa = M == -INFINITY ? 0.0f : exp2_fast(M - Mn);
+            const float sb = exp2_fast(mi[k] - Mn);
+            L = L * sa + li[k] * sb;
+            O = O * sa + oi[k] * sb;
+            M = Mn;
+        }
+    };
+    float ma[kMergeUnroll], la[kMergeUnroll], mb[kMergeUnroll], lb[kMergeUnroll];
+    vecV oa[kMergeUnroll], ob[kMergeUnroll];
+    load(0, ma, la, oa);
+    for (int i0 = 0; i0 < ns; i0 += 2 * kMergeUnroll) {
+        if (i0 + kMergeUnroll < ns)
+            load(i0 + kMergeUnroll, mb, lb, ob);
+        fold(i0, ma, la, oa);
+        if (i0 + kMergeUnroll >= ns)
+            break;
+        if (i0 + 2 * kMergeUnroll < ns)
+            load(i0 + 2 * kMergeUnroll, ma, la, oa);
+        fold(i0 + kMergeUnroll, mb, lb, ob);
     }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    *reinterpret_cast<vecV*>(a.out + ((long long)row * H + h) * KV + c) = O * inv;
+    if (a.lse && c == 0)
+        a.lse[(long long)row * H + h] = (M + __log2f(L)) * kLn2;
 }
 
 // Waves per work item of decode_page_kernel; the metadata's split_pages should match
@@ -570,10 +587,12 @@ hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
     const bool vec4 = a.kv_rank % 4 == 0 &&
                       ((reinterpret_cast<uintptr_t>(a.out) | reinterpret_cast<uintptr_t>(a.part_o)) &
                        15) == 0;
+    const int per_session = a.H * (a.kv_rank / (vec4 ? 4 : 1));  // elements of a row
+    const dim3 grid(a.B, (per_session + kMergeThreads - 1) / kMergeThreads);
     if (vec4)
-        hipLaunchKernelGGL(merge_kernel<4>, dim3(a.B), dim3(kMergeThreads), 0, stream, a);
+        hipLaunchKernelGGL(merge_kernel<4>, grid, dim3(kMergeThreads), 0, stream, a);
     else
-        hipLaunchKernelGGL(merge_kernel<1>, dim3(a.B), dim3(kMergeThreads), 0, stream, a);
+        hipLaunchKernelGGL(merge_kernel<1>, grid, dim3(kMergeThreads), 0, stream, a);
     return hipGetLastError();
 }
 
