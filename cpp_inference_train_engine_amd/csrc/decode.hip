@@ -469,65 +469,89 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
 
 // --------------------------------------------------------------- merge ----
 // Log-sum-exp combine of a session's split partials (log2 domain).  Workgroup (s, y)
-// owns kMergeThreads consecutive (head, V-column) elements of session s, one per
-// thread.  The session's metadata comes in one batch of loads; each thread then folds
-// the splits in order into a running (max, sum, o), kMergeUnroll splits per round, the
-// next round's partials in flight while this round is folded.
-constexpr int kMergeThreads = 256;
+// owns kMergeElems consecutive (head, V-column) elements of session s.  Its
+// kMergeGroups thread groups take one element per thread each and split the session's
+// splits into kMergeGroups consecutive ranges: each thread folds its range in order into
+// a running (max, sum, o), kMergeUnroll splits per round with the next round's partials
+// in flight, and the groups' states are then folded in group order through LDS (a
+// session with 64 splits needs two rounds per thread, not eight).
+constexpr int kMergeElems = 256;
+constexpr int kMergeGroups = 4;
+constexpr int kMergeThreads = kMergeElems * kMergeGroups;
 constexpr int kMergeUnroll = 8;
 
 template <int V>
 __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
     typedef float vecV __attribute__((ext_vector_type(V)));
+    __shared__ float sm_m[kMergeGroups][kMergeElems], sm_l[kMergeGroups][kMergeElems];
+    __shared__ vecV sm_o[kMergeGroups][kMergeElems];
     const int s = blockIdx.x;
     const int built = a.info[0], row = a.cu_q[s], row_end = a.cu_q[s + 1];
     const int ns = a.num_splits[s], w0 = a.cu_splits[s];
     if (built <= 0 || row_end - row != 1 || ns <= 1 || w0 < 0 || w0 + ns > a.max_work)
         return;  // failed build, not a decode row, or nothing to combine
     const int H = a.H, KV = a.kv_rank, per_head = KV / V;
-    const int e = blockIdx.y * kMergeThreads + threadIdx.x;
-    if (e >= H * per_head)
-        return;
-    const int h = e / per_head, c = (e % per_head) * V;
+    const int grp = threadIdx.x / kMergeElems, t = threadIdx.x % kMergeElems;
+    const int e = blockIdx.y * kMergeElems + t;
+    const bool live = e < H * per_head;
+    const int h = live ? e / per_head : 0, c = live ? (e % per_head) * V : 0;
+    // this group's splits [i_lo, i_hi)
+    const int i_lo = ns * grp / kMergeGroups, i_hi = ns * (grp + 1) / kMergeGroups;
     float M = -INFINITY, L = 0.0f;
     vecV O = {};
     auto load = [&](int i0, float (&mi)[kMergeUnroll], float (&li)[kMergeUnroll],
                     vecV (&oi)[kMergeUnroll]) {
 #pragma unroll
         for (int k = 0; k < kMergeUnroll; ++k) {
-            const long long idx = (long long)(w0 + min(i0 + k, ns - 1)) * H + h;
+            const long long idx = (long long)(w0 + min(i0 + k, i_hi - 1)) * H + h;
             mi[k] = a.part_ml[idx * 2];
             li[k] = a.part_ml[idx * 2 + 1];
             oi[k] = *reinterpret_cast<const vecV*>(a.part_o + idx * KV + c);
         }
     };
+    auto fold1 = [&](float mk, float lk, vecV ok) {
+        if (mk == -INFINITY)
+            return;  // a split (or group) with no tokens
+        const float Mn = fmaxf(M, mk);
+        const float sa = M == -INFINITY ? 0.0f : exp2_fast(M - Mn);
+        const float sb = exp2_fast(mk - Mn);
+        L = L * sa + lk * sb;
+        O = O * sa + ok * sb;
+        M = Mn;
+    };
     auto fold = [&](int i0, const float (&mi)[kMergeUnroll], const float (&li)[kMergeUnroll],
                     const vecV (&oi)[kMergeUnroll]) {
 #pragma unroll
-        for (int k = 0; k < kMergeUnroll; ++k) {
-            if (i0 + k >= ns || mi[k] == -INFINITY)
-                continue;  // past the last split, or a split with no tokens
-            const float Mn = fmaxf(M, mi[k]);
-            const float sa = M == -INFINITY ? 0.0f : exp2_fast(M - Mn);
-            const float sb = exp2_fast(mi[k] - Mn);
-            L = L * sa + li[k] * sb;
-            O = O * sa + oi[k] * sb;
-            M = Mn;
-        }
+        for (int k = 0; k < kMergeUnroll; ++k)
+            if (i0 + k < i_hi)
+                fold1(mi[k], li[k], oi[k]);
     };
-    float ma[kMergeUnroll], la[kMergeUnroll], mb[kMergeUnroll], lb[kMergeUnroll];
-    vecV oa[kMergeUnroll], ob[kMergeUnroll];
-    load(0, ma, la, oa);
-    for (int i0 = 0; i0 < ns; i0 += 2 * kMergeUnroll) {
-        if (i0 + kMergeUnroll < ns)
-            load(i0 + kMergeUnroll, mb, lb, ob);
-        fold(i0, ma, la, oa);
-        if (i0 + kMergeUnroll >= ns)
-            break;
-        if (i0 + 2 * kMergeUnroll < ns)
-            load(i0 + 2 * kMergeUnroll, ma, la, oa);
-        fold(i0 + kMergeUnroll, mb, lb, ob);
+    if (live && i_lo < i_hi) {
+        float ma[kMergeUnroll], la[kMergeUnroll], mb[kMergeUnroll], lb[kMergeUnroll];
+        vecV oa[kMergeUnroll], ob[kMergeUnroll];
+        load(i_lo, ma, la, oa);
+        for (int i0 = i_lo; i0 < i_hi; i0 += 2 * kMergeUnroll) {
+            if (i0 + kMergeUnroll < i_hi)
+                load(i0 + kMergeUnroll, mb, lb, ob);
+            fold(i0, ma, la, oa);
+            if (i0 + kMergeUnroll >= i_hi)
+                break;
+            if (i0 + 2 * kMergeUnroll < i_hi)
+                load(i0 + 2 * kMergeUnroll, ma, la, oa);
+            fold(i0 + kMergeUnroll, mb, lb, ob);
+        }
     }
+    if (grp > 0) {
+        sm_m[grp][t] = M;
+        sm_l[grp][t] = L;
+        sm_o[grp][t] = O;
+    }
+    __syncthreads();
+    if (grp > 0 || !live)
+        return;
+#pragma unroll
+    for (int q = 1; q < kMergeGroups; ++q)
+        fold1(sm_m[q][t], sm_l[q][t], sm_o[q][t]);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     *reinterpret_cast<vecV*>(a.out + ((long long)row * H + h) * KV + c) = O * inv;
     if (a.lse && c == 0)
@@ -588,7 +612,7 @@ hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
                       ((reinterpret_cast<uintptr_t>(a.out) | reinterpret_cast<uintptr_t>(a.part_o)) &
                        15) == 0;
     const int per_session = a.H * (a.kv_rank / (vec4 ? 4 : 1));  // elements of a row
-    const dim3 grid(a.B, (per_session + kMergeThreads - 1) / kMergeThreads);
+    const dim3 grid(a.B, (per_session + kMergeElems - 1) / kMergeElems);
     if (vec4)
         hipLaunchKernelGGL(merge_kernel<4>, grid, dim3(kMergeThreads), 0, stream, a);
     else
