@@ -155,6 +155,7 @@ void prefill_page_kernel(PrefillArgs a) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();                     // the staged page ids
     int page_nxt = u + kPfWaves < n_units ? page_of(u + kPfWaves) : 0;
+    const float inv_scale = 1.0f / a.scale_log2;
     const int rope_off = (16 * (rope_lane ? g : g % (RP / 8)) + n) * 8;
     // transpose-read address of lane (g, j=n) inside a token tile: token 4g + n/4,
     // latent 4*(n%4) + (row-tile offset)
@@ -210,23 +211,34 @@ void prefill_page_kernel(PrefillArgs a) {
         V8 pb[QT], pl[QT];  // P^T operands (pl: the low part, bf16 only)
 #pragma unroll
         for (int q = 0; q < QT; ++q) {
-            // this lane's max, raw score units (the scale is > 0)
-            float mp = fmaxf(fmaxf(fmaxf(sc[0][q][0], sc[0][q][1]), fmaxf(sc[0][q][2], sc[0][q][3])),
-                             fmaxf(fmaxf(sc[1][q][0], sc[1][q][1]), fmaxf(sc[1][q][2], sc[1][q][3])));
             // log2 units; m_run starts at a finite floor, so exp2 never sees inf - inf.
             // The reference max m_run is raised only when a score exceeds it by more than
             // kPfRescale; below that the probabilities are exp2(x - m_run) <= 2^kPfRescale,
             // exact in fp32 and fp16, and the final normalisation divides by the same-based
-            // sum.  Each lane checks its own scores, so the row max (a cross-lane
-            // reduction) is formed only on the rare units that raise the reference.
-            if (__builtin_amdgcn_ballot_w64(mp * a.scale_log2 > m_run[q] + kPfRescale)) {
+            // sum.  Each lane compares its own raw scores with the threshold (the scale is
+            // > 0), so the row max (a cross-lane reduction) is formed only on the rare
+            // units that raise the reference, and the accumulators are rescaled only when
+            // a row that has accumulated something is raised.
+            const float thr = (m_run[q] + kPfRescale) * inv_scale;
+            bool rise = false;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    rise |= sc[tt][q][i] > thr;
+            if (__builtin_amdgcn_ballot_w64(rise)) {
+                float mp = fmaxf(fmaxf(fmaxf(sc[0][q][0], sc[0][q][1]), fmaxf(sc[0][q][2], sc[0][q][3])),
+                                 fmaxf(fmaxf(sc[1][q][0], sc[1][q][1]), fmaxf(sc[1][q][2], sc[1][q][3])));
                 mp = rows_max(mp);
                 const float m_new = fmaxf(m_run[q], mp * a.scale_log2);
-                const float alpha = exp2_fast(m_run[q] - m_new);
-                l_run[q] *= alpha;
+                const bool had = m_run[q] != kPfNoMax;  // the row has accumulated state
+                if (__builtin_amdgcn_ballot_w64(had && m_new > m_run[q])) {
+                    const float alpha = exp2_fast(m_run[q] - m_new);
+                    l_run[q] *= alpha;
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
-                    acc[q][rt] *= alpha;
+                    for (int rt = 0; rt < RT; ++rt)
+                        acc[q][rt] *= alpha;
+                }
                 m_run[q] = m_new;
             }
             const float m_ref = m_run[q];
