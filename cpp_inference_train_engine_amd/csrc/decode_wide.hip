@@ -30,6 +30,8 @@ namespace mla {
 namespace {
 
 constexpr int kWideMaxItemPages = 512;  // page ids of an item staged in LDS
+constexpr float kWideNoMax = -1.0e30f;  // running-max floor: below every real score
+constexpr float kWideRescale = 8.0f;    // log2 headroom before the running max is raised
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     floatx4 acc[RT][HT];
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) {
-        m_run[ht] = -INFINITY;
+        m_run[ht] = kWideNoMax;
         l_run[ht] = 0.0f;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
@@ -193,7 +195,14 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
             V8 pb[HT], pl[HT];
 #pragma unroll
             for (int ht = 0; ht < HT; ++ht) {
-                float mp = -INFINITY;
+                // log2 units.  The reference max m_run (from a finite floor) is raised only
+                // when a score passes it by more than kWideRescale: below that the
+                // probabilities are at most 2^kWideRescale (exact in fp32, and the bf16
+                // hi + lo split is relative), and the partial (m, l, o) is consistent for
+                // any reference.  Each lane compares its own scores, so the row max (a
+                // cross-lane reduction) is formed only on the units that raise it, and the
+                // accumulators are rescaled only when a head with accumulated state is.
+                bool rise = false;
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -201,17 +210,24 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
                         const int slot = 32 * u + 16 * tt + 4 * g + i;
                         const float x = slot < valid ? sc[tt][ht][i] * a.scale_log2 : -INFINITY;
                         sc[tt][ht][i] = x;
-                        mp = fmaxf(mp, x);
+                        rise |= x > m_run[ht] + kWideRescale;
                     }
-                mp = rows_max(mp);
-                const float m_new = fmaxf(m_run[ht], mp);
-                if (__ballot(m_new > m_run[ht])) {  // some head's maximum rose
-                    const float alpha =
-                        m_run[ht] == -INFINITY ? 0.0f : exp2_fast(m_run[ht] - m_new);
-                    l_run[ht] *= alpha;
+                if (__ballot(rise)) {
+                    float mp = -INFINITY;
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt)
-                        acc[rt][ht] *= alpha;
+                    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            mp = fmaxf(mp, sc[tt][ht][i]);
+                    const float m_new = fmaxf(m_run[ht], rows_max(mp));
+                    const bool had = m_run[ht] != kWideNoMax;  // the head has accumulated
+                    if (__ballot(had && m_new > m_run[ht])) {
+                        const float alpha = exp2_fast(m_run[ht] - m_new);
+                        l_run[ht] *= alpha;
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt)
+                            acc[rt][ht] *= alpha;
+                    }
                     m_run[ht] = m_new;
                 }
                 float psum = 0.0f;
@@ -219,8 +235,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
                 for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float e =
-                            m_run[ht] == -INFINITY ? 0.0f : exp2_fast(sc[tt][ht][i] - m_run[ht]);
+                        const float e = exp2_fast(sc[tt][ht][i] - m_run[ht]);
                         psum += e;
                         const auto hi = static_cast<typename T::scalar>(e);
                         pb[ht][4 * tt + i] = hi;
