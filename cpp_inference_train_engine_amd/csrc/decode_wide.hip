@@ -32,6 +32,11 @@ namespace {
 constexpr int kWideMaxItemPages = 512;  // page ids of an item staged in LDS
 constexpr float kWideNoMax = -1.0e30f;  // running-max floor: below every real score
 constexpr float kWideRescale = 8.0f;    // log2 headroom before the running max is raised
+// Latent token rows of odd 256-byte sub-chunks sit at slot row ^ kWideRot in LDS.  With 12
+// the transpose reads of the two sub-chunks of a pair fall in disjoint banks: measured at
+// config 5, SQ_LDS_BANK_CONFLICT is 0 cycles per dispatch (168.6 M with 0, 1, 2, 3 or 8;
+// 337 M with 4).
+constexpr int kWideRot = 12;
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -73,11 +78,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int32_t* ptab = a.page_table + (long long)s * a.max_pages;
 
-    // Latent blocks land in LDS with odd 256-byte sub-chunks rotated by 8 token rows
-    // (lane l of the copy fetches the chunk that belongs at LDS slot l): the transpose
-    // reads of two adjacent sub-chunks then hit disjoint banks.  Rope blocks are copied
-    // as stored.
-    const int lat_src = (lane >> 4) * 128 + ((lane & 15) ^ (((lane >> 4) & 1) << 3)) * 8;
+    // Latent blocks land in LDS with the token rows of odd 256-byte sub-chunks permuted
+    // (row ^ kWideRot; lane l of the copy fetches the chunk that belongs at LDS slot l):
+    // the transpose reads of two adjacent sub-chunks then hit disjoint banks.  Rope blocks
+    // are copied as stored.
+    const int lat_src = (lane >> 4) * 128 + ((lane & 15) ^ (((lane >> 4) & 1) * kWideRot)) * 8;
     auto page_src = [&](int page) {
         return a.pages + (long long)((unsigned)page < (unsigned)a.num_pool_pages ? page : 0) * REC;
     };
@@ -124,11 +129,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
                 ok ? *reinterpret_cast<const V8*>(a.q_rope + q * RP + 32 * j + 8 * g) : V8{};
     }
     // transpose-read address of lane (g, n) in a 16-token tile: sub-chunk parity
-    // (n & 3) >> 1 (odd sub-chunks rotated by 8 rows), token 4g + n/4, half n & 1
+    // (n & 3) >> 1 (odd sub-chunks: rows permuted by ^ kWideRot), token 4g + n/4, half n & 1
     const int tr_par = (n & 3) >> 1;
-    const int tr_lane = tr_par * 128 + ((4 * g + (n >> 2)) ^ (tr_par << 3)) * 8 + 4 * (n & 1);
+    const int tr_lane = tr_par * 128 + ((4 * g + (n >> 2)) ^ (tr_par * kWideRot)) * 8 + 4 * (n & 1);
     // score A-operand read of lane (g, n): sub-chunk g, token n
-    const int s_lane = g * 128 + (n ^ ((g & 1) << 3)) * 8;
+    const int s_lane = g * 128 + (n ^ ((g & 1) * kWideRot)) * 8;
 
     float m_run[HT], l_run[HT];
     floatx4 acc[RT][HT];
@@ -153,7 +158,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
             for (int c = tid; c < CHUNKS; c += THREADS) {
                 const int slot =
                     c < PS * KV / 8
-                        ? (c / (16 * 4 * KS)) * 16 + ((c & 15) ^ ((((c >> 4) & 1)) << 3))
+                        ? (c / (16 * 4 * KS)) * 16 + ((c & 15) ^ (((c >> 4) & 1) * kWideRot))
                         : ((c - PS * KV / 8) / (16 * (RP / 8))) * 16 + (c & 15);
                 if (slot >= valid)
                     *reinterpret_cast<u32x4*>(wpg + c * 8) = u32x4{0, 0, 0, 0};

@@ -57,6 +57,10 @@ constexpr int kPfWaves = 4;           // waves per workgroup, each streaming its
 constexpr int kPfQT = 2;              // 16-row q-tiles per workgroup (shared by its waves)
 constexpr int kPfUnit = 32;           // tokens per unit (two 16-token tiles)
 constexpr int kPfMaxIds = 512;        // page ids staged in LDS (later pages: page table)
+// Latent token rows of odd 256-byte sub-chunks sit at slot row ^ kPfRot in LDS, which puts
+// the transpose reads of a sub-chunk pair in disjoint banks (the decode_wide_kernel
+// measurement: 0 conflict cycles with 12, 168.6 M per config-5 dispatch as stored).
+constexpr int kPfRot = 12;
 
 template <typename T, int KV, int RP, int PS>
 __global__ __launch_bounds__(64 * kPfWaves) __attribute__((amdgpu_waves_per_eu(2, 8)))
@@ -113,6 +117,9 @@ void prefill_page_kernel(PrefillArgs a) {
             id = ptab[pg];
         return __builtin_amdgcn_readfirstlane(id);
     };
+    // lane l of a latent copy fetches the chunk of LDS slot l: sub-chunk l / 16, token row
+    // (l % 16) ^ kPfRot in odd sub-chunks (byte offset in the 1 KB block)
+    const uint32_t lat_off = 2 * ((lane >> 4) * 128 + ((lane & 15) ^ (((lane >> 4) & 1) * kPfRot)) * 8);
     auto issue_unit = [&](int u, int page, uint16_t* dst) {
         if ((unsigned)page >= (unsigned)a.num_pool_pages)
             return false;
@@ -120,7 +127,7 @@ void prefill_page_kernel(PrefillArgs a) {
         const int h = u % UPP;
 #pragma unroll
         for (int k = 0; k < LAT_BLOCKS; ++k)
-            copy_block_to_lds(base + (LAT_BLOCKS * h + k) * 512, 16 * lane, dst + k * 512);
+            copy_block_to_lds(base + (LAT_BLOCKS * h + k) * 512, lat_off, dst + k * 512);
         copy_block_to_lds(base + PS * KV + ROPE_WORDS * h, 16 * lane, dst + LAT_BLOCKS * 512);
         return true;
     };
@@ -157,9 +164,12 @@ void prefill_page_kernel(PrefillArgs a) {
     int page_nxt = u + kPfWaves < n_units ? page_of(u + kPfWaves) : 0;
     const float inv_scale = 1.0f / a.scale_log2;
     const int rope_off = (16 * (rope_lane ? g : g % (RP / 8)) + n) * 8;
-    // transpose-read address of lane (g, j=n) inside a token tile: token 4g + n/4,
-    // latent 4*(n%4) + (row-tile offset)
-    const int tr_lane = (((n & 3) >> 1) * 128) + (4 * g + (n >> 2)) * 8 + 4 * (n & 1);
+    // transpose-read address of lane (g, j=n) inside a token tile: token 4g + n/4 (its row
+    // permuted in odd sub-chunks), latent 4*(n%4) + (row-tile offset)
+    const int tr_par = (n & 3) >> 1;
+    const int tr_lane = tr_par * 128 + ((4 * g + (n >> 2)) ^ (tr_par * kPfRot)) * 8 + 4 * (n & 1);
+    // score A-operand read of lane (g, n): sub-chunk g, token n
+    const int s_lane = g * 128 + (n ^ ((g & 1) * kPfRot)) * 8;
     // The lowest causal limit of the workgroup's rows (-1 when some row is past the chunk).
     const int lim_min = rb + WG_ROWS <= n_rows ? ctx + rb / H : -1;
 
@@ -185,7 +195,7 @@ void prefill_page_kernel(PrefillArgs a) {
                 sc[tt][q] = floatx4{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
-                const V8 ka = *reinterpret_cast<const V8*>(sp + (tt * KS + j) * 512 + lane * 8);
+                const V8 ka = *reinterpret_cast<const V8*>(sp + (tt * KS + j) * 512 + s_lane);
 #pragma unroll
                 for (int q = 0; q < QT; ++q)
                     sc[tt][q] = T::mma32(ka, qv[q][j], sc[tt][q]);
@@ -274,14 +284,16 @@ void prefill_page_kernel(PrefillArgs a) {
     };
     // Tokens of unit uu at or past k_len, or the whole unit when its page id is invalid,
     // read as zero: the unit's chunks are cleared in LDS (chunk c of block k holds token
-    // 16 * (k / KS) + c % 16 of a latent block, 16 * (c / 32) + c % 16 of the rope block).
+    // 16 * (k / KS) + ((c % 16) ^ kPfRot when c / 16 is odd) of a latent block, and
+    // 16 * (c / 32) + c % 16 of the rope block).
     auto clear_tail = [&](uint16_t* sp, int uu, int page) {
         const int valid = (unsigned)page < (unsigned)a.num_pool_pages ? k_len - uu * kPfUnit : 0;
         if (valid >= kPfUnit)
             return;
 #pragma unroll
         for (int k = 0; k < UBLOCKS; ++k) {
-            const int tok = k < LAT_BLOCKS ? 16 * (k / KS) + n : 16 * (lane >> 5) + n;
+            const int tok = k < LAT_BLOCKS ? 16 * (k / KS) + (n ^ ((g & 1) * kPfRot))
+                                           : 16 * (lane >> 5) + n;
             if (tok >= valid)
                 *reinterpret_cast<u32x4*>(sp + k * 512 + lane * 8) = u32x4{0, 0, 0, 0};
         }
