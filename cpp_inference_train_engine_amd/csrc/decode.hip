@@ -469,22 +469,24 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
 
 // --------------------------------------------------------------- merge ----
 // Log-sum-exp combine of a session's split partials (log2 domain).  Workgroup (s, y)
-// owns kMergeElems consecutive (head, V-column) elements of session s.  Its
-// kMergeGroups thread groups take one element per thread each and split the session's
-// splits into kMergeGroups consecutive ranges: each thread folds its range in order into
-// a running (max, sum, o), kMergeUnroll splits per round with the next round's partials
-// in flight, and the groups' states are then folded in group order through LDS (a
-// session with 64 splits needs two rounds per thread, not eight).
+// owns kMergeElems consecutive (head, V-column) elements of session s.  Its G thread
+// groups take one element per thread each and split the session's splits into G
+// consecutive ranges: each thread folds its range in order into a running (max, sum, o),
+// kMergeUnroll splits per round with the next round's partials in flight, and the
+// groups' states are then folded in group order through LDS.  G = 4 for small batches of
+// many splits per session (config 3: ~9 splits, one round per thread instead of two); G =
+// 1 when the batch has many elements (config 5: 256 sessions x 16 K elements, ~3 splits
+// each), where workgroups of 256 threads fit eight to a CU and the launch runs in a
+// quarter of the rounds (measured at config 5: 262 us per call with G = 4).
 constexpr int kMergeElems = 256;
-constexpr int kMergeGroups = 4;
-constexpr int kMergeThreads = kMergeElems * kMergeGroups;
 constexpr int kMergeUnroll = 8;
+constexpr long long kMergeGroupedMax = 512LL * kMergeElems;  // elements of a batch for G = 4
 
-template <int V>
-__global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
+template <int V, int G>
+__global__ __launch_bounds__(kMergeElems* G) void merge_kernel(DecodeArgs a) {
     typedef float vecV __attribute__((ext_vector_type(V)));
-    __shared__ float sm_m[kMergeGroups][kMergeElems], sm_l[kMergeGroups][kMergeElems];
-    __shared__ vecV sm_o[kMergeGroups][kMergeElems];
+    __shared__ float sm_m[G][kMergeElems], sm_l[G][kMergeElems];
+    __shared__ vecV sm_o[G][kMergeElems];
     const int s = blockIdx.x;
     const int built = a.info[0], row = a.cu_q[s], row_end = a.cu_q[s + 1];
     const int ns = a.num_splits[s], w0 = a.cu_splits[s];
@@ -496,7 +498,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
     const bool live = e < H * per_head;
     const int h = live ? e / per_head : 0, c = live ? (e % per_head) * V : 0;
     // this group's splits [i_lo, i_hi)
-    const int i_lo = ns * grp / kMergeGroups, i_hi = ns * (grp + 1) / kMergeGroups;
+    const int i_lo = ns * grp / G, i_hi = ns * (grp + 1) / G;
     float M = -INFINITY, L = 0.0f;
     vecV O = {};
     auto load = [&](int i0, float (&mi)[kMergeUnroll], float (&li)[kMergeUnroll],
@@ -550,7 +552,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_kernel(DecodeArgs a) {
     if (grp > 0 || !live)
         return;
 #pragma unroll
-    for (int q = 1; q < kMergeGroups; ++q)
+    for (int q = 1; q < G; ++q)
         fold1(sm_m[q][t], sm_l[q][t], sm_o[q][t]);
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     *reinterpret_cast<vecV*>(a.out + ((long long)row * H + h) * KV + c) = O * inv;
@@ -613,10 +615,15 @@ hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream) {
                        15) == 0;
     const int per_session = a.H * (a.kv_rank / (vec4 ? 4 : 1));  // elements of a row
     const dim3 grid(a.B, (per_session + kMergeElems - 1) / kMergeElems);
-    if (vec4)
-        hipLaunchKernelGGL(merge_kernel<4>, grid, dim3(kMergeThreads), 0, stream, a);
+    const bool grouped = (long long)a.B * per_session <= kMergeGroupedMax;
+    if (vec4 && grouped)
+        hipLaunchKernelGGL((merge_kernel<4, 4>), grid, dim3(kMergeElems * 4), 0, stream, a);
+    else if (vec4)
+        hipLaunchKernelGGL((merge_kernel<4, 1>), grid, dim3(kMergeElems), 0, stream, a);
+    else if (grouped)
+        hipLaunchKernelGGL((merge_kernel<1, 4>), grid, dim3(kMergeElems * 4), 0, stream, a);
     else
-        hipLaunchKernelGGL(merge_kernel<1>, grid, dim3(kMergeThreads), 0, stream, a);
+        hipLaunchKernelGGL((merge_kernel<1, 1>), grid, dim3(kMergeElems), 0, stream, a);
     return hipGetLastError();
 }
 
