@@ -33,7 +33,7 @@ class HipEngine:
         h = C.c_void_p()
         check(lib().mla_engine_create(C.byref(cfg), params.ctypes.data, max_sessions, max_rows,
                                       num_pages, page_size, C.byref(h)))
-        self._h = h
+        self._lib, self._h = lib(), h
 
     @classmethod
     def load(cls, path: str, max_sessions: int = 16, max_rows: int = 1024,
@@ -45,7 +45,7 @@ class HipEngine:
         h = C.c_void_p()
         check(lib().mla_engine_load(os.fsencode(path), max_sessions, max_rows, num_pages,
                                     page_size, C.byref(self.cfg), C.byref(h)))
-        self._h = h
+        self._lib, self._h = lib(), h
         return self
 
     @property
@@ -59,7 +59,7 @@ class HipEngine:
         for dependent in list(getattr(self, "_dependents", ())):
             dependent.close()
         if getattr(self, "_h", None):
-            lib().mla_engine_destroy(self._h)
+            self._lib.mla_engine_destroy(self._h)  # kept at creation (interpreter exit)
             self._h = None
 
     def _attach(self, dependent) -> None:

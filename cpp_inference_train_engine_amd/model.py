@@ -89,7 +89,7 @@ class HipModel:
         h = C.c_void_p()
         check(lib().mla_model_create(C.byref(cfg), params.ctypes.data, max_batch, page_size,
                                      C.byref(h)))
-        self._h = h
+        self._lib, self._h = lib(), h
 
     @classmethod
     def load(cls, path: str, max_batch: int, page_size: int = 64) -> "HipModel":
@@ -99,7 +99,7 @@ class HipModel:
         h = C.c_void_p()
         check(lib().mla_model_load(os.fsencode(path), max_batch, page_size, C.byref(self.cfg),
                                    C.byref(h)))
-        self._h = h
+        self._lib, self._h = lib(), h
         return self
 
     def update_weights(self, params) -> int:
@@ -114,8 +114,10 @@ class HipModel:
         return rev.value
 
     def close(self):
+        # The library handle kept at creation: at interpreter exit the package's
+        # globals may already be cleared when this runs.
         if getattr(self, "_h", None):
-            lib().mla_model_destroy(self._h)
+            self._lib.mla_model_destroy(self._h)
             self._h = None
 
     def __del__(self):

@@ -54,6 +54,7 @@ class Scheduler:
         self._cv = threading.Condition()
         self._active, self._closing = 0, False
         check(lib().mla_scheduler_create(engine.handle, tokenizer._h, C.byref(c), C.byref(h)))
+        self._lib = lib()  # used by close(), which may run at interpreter exit
         self._h, self.engine, self.tokenizer = h, engine, tokenizer
         self.max_new_tokens = max_new_tokens
         engine._attach(self)  # closing the engine stops this scheduler first
@@ -84,11 +85,11 @@ class Scheduler:
             if not h or self._closing:
                 return
             self._closing = True
-        lib().mla_scheduler_stop(h)
+        self._lib.mla_scheduler_stop(h)
         with cv:
             cv.wait_for(lambda: self._active == 0)
             self._h = None
-        lib().mla_scheduler_destroy(h)
+        self._lib.mla_scheduler_destroy(h)
 
     def __del__(self):
         self.close()

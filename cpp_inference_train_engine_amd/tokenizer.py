@@ -22,7 +22,7 @@ class HipTokenizer:
     def __init__(self, path: str):
         h = C.c_void_p()
         check(lib().mla_tokenizer_load(os.fsencode(path), C.byref(h)))
-        self._h = h
+        self._lib, self._h = lib(), h
         vocab = C.c_int()
         digest = C.create_string_buffer(65)
         check(lib().mla_tokenizer_info(h, C.byref(vocab), digest))
@@ -31,7 +31,7 @@ class HipTokenizer:
 
     def close(self):
         if getattr(self, "_h", None):
-            lib().mla_tokenizer_destroy(self._h)
+            self._lib.mla_tokenizer_destroy(self._h)  # kept at creation (interpreter exit)
             self._h = None
 
     def __del__(self):
