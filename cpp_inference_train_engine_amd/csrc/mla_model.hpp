@@ -80,9 +80,10 @@ hipError_t model_kernel_attributes(const ModelDims& m);
 hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t st);
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
                             hipStream_t st);  // qkv_kernel (which appends to `pool`)
-// next_norm: attn_norm of the next layer, or final_norm after the last one
+// next_norm: attn_norm of the next layer, or final_norm after the last one; next: the
+// next layer's weights (their qkv blocks are prefetched into L2), or null
 hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const float* next_norm,
-                             hipStream_t st);
+                             const LayerWeights* next, hipStream_t st);
 hipError_t launch_logits(const StepArgs& s, hipStream_t st);
 // Row b < B of (xw_out, ss_out) = row cu_q[b+1]-1 of (s.xw, s.ss_x) for the B sessions
 // of cu_q; rows [B, round_up(B, 64)) are zeroed.  s describes the forward's rows.

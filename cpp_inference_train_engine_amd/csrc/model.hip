@@ -53,6 +53,37 @@ __device__ __forceinline__ V8 to_half8(floatx4 a, floatx4 b) {
               (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
 }
 
+// ---- L2 prefetch for the next kernel on the stream -------------------------------------
+// Workgroup b of a launch (x-fastest linear id) runs on XCD b % 8: the dispatcher deals
+// workgroups to the 8 XCDs in turn.  Each XCD has its own L2, which keeps its lines across
+// kernel boundaries, while the attention's page stream evicts every layer's weights from
+// it.  So the kernel that runs before a weight-latency-bound one touches, from each XCD,
+// the 1 KB weight blocks that the next kernel's workgroups on that XCD will read; the next
+// kernel's grid is padded to a multiple of 8 columns, so that each of its column tiles runs
+// on one fixed XCD.  The loads go straight to a scratch block of LDS (global_load_lds: no
+// VGPR is written behind the compiler's back), issued by the split-K waves that have handed
+// their partial sums over and have nothing left to do: issued any earlier, the compiler's
+// waits for the kernel's own operands would wait for them too (vmcnt retires in order),
+// which measured slower than no prefetch.  A different placement only costs the prefetch
+// its effect, never a result.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int block_xcd() {
+    return (int)((blockIdx.y * gridDim.x + blockIdx.x) % kXcds);
+}
+
+// Blocks [0, n) of this XCD's list (block k at addr(k)), spread over waves
+// [first, blockDim/64) of all of this launch's workgroups on the XCD.
+template <typename F>
+__device__ __forceinline__ void l2_prefetch(int n, F&& addr, uint16_t* scratch, int first) {
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x, total = gridDim.x * gridDim.y;
+    const int x = lin % kXcds, wgs = (total - x + kXcds - 1) / kXcds;
+    const int nw = (blockDim.x >> 6) - first, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) - first;
+    for (int k = (lin / kXcds) * nw + wave; k < n; k += wgs * nw)
+        copy_block_to_lds(addr(k), lane * 16, scratch);
+}
+
 // Sum over the 16 lanes of an MFMA output row group (lanes with equal g hold the same
 // rows, one column each).
 __device__ __forceinline__ float sum16(float v) {
@@ -332,6 +363,8 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     __shared__ float inv_x[kQkvRows];
 
     const int h = blockIdx.x, row0 = blockIdx.y * kQkvRows;
+    if (h > m.H)
+        return;  // the grid's columns are padded to a multiple of 8 (head h on XCD h % 8)
     const bool kv = h == m.H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32, q_tiles = m.q_pad / 16;
@@ -545,11 +578,12 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
 // (fp32), y o wnorm to `outw` (fp16, the next consumer's normalised A operand), and
 // y's per-tile sums of squares.  The residual and norm columns are fetched with the
 // operands.
-template <int KW, typename ALoad>
+template <int KW, typename ALoad, typename Pf>
 __device__ __forceinline__ void splitk_residual(ALoad&& aload, const uint16_t* w, int KT, int N,
                                                 const float* residual, const float* wnorm,
                                                 float* out, uint16_t* outw, float* ss,
-                                                int n_tiles, int ld, int row0, int B) {
+                                                int n_tiles, int ld, int row0, int B,
+                                                Pf&& prefetch) {
     __shared__ __attribute__((aligned(16))) floatx4 part[kWaves * 64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int nt = blockIdx.x, col = nt * 16 + n;
@@ -568,8 +602,10 @@ __device__ __forceinline__ void splitk_residual(ALoad&& aload, const uint16_t* w
     aload(acc, bw, wave, lane);
     int mt;
     floatx4 v[1];
-    if (!splitk_reduce<1, 1, kWaves>(acc, part, mt, v))
+    if (!splitk_reduce<1, 1, kWaves>(acc, part, mt, v)) {
+        prefetch();  // waves 1.. have nothing left to do but this
         return;
+    }
     floatx4 y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -585,6 +621,7 @@ __device__ __forceinline__ void splitk_residual(ALoad&& aload, const uint16_t* w
 
 template <int KW>
 __global__ __launch_bounds__(64 * kWaves) void g4_kernel(StepArgs s, LayerWeights L) {
+    __shared__ __attribute__((aligned(16))) uint16_t pf_scratch[512];
     const ModelDims& m = s.dims;
     const int row0 = blockIdx.y * 16, ctx_w = m.H * m.kv_rank;  // attention rows: H*kv_rank
     const int KT = m.ctx_pad / 32;
@@ -595,14 +632,28 @@ __global__ __launch_bounds__(64 * kWaves) void g4_kernel(StepArgs s, LayerWeight
             mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
         },
         L.w_out, KT, m.d_model, s.x, L.ffn_norm, s.res, s.resw, s.ss_res, m.d_pad / 16, m.d_pad,
-        row0, s.B);
+        row0, s.B, [&]() {
+            // g5 (next on the stream) runs column pair p on XCD p % 8: its two tiles of
+            // every k-step are 2 * KT5 contiguous blocks
+            const int x = block_xcd(), np = m.ff_pad / 16, KT5 = m.d_pad / 32, per = 2 * KT5;
+            const int pairs = x < np ? (np - x + kXcds - 1) / kXcds : 0;
+            l2_prefetch(pairs * per, [&](int k) {
+                const int p = x + kXcds * (k / per);
+                return L.w_gate_up + ((long long)2 * p * KT5 + k % per) * 512;
+            }, pf_scratch, 1);
+        });
 }
 
 // next_norm: the norm weight of x's next consumer (attn_norm of the next layer, or
-// final_norm after the last layer).
+// final_norm after the last layer).  next: the next layer's weights (qkv_kernel runs
+// next on the stream), or null after the last layer.
 template <int KW>
 __global__ __launch_bounds__(64 * kWaves) void g6_kernel(StepArgs s, LayerWeights L,
-                                                         const float* next_norm) {
+                                                         const float* next_norm,
+                                                         const uint16_t* next_dq_dkv,
+                                                         const uint16_t* next_uq,
+                                                         const uint16_t* next_uk) {
+    __shared__ __attribute__((aligned(16))) uint16_t pf_scratch[512];
     const ModelDims& m = s.dims;
     const int row0 = blockIdx.y * 16, KT = m.ff_pad / 32;
     splitk_residual<KW>(
@@ -612,7 +663,30 @@ __global__ __launch_bounds__(64 * kWaves) void g6_kernel(StepArgs s, LayerWeight
             mma_steps(acc, bw, [&](int kk, int mt) { return a.x[kk][mt]; });
         },
         L.w_down, KT, m.d_model, s.res, next_norm, s.x, s.xw, s.ss_x, m.d_pad / 16, m.d_pad,
-        row0, s.B);
+        row0, s.B, [&]() {
+            if (!next_dq_dkv)
+                return;
+            // qkv_kernel runs head h on XCD h % 8 and the append workgroup (h = H) on XCD H % 8:
+            // head workgroups read the w_dq tiles, the append one the w_dkv tiles, and head h
+            // its w_uq and W_uk blocks (contiguous per head)
+            const int x = block_xcd(), KTq = m.d_pad / 32, q_tiles = m.q_pad / 16;
+            const int n_dq = x < m.H ? q_tiles * KTq : 0;
+            const int n_dkv = m.H % kXcds == x ? (m.kvw_pad / 16) * KTq : 0;
+            const int n_uq = (m.qk_pad / 16) * (m.q_pad / 32), n_uk = (m.kv_pad / 16) * (m.nope_pad / 32);
+            const int heads = x < m.H ? (m.H - x + kXcds - 1) / kXcds : 0;
+            l2_prefetch(n_dq + n_dkv + heads * (n_uq + n_uk), [&](int k) {
+                if (k < n_dq)
+                    return next_dq_dkv + (long long)k * 512;
+                k -= n_dq;
+                if (k < n_dkv)
+                    return next_dq_dkv + ((long long)q_tiles * KTq + k) * 512;
+                k -= n_dkv;
+                const int h = x + kXcds * (k / (n_uq + n_uk));
+                k %= n_uq + n_uk;
+                return k < n_uq ? next_uq + ((long long)h * n_uq + k) * 512
+                                : next_uk + ((long long)h * n_uk + k - n_uq) * 512;
+            }, pf_scratch, 1);
+        });
 }
 
 // --------------------------------------------------------------------- g5 ----
@@ -632,6 +706,8 @@ __global__ __launch_bounds__(64 * kWaves) void g5_kernel(StepArgs s, LayerWeight
     __shared__ float inv_s[16];
     const ModelDims& m = s.dims;
     const int row0 = blockIdx.y * 16, p = blockIdx.x;
+    if (p >= m.ff_pad / 16)
+        return;  // the grid's columns are padded to a multiple of 8 (one XCD per pair)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32;
     RmsPrefetch<16> rms;
@@ -839,6 +915,7 @@ int kw_variant(int ksteps) {
     return ksteps <= 1 ? 1 : ksteps <= 2 ? 2 : ksteps <= 3 ? 3 : ksteps <= 4 ? 4 : ksteps <= 6 ? 6 : 8;
 }
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
+int round_up_to(int a, int b) { return ceil_div(a, b) * b; }
 
 }  // namespace
 
@@ -890,7 +967,7 @@ hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t 
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
                             hipStream_t st) {
     const ModelDims& m = s.dims;
-    const dim3 grid(m.H + 1, ceil_div(s.B, kQkvRows));
+    const dim3 grid(round_up_to(m.H + 1, kXcds), ceil_div(s.B, kQkvRows));  // see l2_prefetch
     const size_t lds = qkv_lds_bytes(m);
     const int nt = max(m.q_pad, m.kvw_pad) / 16;  // <= 16 (mla_model_create checks)
     const int tiles = nt <= 4 ? 4 : nt <= 8 ? 8 : nt <= 12 ? 12 : 16;
@@ -910,7 +987,7 @@ hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* 
 }
 
 hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const float* next_norm,
-                             hipStream_t st) {
+                             const LayerWeights* next, hipStream_t st) {
     const ModelDims& m = s.dims;
     const int chunks = ceil_div(s.B, 16), d_tiles = m.d_pad / 16;
     MLA_KW_DISPATCH(kw_variant(ceil_div(m.ctx_pad / 32, kWaves)), g4_kernel,
@@ -919,12 +996,15 @@ hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const flo
     if (e != hipSuccess)
         return e;
     MLA_KW4_DISPATCH(kw_variant(ceil_div(m.d_pad / 32, kWaves)), g5_kernel,
-                     dim3(m.ff_pad / 16, chunks), dim3(64 * kWaves), 0, st, s, w);
+                     dim3(round_up_to(m.ff_pad / 16, kXcds), chunks), dim3(64 * kWaves), 0, st, s,
+                     w);  // columns padded: see l2_prefetch
     e = hipGetLastError();
     if (e != hipSuccess)
         return e;
     MLA_KW_DISPATCH(kw_variant(ceil_div(m.ff_pad / 32, kWaves)), g6_kernel,
-                    dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w, next_norm);
+                    dim3(d_tiles, chunks), dim3(64 * kWaves), 0, st, s, w, next_norm,
+                    next ? next->w_dq_dkv : nullptr, next ? next->w_uq : nullptr,
+                    next ? next->w_uk : nullptr);
     return hipGetLastError();
 }
 

@@ -411,7 +411,8 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
         if (e == hipSuccess && max_q_len > 1)
             e = launch_prefill(pa, max_q_len, MLA_DTYPE_F16, false, st);
         if (e == hipSuccess)
-            e = launch_layer_post(s, M->layers[l], next_norm, st);
+            e = launch_layer_post(s, M->layers[l], next_norm,
+                                  l + 1 < m.n_layers ? &M->layers[l + 1] : nullptr, st);
         launched += 1 + attn_launches + (max_q_len > 1) + 3;
     }
     if (e == hipSuccess && rows != B && !all_rows) {  // logits of each session's last row only
