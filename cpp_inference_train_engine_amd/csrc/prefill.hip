@@ -14,22 +14,24 @@
 //
 // prefill_page_kernel -- the production kernel (H <= 16, kv_rank 128, rope 16,
 //   64-token tiled pages).  Every head of a query shares the latent, so the kernel
-//   flattens (query, head) into q-rows r = i*H + h: a workgroup of 4 waves (two
-//   q-groups x two halves of each page's tokens) owns 32 consecutive q-rows of one
-//   session (4 queries at H = 8), a q-group QT = 1 16-row tile.
-//   The session's pages stream through a double-buffered LDS copy (the tiled record
-//   as stored); per page and q-tile
-//     S^T = K . Q^T     v_mfma_f32_16x16x32: the page's token tiles, read from LDS
-//                       as loaded (one 1 KB block per wave read), are the A operand;
-//                       Q^T (latent k-steps + the rope step) is the B operand held in
-//                       registers for the whole kernel
-//     causal mask, online softmax in the log2 domain
+//   flattens (query, head) into q-rows r = i*H + h.  A workgroup of 4 waves owns 32
+//   consecutive q-rows of one session (4 queries at H = 8; two 16-row tiles), and every
+//   wave holds all 32: Q^T of both tiles in registers, O^T of both in accumulators.  The
+//   session's key range is cut into 32-token units (half a page), and wave w streams
+//   units w, w+4, w+8, ... through its own two-slot LDS ring (direct global->LDS copies
+//   of the tiled record as stored, the next unit in flight while this one is consumed),
+//   with its own online-softmax state; no barrier is taken until the four states meet in
+//   LDS at the end.  Per unit and q-tile
+//     S^T = K . Q^T     v_mfma_f32_16x16x32: the unit's token tiles, read from LDS as
+//                       copied, are the A operand; Q^T (latent k-steps + the rope step)
+//                       the B operand
+//     causal mask (units that hold a row's causal edge only), online softmax in the
+//                       log2 domain
 //     O^T += C^T . P^T  the S^T accumulators already are P^T's B operand; C^T comes
-//                       straight from the tiled LDS record through the gfx950
-//                       transpose read ds_read_b64_tr_b16 (lane j of a 16-lane group
-//                       points at 4 latent values of one token; lane 4a+b receives
-//                       value b of lanes a, a+4, a+8, a+12), shared by the wave's
-//                       q-tiles
+//                       straight from the tiled unit through the gfx950 transpose read
+//                       ds_read_b64_tr_b16 (lane j of a 16-lane group points at 4 latent
+//                       values of one token; lane 4a+b receives value b of lanes a, a+4,
+//                       a+8, a+12)
 //   This work is MFMA-bound (512 queries x 8 heads over a 2k context is ~6k flop per
 //   cached byte).
 // prefill_generic_kernel -- any H / kv_rank / rope / page size / layout: one
