@@ -140,6 +140,44 @@ __device__ __forceinline__ void copy_block_to_lds(const void* base, uint32_t off
                  : "s"(m0), "v"(off), "s"(reinterpret_cast<const void*>(sb))
                  : "memory", "m0");
 }
+// The 32-bit LDS address of a __shared__ object, for copy_block_to_lds_at: a caller that
+// issues several copies converts its destination once and adds byte offsets, instead of
+// paying the generic-to-LDS conversion (a null check on a 64-bit pointer) per copy.
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)p));
+}
+// copy_block_to_lds with the destination given as an LDS address (uniform).
+__device__ __forceinline__ void copy_block_to_lds_at(const void* base, uint32_t off, uint32_t lds) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane((uint32_t)b));
+    const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
+    const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lds));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(m0), "v"(off), "s"(reinterpret_cast<const void*>(sb))
+                 : "memory", "m0");
+}
+// Four consecutive 1 KB blocks, base + k KB -> lds + k KB (k < 4), through the
+// instruction offset, which global_load_lds applies to the global and the LDS address
+// alike: one M0 and one base for the four copies.
+__device__ __forceinline__ void copy_4blocks_to_lds_at(const void* base, uint32_t off, uint32_t lds) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane((uint32_t)b));
+    const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
+    const uint32_t m0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lds));
+    asm volatile(
+        "s_mov_b32 m0, %0\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "global_load_lds_dwordx4 %1, %2 offset:1024\n\t"
+        "global_load_lds_dwordx4 %1, %2 offset:2048\n\t"
+        "global_load_lds_dwordx4 %1, %2 offset:3072"
+        :
+        : "s"(m0), "v"(off), "s"(reinterpret_cast<const void*>(sb))
+        : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Orders this wave's LDS accesses: nothing before it moves after it, or after it before.

@@ -127,10 +127,12 @@ void prefill_page_kernel(PrefillArgs a) {
             return false;
         const uint16_t* base = a.pages + page * rec;
         const int h = u % UPP;
+        const uint32_t l0 = lds_u32(dst);
+        static_assert(LAT_BLOCKS % 4 == 0, "latent blocks go in fours");
 #pragma unroll
-        for (int k = 0; k < LAT_BLOCKS; ++k)
-            copy_block_to_lds(base + (LAT_BLOCKS * h + k) * 512, lat_off, dst + k * 512);
-        copy_block_to_lds(base + PS * KV + ROPE_WORDS * h, 16 * lane, dst + LAT_BLOCKS * 512);
+        for (int k = 0; k < LAT_BLOCKS; k += 4)
+            copy_4blocks_to_lds_at(base + (LAT_BLOCKS * h + k) * 512, lat_off, l0 + k * 1024);
+        copy_block_to_lds_at(base + PS * KV + ROPE_WORDS * h, 16 * lane, l0 + LAT_BLOCKS * 1024);
         return true;
     };
 
