@@ -191,24 +191,27 @@ void prefill_page_kernel(PrefillArgs a) {
     // Scores, mask, online softmax and PV of unit u (in LDS at sp).
     auto compute = [&](const uint16_t* sp, int uu) {
         const int tok0 = uu * kPfUnit;
+        // the 2 x QT score tiles advance together, k-step by k-step: four independent
+        // accumulation chains, so no MFMA waits on the one before it
         floatx4 sc[2][QT];
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int q = 0; q < QT; ++q)
                 sc[tt][q] = floatx4{0, 0, 0, 0};
 #pragma unroll
-            for (int j = 0; j < KS; ++j) {
-                const V8 ka = *reinterpret_cast<const V8*>(sp + (tt * KS + j) * 512 + s_lane);
+        for (int j = 0; j <= KS; ++j) {
+            V8 ka[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+                ka[tt] = j < KS ? *reinterpret_cast<const V8*>(sp + (tt * KS + j) * 512 + s_lane)
+                                : *reinterpret_cast<const V8*>(sp + LAT_BLOCKS * 512 +
+                                                               tt * 16 * RP + rope_off);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int q = 0; q < QT; ++q)
-                    sc[tt][q] = T::mma32(ka, qv[q][j], sc[tt][q]);
-            }
-            const V8 kr = *reinterpret_cast<const V8*>(sp + LAT_BLOCKS * 512 + tt * 16 * RP +
-                                                        rope_off);
-#pragma unroll
-            for (int q = 0; q < QT; ++q)
-                sc[tt][q] = T::mma32(kr, qv[q][KS], sc[tt][q]);
+                    sc[tt][q] = T::mma32(ka[tt], qv[q][j], sc[tt][q]);
         }
         // Every row of the workgroup sees all 32 tokens of this unit unless it holds the
         // causal edge (or rows past the chunk): only then are tokens masked.
