@@ -37,6 +37,7 @@ struct F16 {
     __device__ static floatx4 mma32(vec8 a, vec8 b, floatx4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
+    __device__ static vec8 ones8() { return vec8{1, 1, 1, 1, 1, 1, 1, 1}; }
     __device__ static floatx4 mma16(vec4 a, vec4 b, floatx4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
     }
@@ -62,6 +63,10 @@ struct BF16 {
     }
     __device__ static floatx4 mma32(vec8 a, vec8 b, floatx4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    __device__ static vec8 ones8() {
+        const __bf16 one = __builtin_bit_cast(__bf16, static_cast<uint16_t>(0x3f80));
+        return vec8{one, one, one, one, one, one, one, one};
     }
     __device__ static floatx4 mma16(vec4 a, vec4 b, floatx4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);

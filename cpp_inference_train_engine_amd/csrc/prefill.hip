@@ -177,12 +177,17 @@ void prefill_page_kernel(PrefillArgs a) {
     // The lowest causal limit of the workgroup's rows (-1 when some row is past the chunk).
     const int lim_min = rb + WG_ROWS <= n_rows ? ctx + rb / H : -1;
 
+    // The row sums of P come out of the MFMA too: lsum[q] = ONES . P^T, whose A operand is
+    // 1 in row 0 (lanes with n == 0) and 0 elsewhere, so lane n of lane group 0 holds the
+    // sum for q-row n in element 0 (every other lane and element holds 0).  They are sums
+    // of the probabilities as rounded for the P.C product, the weights the numerator uses.
     float m_run[QT], l_run[QT];
-    floatx4 acc[QT][RT];
+    floatx4 acc[QT][RT], lsum[QT];
+    const V8 ones = n == 0 ? T::ones8() : V8{};
 #pragma unroll
     for (int q = 0; q < QT; ++q) {
         m_run[q] = kPfNoMax;
-        l_run[q] = 0.0f;
+        lsum[q] = floatx4{0, 0, 0, 0};
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
             acc[q][rt] = floatx4{0, 0, 0, 0};
@@ -251,7 +256,7 @@ void prefill_page_kernel(PrefillArgs a) {
                 const bool had = m_run[q] != kPfNoMax;  // the row has accumulated state
                 if (__builtin_amdgcn_ballot_w64(had && m_new > m_run[q])) {
                     const float alpha = exp2_fast(m_run[q] - m_new);
-                    l_run[q] *= alpha;
+                    lsum[q] *= alpha;
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt)
                         acc[q][rt] *= alpha;
@@ -259,20 +264,17 @@ void prefill_page_kernel(PrefillArgs a) {
                 m_run[q] = m_new;
             }
             const float m_ref = m_run[q];
-            float psum = 0.0f;
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float e = exp2_fast(fmaf(sc[tt][q][i], a.scale_log2, -m_ref));
-                    psum += e;
                     const auto hi = static_cast<typename T::scalar>(e);
                     pb[q][4 * tt + i] = hi;
                     if constexpr (T::split_p)
                         pl[q][4 * tt + i] =
                             static_cast<typename T::scalar>(e - static_cast<float>(hi));
                 }
-            l_run[q] += psum;  // per lane; summed over the 4 lane groups at the end
         }
         // O^T += C^T . P^T over the unit's 32 tokens (one K-step per 16 latent rows)
 #pragma unroll
@@ -287,6 +289,12 @@ void prefill_page_kernel(PrefillArgs a) {
                 if constexpr (T::split_p)
                     acc[q][rt] = T::mma32(ca, pl[q], acc[q][rt]);
             }
+        }
+#pragma unroll
+        for (int q = 0; q < QT; ++q) {
+            lsum[q] = T::mma32(ones, pb[q], lsum[q]);
+            if constexpr (T::split_p)
+                lsum[q] = T::mma32(ones, pl[q], lsum[q]);
         }
     };
     // Tokens of unit uu at or past k_len, or the whole unit when its page id is invalid,
@@ -331,7 +339,7 @@ void prefill_page_kernel(PrefillArgs a) {
     // ---- the waves' softmax states meet in LDS; normalise and store ----
 #pragma unroll
     for (int q = 0; q < QT; ++q)
-        l_run[q] = rows_sum(l_run[q]);
+        l_run[q] = rows_sum(lsum[q][0]);  // lane group 0's value, to every lane of column n
     __syncthreads();  // every wave is done with its slots
     // per wave: acc [QT][RT][64 lanes] floatx4, then m and l of its 32 rows
     constexpr int XO = QT * RT * 64 * 4;
