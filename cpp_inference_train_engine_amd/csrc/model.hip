@@ -84,14 +84,29 @@ __device__ __forceinline__ void l2_prefetch(int n, F&& addr, uint16_t* scratch, 
         copy_block_to_lds(addr(k), lane * 16, scratch);
 }
 
-// Sum over the 16 lanes of an MFMA output row group (lanes with equal g hold the same
-// rows, one column each).
-__device__ __forceinline__ float sum16(float v) {
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1)
-        v += __shfl_xor(v, off, 16);
+// Sums over aligned groups of G = 4, 8 or 16 lanes of a 16-lane row, left in every lane
+// of the group, on DPP lane moves (VALU) instead of LDS permutes: the two quad swaps give
+// every lane its quad's sum, then the half-row mirror pairs the quads of each half and the
+// row mirror the halves (each pairs lanes that hold equal partial sums, so every lane ends
+// with the same bits).  Every lane of the row must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G == 4 || G == 8 || G == 16, "group of 4, 8 or 16 lanes");
+    v += dpp_mov<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);  // quad_perm [2,3,0,1]
+    if constexpr (G >= 8)
+        v += dpp_mov<0x141>(v);  // row_half_mirror
+    if constexpr (G >= 16)
+        v += dpp_mov<0x140>(v);  // row_mirror
     return v;
 }
+// Sum over the 16 lanes of an MFMA output row group (lanes with equal g hold the same
+// rows, one column each).
+__device__ __forceinline__ float sum16(float v) { return group_sum<16>(v); }
 
 template <int MT, int NT>
 __device__ __forceinline__ void zero(floatx4 (&acc)[MT][NT]) {
@@ -213,9 +228,7 @@ struct RmsPrefetch {
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
             sum += v[i];
-#pragma unroll
-        for (int off = 1; off < TPR; off <<= 1)
-            sum += __shfl_xor(sum, off, TPR);
+        sum = group_sum<TPR>(sum);
         if (t < TPR * rows && t % TPR == 0)
             inv_s[t / TPR] = 1.0f / sqrtf(sum / (float)K + eps);
     }
@@ -320,6 +333,9 @@ constexpr int kQkvWaves = 8;
 constexpr int kQkvRows = 16;
 constexpr int kQkvMaxTiles = 16;  // q_pad <= 256, kvw_pad <= 192: at most 16 column tiles
 constexpr int kQkvPad = 8;        // fp16 pad of the LDS A-operand rows
+// fp32 pad of the LDS y rows: with a pitch of 36 mod 64 words, the split-K reduction's
+// writes (rows 4g + i of lane group g) fall 16 banks apart per group, conflict-free.
+constexpr int kQkvYPad = 36;
 
 // LDS layout of qkv_kernel (bytes), from the model dims.
 struct QkvLds {
@@ -335,17 +351,17 @@ __host__ __device__ inline QkvLds qkv_lds(const ModelDims& m) {
     l.qf = l.ya + kQkvRows * (m.q_pad + kQkvPad) * 2;       // [16][qk_pad + 4] fp32
     l.qn = l.qf + kQkvRows * (m.qk_pad + 4) * 4;            // [16][nope_pad + pad] fp16
     const int end = l.qn + kQkvRows * (m.nope_pad + kQkvPad) * 2;
-    l.y = max(kQkvWaves * nt * 64 * 16, end);               // [16][ncol] fp32
-    l.total = l.y + kQkvRows * ncol * 4;
+    l.y = max(kQkvWaves * nt * 64 * 16, end);               // [16][ncol + kQkvYPad] fp32
+    l.total = l.y + kQkvRows * (ncol + kQkvYPad) * 4;
     return l;
 }
 
-// Sum over the 32 lanes of a half wave.
+// Sum over the 32 lanes of a half wave: each 16-lane row's sum, then the rows of each pair
+// {0,1}, {2,3} exchanged by v_permlane16_swap (every lane of the wave active).
 __device__ __forceinline__ float sum32(float v) {
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1)
-        v += __shfl_xor(v, off, 32);
-    return v;
+    float a, b;
+    swap_rows16(group_sum<16>(v), a, b);
+    return a + b;
 }
 
 // KC: chunks of two k-steps per wave (KT <= 16 * KC); NT >= the workgroup's column tiles.
@@ -369,7 +385,7 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32, q_tiles = m.q_pad / 16;
     const int nt0 = kv ? q_tiles : 0, ntv = kv ? m.kvw_pad / 16 : q_tiles;
-    const int ncol = 16 * ntv, ldy = max(m.q_pad, m.kvw_pad);
+    const int ncol = 16 * ntv, ldy = max(m.q_pad, m.kvw_pad) + kQkvYPad;
     __shared__ int32_t slot_s[kQkvRows];
     RmsPrefetch<16> rms;
     rms.issue(s.ss_x, m.d_pad / 16, row0, kQkvRows);

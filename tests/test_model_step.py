@@ -228,6 +228,16 @@ def test_model_step_tiny_matches_oracle(gpu, orc):
 
 
 @pytest.mark.gpu
+def test_model_step_16_heads_matches_oracle(gpu, orc):
+    """mla36m with 16 heads: the MFMA attention path at its largest head count, and two
+    query heads per XCD in qkv_kernel's grid (head h on XCD h % 8, the append workgroup
+    with heads 0 and 8), whose weight blocks g6_kernel prefetches per XCD."""
+    r = _step_case(dict(MLA36M, n_heads=16, max_sequence_length=1024), B=24, max_ctx=400,
+                   seed=2)
+    _check_step(r, "mla36m H=16")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("B, max_ctx, seed", [(16, 700, 0), (70, 300, 1)])
 def test_model_step_mla36m_matches_oracle(gpu, orc, B, max_ctx, seed):
     """mla36m (config 2/3 model): MFMA attention path; B=70 spans two 64-row chunks."""
