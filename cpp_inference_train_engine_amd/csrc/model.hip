@@ -42,7 +42,6 @@ namespace {
 
 using V8 = half8;
 constexpr int kWaves = 8;  // waves per GEMM workgroup
-constexpr int kLdsPad = 8;
 
 __device__ __forceinline__ floatx4 mma(V8 a, V8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -329,6 +328,10 @@ __global__ __launch_bounds__(256) void embed_kernel(StepArgs s, const float* nor
 //            cache dtype) -> q_latent = q_nope . W_uk_h^T (the MPS graph keeps q_latent
 //            in the storage dtype, mps_backend.mm:561)
 //   kv:      kv_norm of the latent columns, RoPE of the key, rounding, paged append
+// The norms are RMSNorm(v)_c = v_c * inv * w_c with one inv per row, and everything after
+// them is linear, so the split-K reduction writes v o w straight away, with the rows'
+// sums of squares per 16-column tile, and inv is applied later: to the w_uq products
+// (head) or at the append (kv).  No pass over the rows waits for a row norm.
 constexpr int kQkvWaves = 8;
 constexpr int kQkvRows = 16;
 constexpr int kQkvMaxTiles = 16;  // q_pad <= 256, kvw_pad <= 192: at most 16 column tiles
@@ -344,24 +347,17 @@ struct QkvLds {
 __host__ __device__ inline QkvLds qkv_lds(const ModelDims& m) {
     const int nt = max(m.q_pad, m.kvw_pad) / 16;
     const int ncol = max(m.q_pad, m.kvw_pad);
-    // The split-K partials are dead once y is summed, so ya / qf / qn reuse them.
+    // The split-K partials are dead once they are summed, so qf / qn reuse them; a head
+    // workgroup writes ya where the append workgroup keeps y (neither needs the other).
     QkvLds l;
     l.part = 0;                                             // [8 waves][nt][64] floatx4
-    l.ya = 0;                                               // [16][q_pad + pad] fp16
-    l.qf = l.ya + kQkvRows * (m.q_pad + kQkvPad) * 2;       // [16][qk_pad + 4] fp32
+    l.qf = 0;                                               // [16][qk_pad + 4] fp32
     l.qn = l.qf + kQkvRows * (m.qk_pad + 4) * 4;            // [16][nope_pad + pad] fp16
     const int end = l.qn + kQkvRows * (m.nope_pad + kQkvPad) * 2;
     l.y = max(kQkvWaves * nt * 64 * 16, end);               // [16][ncol + kQkvYPad] fp32
+    l.ya = l.y;                                             // [16][q_pad + pad] fp16
     l.total = l.y + kQkvRows * (ncol + kQkvYPad) * 4;
     return l;
-}
-
-// Sum over the 32 lanes of a half wave: each 16-lane row's sum, then the rows of each pair
-// {0,1}, {2,3} exchanged by v_permlane16_swap (every lane of the wave active).
-__device__ __forceinline__ float sum32(float v) {
-    float a, b;
-    swap_rows16(group_sum<16>(v), a, b);
-    return a + b;
 }
 
 // KC: chunks of two k-steps per wave (KT <= 16 * KC); NT >= the workgroup's column tiles.
@@ -390,15 +386,16 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     RmsPrefetch<16> rms;
     rms.issue(s.ss_x, m.d_pad / 16, row0, kQkvRows);
     // Side inputs of the later phases travel with the GEMM operands: the norm weight of
-    // this thread's columns in the row-norm phase (32 threads a row, cols <= 256), the
-    // RoPE rotation of its first RoPE element, and (kv workgroup) the rows' cache slots.
-    const int nr = tid >> 5, nsub = tid & 31, ncols = kv ? m.kv_rank : m.q_rank;
+    // the two columns this thread reduces (16 * (wave + 8k) + n: 1 for the key's RoPE
+    // columns, 0 past q_rank), the RoPE rotation of its first RoPE element, and (kv
+    // workgroup) the rows' cache slots.
+    const int ncols = kv ? m.kv_rank : m.q_rank;
     const float* nwp = kv ? L.kv_norm : L.q_norm;
-    float nw[8];
+    float nw[2];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int c = nsub + 32 * k;
-        nw[k] = c < ncols ? nwp[c] : 0.0f;
+    for (int k = 0; k < 2; ++k) {
+        const int c = 16 * (wave + kQkvWaves * k) + n;
+        nw[k] = c < ncols ? nwp[c] : kv ? 1.0f : 0.0f;
     }
     const int rhalf = m.rope / 2;
     float2 rcs = {0.0f, 0.0f};
@@ -461,40 +458,44 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     for (int j = 0; j < NT; ++j)
         if (j < ntv)
             part[(wave * ntv + j) * 64 + lane] = acc[j];
+    __shared__ float ss_part[kQkvRows][kQkvMaxTiles];  // row sums of squares per column tile
+    __shared__ float inv_n[kQkvRows];                  // q_norm / kv_norm factor per row
     __syncthreads();
-    // y[r][c] = inv_x[r] * sum over the waves (rows 4g+i, column 16j+n of lane group e)
-    for (int e = tid; e < ntv * 64; e += 64 * kQkvWaves) {
-        const int j = e >> 6, l = e & 63;
+    // v[r][c] = inv_x[r] * sum over the waves (rows 4g+i, column 16j+n of lane group e);
+    // head: ya = v o q_norm weight (fp16 A operand); kv: y = v o kv_norm weight (1 for the
+    // key's RoPE columns).  ss_part[r][j] = sum of v^2 over tile j's norm columns.
+    for (int e = tid, k = 0; e < ntv * 64; e += 64 * kQkvWaves, ++k) {
+        const int j = e >> 6, l = e & 63, col = 16 * j + (l & 15);
         floatx4 v = {0, 0, 0, 0};
 #pragma unroll
         for (int w = 0; w < kQkvWaves; ++w)
             v += part[(w * ntv + j) * 64 + l];
+        const float wc = k == 0 ? nw[0] : nw[1];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 4 * (l >> 4) + i;
-            y[r * ldy + 16 * j + (l & 15)] = v[i] * inv_x[r];
+            const float yv = v[i] * inv_x[r];
+            if (kv)
+                y[r * ldy + col] = yv * wc;
+            else
+                ya[r * (m.q_pad + kQkvPad) + col] = (_Float16)(yv * wc);
+            const float sq = sum16(col < ncols ? yv * yv : 0.0f);
+            if ((l & 15) == 0)
+                ss_part[r][j] = sq;
         }
     }
     __syncthreads();
-
-    // ---- row norms: q_norm over q_rank columns (to the fp16 A operand), or kv_norm over
-    // kv_rank (in place); in the kv workgroup also the key's RoPE, in place ----
-    {
-        const int r = nr, sub = nsub;  // 32 threads a row (512 threads, 16 rows)
+    // inv of each row (ops.cpp:37-44: 1/sqrt(mean(v^2) + eps)) by the last wave's first
+    // lanes, visible after the next barrier
+    if (wave == kQkvWaves - 1 && lane < kQkvRows) {
         float ss = 0.0f;
-        for (int c = sub; c < ncols; c += 32) {
-            const float v = y[r * ldy + c];
-            ss += v * v;
-        }
-        ss = sum32(ss);
-        const float inv = 1.0f / sqrtf(ss / (float)ncols + m.eps);  // ops.cpp:37-44
-        if (kv) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int c = sub + 32 * k;
-                if (c < m.kv_rank)
-                    y[r * ldy + c] = y[r * ldy + c] * inv * nw[k];
-            }
+        for (int j = 0; j * 16 < ncols; ++j)
+            ss += ss_part[lane][j];
+        inv_n[lane] = 1.0f / sqrtf(ss / (float)ncols + m.eps);
+    }
+
+    if (kv) {  // ---- RoPE of the key (in place), then rounding and the paged append ----
+        {
             for (int e = tid; e < kQkvRows * rhalf; e += 64 * kQkvWaves) {
                 const int rr = e / rhalf, jp = 2 * (e % rhalf);
                 const float2 cs =
@@ -504,19 +505,8 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
                 yk[0] = a0 * cs.x - a1 * cs.y;
                 yk[1] = a0 * cs.y + a1 * cs.x;
             }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int c = sub + 32 * k;
-                if (c < m.q_pad)
-                    ya[r * (m.q_pad + kQkvPad) + c] =
-                        (_Float16)(c < m.q_rank ? y[r * ldy + c] * inv * nw[k] : 0.0f);
-            }
         }
-    }
-    __syncthreads();
-
-    if (kv) {  // ---- rounding, append ----
+        __syncthreads();
         const bool tiled = page_tiled(m.page_size, m.kv_rank, m.rope);
         const int width = m.kv_rank + m.rope;
         for (int e = tid; e < kQkvRows * width; e += 64 * kQkvWaves) {
@@ -528,7 +518,8 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
             if (slot < 0 || page >= s.num_pool_pages)
                 continue;
             uint16_t* base = pool + (long long)page * m.page_size * width;
-            const uint16_t v = F16::from_float(y[r * ldy + c]);
+            const uint16_t v = F16::from_float(c < m.kv_rank ? y[r * ldy + c] * inv_n[r]
+                                                             : y[r * ldy + c]);
             if (c < m.kv_rank)
                 base[latent_word(tiled, off, c, m.page_size, m.kv_rank)] = v;
             else
@@ -538,7 +529,8 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     }
     (void)ncol;
 
-    // ---- q_h = q_norm(cq) . w_uq[:, head h]: wave w < qk_tiles owns column tile w ----
+    // ---- q_h = (cq o q_norm weight) . w_uq[:, head h], times the row's inv below: wave
+    // w < qk_tiles owns column tile w ----
     if (wave < qk_tiles) {
         floatx4 q = {0, 0, 0, 0};
 #pragma unroll
@@ -558,15 +550,15 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
             if (row >= s.B)
                 continue;
             const float2 cs = e == tid ? rcs : s.rope_rows[(long long)row * half + j2];
-            const float a0 = qf[r * (m.qk_pad + 4) + m.nope + jp];
-            const float a1 = qf[r * (m.qk_pad + 4) + m.nope + jp + 1];
+            const float a0 = qf[r * (m.qk_pad + 4) + m.nope + jp] * inv_n[r];
+            const float a1 = qf[r * (m.qk_pad + 4) + m.nope + jp + 1] * inv_n[r];
             uint16_t* qr = s.q_rope + ((long long)row * m.H + h) * m.rope;
             qr[jp] = F16::from_float(a0 * cs.x - a1 * cs.y);
             qr[jp + 1] = F16::from_float(a0 * cs.y + a1 * cs.x);
         }
         for (int e = tid; e < kQkvRows * m.nope_pad; e += 64 * kQkvWaves) {
             const int r = e / m.nope_pad, c = e % m.nope_pad;
-            qn[r * ldq + c] = (_Float16)(c < m.nope ? qf[r * (m.qk_pad + 4) + c] : 0.0f);
+            qn[r * ldq + c] = (_Float16)(c < m.nope ? qf[r * (m.qk_pad + 4) + c] * inv_n[r] : 0.0f);
         }
     }
     __syncthreads();
