@@ -42,6 +42,7 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBS = 8000.0
 N_LAYERS = 10
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "pmc_decode_page_kernel_config3.txt")
+TRAFFIC_FILE_FUSED = os.path.join(REPO, "profiles", "pmc_decode_page_kernel_fused_config3.txt")
 
 
 def parse():
@@ -55,6 +56,8 @@ def parse():
     ap.add_argument("--kernel-reps", type=int, default=50,
                     help="graph replays of 20 back-to-back attention calls")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
+    ap.add_argument("--no-placement", action="store_true",
+                    help="work items in session order and a separate merge launch per layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the config-2, config-4 and config-5 legs")
@@ -68,8 +71,10 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_from_profile(path=TRAFFIC_FILE):
-    """HBM bytes per decode_page_kernel launch, as recorded by the counter passes."""
+def traffic_from_profile(fused: bool = False):
+    """HBM bytes per decode_page_kernel launch, as recorded by the counter passes (of the
+    fused-merge instantiation when ``fused``)."""
+    path = TRAFFIC_FILE_FUSED if fused else TRAFFIC_FILE
     try:
         with open(path) as f:
             m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
@@ -422,9 +427,14 @@ def main():
     qr = dev(batch.q_rope.view(np.int16)).view(torch.float16)
     tokens = dev(np.random.default_rng(1).integers(0, MLA36M["vocab_size"], B).astype(np.int32))
     logits = torch.empty((B, MLA36M["vocab_size"]), dtype=torch.float32, device="cuda")
-    # The host knows every session's length, so the work-item count is exact.
+    # The host knows every session's length, so the work-item count is exact.  With XCD
+    # placement the work list has the slots of the placed layout (empty ones included).
     pages_per_session = (batch.k_len + 63) // 64
     max_work = int(((pages_per_session + args.split_pages - 1) // args.split_pages).sum())
+    n_xcd = 0 if args.no_placement or B > mla.PLACE_MAX_SESSIONS else mla.xcd_count()
+    placed = n_xcd > 0
+    if placed:
+        max_work = mla.placed_work_slots(batch.ctx_len, batch.q_len, 64, args.split_pages, n_xcd)
     out = torch.empty((B, H, 128), dtype=torch.float32, device="cuda")
     ws = mla.decode_workspace(max_work, B, H, 128)
     scale = 1.0 / 8.0
@@ -433,7 +443,7 @@ def main():
         return mla.build_metadata(ctx_len, q_len, cu_pages, page_ids, 64, batch.max_pages,
                                   batch.num_pages, split_pages=args.split_pages,
                                   target_blocks=args.target_blocks, max_work=max_work,
-                                  max_rows=B)
+                                  max_rows=B, placement=placed)
 
     def step():
         rb = meta()
@@ -444,22 +454,25 @@ def main():
     info = rb.read_info()  # raises on a metadata error
     torch.cuda.synchronize()
 
-    def attn_calls(n, fn):
+    def attn_calls(n, fn, fused):
         for i in range(n):
             fn(rb, cache.layer(i % N_LAYERS), ql, qr, scale, kv_rank=128, rope_dim=16, out=out,
-               workspace=ws, flags=args.flags)
+               workspace=ws, flags=args.flags, fused=fused)
 
     calls_per_replay = 2 * N_LAYERS
-    kinds = {"partials": mla.decode_partials, "attention": mla.decode_attention}
+    # partials: the decode kernel without the merge; attention: the call as the step makes
+    # it (one launch over placed metadata); two_launch: decode kernel + merge_kernel
+    kinds = {"partials": (mla.decode_partials, False), "attention": (mla.decode_attention, placed),
+             "two_launch": (mla.decode_attention, False)}
     if args.no_graph:
         run_step = step
-        runners = {k: (lambda f=f: attn_calls(calls_per_replay, f)) for k, f in kinds.items()}
+        runners = {k: (lambda f=f: attn_calls(calls_per_replay, *f)) for k, f in kinds.items()}
     else:
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):  # warm the allocator outside capture
             step()
-            attn_calls(1, mla.decode_attention)
+            attn_calls(1, mla.decode_attention, placed)
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         g_step = torch.cuda.CUDAGraph()
@@ -469,7 +482,7 @@ def main():
         for k, f in kinds.items():
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                attn_calls(calls_per_replay, f)
+                attn_calls(calls_per_replay, *f)
             runners[k] = g
         run_step = g_step.replay
         runners = {k: g.replay for k, g in runners.items()}
@@ -502,8 +515,11 @@ def main():
         us[k] = e0.elapsed_time(e1) * 1e3 / (args.kernel_reps * calls_per_replay)
     rb.read_info()
     bytes_layer = batch.cache_bytes_per_layer()
-    achieved = bytes_layer / (us["partials"] * 1e-6) / 1e9
-    attn_gbs = bytes_layer / (us["attention"] * 1e-6) / 1e9
+    gbs = {k: bytes_layer / (v * 1e-6) / 1e9 for k, v in us.items()}
+    # The dominant kernel as the step runs it: with placement, decode_page_kernel with the
+    # split merge inside (the whole attention of a layer in one launch).
+    main_k = "attention" if placed else "partials"
+    achieved = gbs[main_k]
     result = {
         "metric": "MLA decode tok/s + attn-kernel HBM GB/s (% of peak), 64 ragged sessions",
         "value": round(B / (ms_step * 1e-3), 1),
@@ -524,15 +540,25 @@ def main():
                                "attention, FFN, logits, greedy), one HIP graph",
                    "sessions": B, "cached_tokens_per_layer": int(batch.k_len.sum()),
                    "split_pages": info[1], "work_items": info[0],
+                   "xcd_placement": placed, "work_slots": max_work,
                    "timing": "eager" if args.no_graph else "hip graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profile(),
-                     "kernel": "decode_page_kernel (mla_decode_partials, one layer)",
-                     "us_per_launch": round(us["partials"], 3), "bytes_per_launch": bytes_layer},
-        "attention_call": {"kernels": "decode_page_kernel + merge_kernel (mla_decode_attention)",
-                           "us": round(us["attention"], 3), "GB/s": round(attn_gbs, 1),
-                           "frac": round(attn_gbs / HBM_PEAK_GBS, 4)},
+                     "traffic": traffic_from_profile(placed),
+                     "kernel": ("decode_page_kernel<..., fused merge> (mla_decode_attention over "
+                                "XCD-placed metadata: a layer's whole attention, split merge "
+                                "included, in one launch)" if placed else
+                                "decode_page_kernel (mla_decode_partials, one layer)"),
+                     "us_per_launch": round(us[main_k], 3), "bytes_per_launch": bytes_layer},
+        "decode_kernel_without_merge": {
+            "kernel": "decode_page_kernel (mla_decode_partials: split partials left for a merge)",
+            "us": round(us["partials"], 3), "GB/s": round(gbs["partials"], 1),
+            "frac": round(gbs["partials"] / HBM_PEAK_GBS, 4)},
+        "attention_two_launches": {
+            "kernels": "decode_page_kernel + merge_kernel (mla_decode_attention without the "
+                       "fused merge)",
+            "us": round(us["two_launch"], 3), "GB/s": round(gbs["two_launch"], 1),
+            "frac": round(gbs["two_launch"] / HBM_PEAK_GBS, 4)},
     }
     model.close()
     trace = None

@@ -20,6 +20,8 @@ ERROR_NAMES = {1: "invalid_argument", 2: "io_error", 3: "unsupported", 4: "out_o
 DTYPE_F16, DTYPE_BF16 = 0, 1
 WORK_DESC_INTS, WORK_PAGES, MAX_WORK = 8, 8, 65535
 DECODE_FORCE_GENERIC = 1
+DECODE_FUSED_MERGE = 2
+PLACE_MAX_SESSIONS = 256
 
 
 class MlaError(RuntimeError):
@@ -37,7 +39,8 @@ _SIGNATURES = {
     "mla_last_error": (C.c_char_p, []),
     "mla_abi_version": (C.c_int, []),
     "mla_build_metadata": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 4 +
-                           [C.c_int] * 7 + [C.c_void_p] * 11),
+                           [C.c_int] * 8 + [C.c_void_p] * 11),
+    "mla_xcd_placement_supported": (C.c_int, []),
     "mla_read_metadata_info": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "mla_append_latent": (C.c_int, [C.c_void_p] + [C.c_int] * 5 + [C.c_void_p] * 3 +
                           [C.c_int, C.c_void_p]),
@@ -66,12 +69,12 @@ _SIGNATURES = {
     "mla_model_destroy": (C.c_int, [C.c_void_p]),
     "mla_model_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int] + [C.c_void_p] * 4 +
                        [C.c_int, C.c_int] + [C.c_void_p] * 6 + [C.c_int] +
-                       [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
+                       [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p, C.c_int]),
     "mla_model_logits": (C.c_void_p, [C.c_void_p]),
     "mla_model_forward": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
                                     C.c_int, C.c_int] + [C.c_void_p] * 3 + [C.c_int, C.c_int] +
                           [C.c_void_p] * 6 + [C.c_int] +
-                          [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]),
+                          [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p, C.c_int]),
     "mla_engine_create": (C.c_int, [C.c_void_p, C.c_void_p] + [C.c_int] * 4 +
                           [C.POINTER(C.c_void_p)]),
     "mla_engine_destroy": (C.c_int, [C.c_void_p]),
@@ -171,7 +174,9 @@ def stream_handle(stream=None) -> int | None:
 
 from .ops import (  # noqa: E402  (re-exported operator interface)
     PagedLatentCache, RaggedBatch, append_latent, build_metadata, decode_attention,
-    decode_merge, decode_partials, decode_workspace, decode_workspace_bytes, prefill_attention)
+    decode_merge, decode_partials, decode_workspace, decode_workspace_bytes, placed_work_slots,
+    prefill_attention, xcd_count)
+from . import ops  # noqa: E402
 
 from .model import (HipModel, ModelConfig, config_hash, config_parameter_count,  # noqa: E402
                     config_validate, read_export)

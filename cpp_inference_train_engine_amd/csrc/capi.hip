@@ -6,6 +6,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 namespace mla {
 
@@ -36,14 +37,26 @@ int mla_abi_version(void) { return 1; }
 int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
                        int max_pages, int num_pool_pages, int split_pages, int target_blocks,
-                       int max_work, int max_rows, int32_t* cu_seqlens_q,
+                       int max_work, int max_rows, int placement, int32_t* cu_seqlens_q,
                        int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
                        int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
                        int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
                        int32_t* info) {
     if (B < 0 || page_size < 1 || max_pages < 0 || num_pool_pages < 0 || split_pages < 0 ||
-        target_blocks < 1 || max_work < 0 || max_work > kMaxWork || max_rows < 0)
+        target_blocks < 1 || max_work < 0 || max_work > kMaxWork || max_rows < 0 ||
+        (placement != 0 && placement != 1))
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: invalid scalar argument");
+    int n_xcd = 0;
+    if (placement) {
+        if (B > kPlaceMaxSessions)
+            return fail(MLA_ERR_UNSUPPORTED, "mla_build_metadata: XCD placement takes at most " +
+                                                 std::to_string(kPlaceMaxSessions) + " sessions");
+        n_xcd = mla_xcd_placement_supported();
+        if (n_xcd < 1)
+            return fail(MLA_ERR_UNSUPPORTED,
+                        "mla_build_metadata: XCD placement unavailable on this device (" +
+                            g_last_error + ")");
+    }
     if (!info || !cu_seqlens_q || !cu_seqlens_k || !cu_splits || !cu_pages ||
         (B > 0 && (!ctx_len || !q_len || !num_splits || (max_pages > 0 && !page_table))) ||
         (max_work > 0 && (!work_session || !work_split || !work_desc || !work_pages)) ||
@@ -54,9 +67,30 @@ int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_
     MetadataArgs a{B, ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num_pool_pages,
                    split_pages, target_blocks, max_work, max_rows, cu_seqlens_q, cu_seqlens_k,
                    page_table, slot_mapping, num_splits, cu_splits, work_session, work_split,
-                   work_desc, work_pages, info};
+                   work_desc, work_pages, info, n_xcd};
     return gpu_status(launch_build_metadata(a, static_cast<hipStream_t>(stream)),
                       "mla_build_metadata");
+}
+
+int mla_xcd_placement_supported(void) {
+    static std::mutex mu;
+    static int known[64];  // per device: 0 unknown, else 1 + the XCD count (0 = fails)
+    static std::string reason[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        fail(MLA_ERR_GPU, "mla_xcd_placement_supported: no current device");
+        return 0;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    if (!known[dev]) {
+        reason[dev] = probe_xcd_placement();
+        known[dev] = 1 + (reason[dev].empty() ? xcd_count() : 0);
+    }
+    if (known[dev] == 1) {
+        fail(MLA_ERR_UNSUPPORTED, reason[dev]);
+        return 0;
+    }
+    return known[dev] - 1;
 }
 
 int mla_read_metadata_info(void* stream, const int32_t* info, int32_t* host_info) {
@@ -92,15 +126,11 @@ int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_s
                       "mla_append_latent");
 }
 
-static size_t partial_bytes(int max_work, int n_heads, int kv_rank) {
-    const size_t b = (size_t)max_work * n_heads * ((size_t)kv_rank + 2) * sizeof(float);
-    return (b + 255) & ~(size_t)255;
-}
 
 size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, int kv_rank) {
     if (max_work <= 0 || max_sessions < 0 || n_heads <= 0 || kv_rank <= 0)
         return 0;
-    return partial_bytes(max_work, n_heads, kv_rank);
+    return decode_workspace_size(max_work, n_heads, kv_rank);
 }
 
 }  // extern "C"
@@ -129,7 +159,6 @@ int decode_args(const char* fn, int B, int n_heads, int kv_rank, int rope_dim, i
     if (!workspace || workspace_bytes < need)
         return fail(MLA_ERR_INVALID_ARGUMENT,
                     std::string(fn) + ": workspace needs " + std::to_string(need) + " bytes");
-    float* ws = static_cast<float*>(workspace);
     a = DecodeArgs{};
     a.B = B;
     a.H = n_heads;
@@ -152,8 +181,7 @@ int decode_args(const char* fn, int B, int n_heads, int kv_rank, int rope_dim, i
     a.q_rope = static_cast<const uint16_t*>(q_rope);
     a.out = out;
     a.lse = lse;
-    a.part_o = ws;
-    a.part_ml = ws + (size_t)max_work * n_heads * kv_rank;
+    decode_workspace_layout(workspace, max_work, n_heads, kv_rank, a);
     return MLA_OK;
 }
 
@@ -190,9 +218,12 @@ int mla_decode_attention(MLA_DECODE_PARAMS) {
     if (B == 0 || max_work == 0)
         return MLA_OK;
     const auto s = static_cast<hipStream_t>(stream);
-    if (int st = gpu_status(launch_decode_partials(a, dtype, use_generic(a, workspace, flags), s),
-                            "mla_decode_attention"))
+    const bool generic = use_generic(a, workspace, flags);
+    a.fused_merge = (flags & MLA_DECODE_FUSED_MERGE) && decode_fuses_merge(a, generic);
+    if (int st = gpu_status(launch_decode_partials(a, dtype, generic, s), "mla_decode_attention"))
         return st;
+    if (a.fused_merge)
+        return MLA_OK;
     return gpu_status(launch_merge(a, s), "mla_decode_attention");
 }
 
@@ -202,8 +233,9 @@ int mla_decode_partials(MLA_DECODE_PARAMS) {
         return st;
     if (B == 0 || max_work == 0)
         return MLA_OK;
-    return gpu_status(launch_decode_partials(a, dtype, use_generic(a, workspace, flags),
-                                             static_cast<hipStream_t>(stream)),
+    const bool generic = use_generic(a, workspace, flags);
+    a.fused_merge = (flags & MLA_DECODE_FUSED_MERGE) && decode_fuses_merge(a, generic);
+    return gpu_status(launch_decode_partials(a, dtype, generic, static_cast<hipStream_t>(stream)),
                       "mla_decode_partials");
 }
 
@@ -233,8 +265,7 @@ int mla_decode_merge(void* stream, int B, int n_heads, int kv_rank, const int32_
     a.info = info;
     a.out = out;
     a.lse = lse;
-    a.part_o = const_cast<float*>(static_cast<const float*>(workspace));
-    a.part_ml = a.part_o + (size_t)max_work * n_heads * kv_rank;
+    decode_workspace_layout(const_cast<void*>(workspace), max_work, n_heads, kv_rank, a);
     return gpu_status(launch_merge(a, static_cast<hipStream_t>(stream)), "mla_decode_merge");
 }
 

@@ -61,6 +61,98 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
 
+// The split merge inside the decode launch (DecodeArgs::fused_merge), called by every
+// item of a split session after its partial stores.  The metadata was built XCD-placed,
+// so all items of the session ran on this XCD and their partials sit in its L2: each
+// item waits for its own stores to be acknowledged, then bumps the session's counter
+// with an atomic in that L2 (no device-scope traffic); the item that brings it to
+// num_splits knows every partial has landed, resets the counter for the next launch and
+// folds the partials (log-sum-exp, as merge_kernel) into the session's row.  The loads
+// bypass this CU's L1, which never held the lines.  No item waits on another.
+// Folds the partials at rows base, base + H, .., base + (N-1) H of part_ml / part_o
+// (column c of the o rows) into the running log-sum-exp state (M, L, O).
+template <int N, int KV>
+__device__ __forceinline__ void fold_partials(const DecodeArgs& a, long long base, int c,
+                                              float& M, float& L, floatx4& O) {
+    float m[N], l[N];
+    floatx4 o[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const long long r = base + (long long)j * a.H;
+        m[j] = __builtin_nontemporal_load(a.part_ml + r * 2);
+        l[j] = __builtin_nontemporal_load(a.part_ml + r * 2 + 1);
+        o[j] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(a.part_o + r * KV + c));
+    }
+    float Mn = M;
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+        Mn = fmaxf(Mn, m[j]);
+    const float r = M == -INFINITY ? 0.0f : exp2_fast(M - Mn);
+    L *= r;
+    O *= r;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const float f = m[j] == -INFINITY ? 0.0f : exp2_fast(m[j] - Mn);
+        L += l[j] * f;
+        O += o[j] * f;
+    }
+    M = Mn;
+}
+
+template <int KV, int THREADS>
+__device__ __forceinline__ void fused_merge_tail(const DecodeArgs& a, int s, int row, int ns,
+                                                 long long first) {
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are in L2
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(a.merge_count + s, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        s_last = old == ns - 1;
+        if (old == ns - 1)
+            __hip_atomic_store(a.merge_count + s, 0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __syncthreads();
+    if (!s_last)
+        return;
+    // N partials at a time (N <= 16, fixed per instantiation so that every load is
+    // unconditional and all of them are in flight together): (m, l) and o rows, folded with
+    // the weights 2^(m_j - M) into the running (M, L, O).
+    for (int e = tid; e < a.H * (KV / 4); e += THREADS) {
+        const int h = e / (KV / 4), c = (e % (KV / 4)) * 4;
+        float M = -INFINITY, L = 0.0f;
+        floatx4 O = {0, 0, 0, 0};
+        for (int j0 = 0; j0 < ns; j0 += 16) {
+            const long long base = (first + j0) * a.H + h;
+            switch (min(ns - j0, 16)) {
+#define MLA_FOLD_CASE(N) \
+    case N:                 \
+        fold_partials<N, KV>(a, base, c, M, L, O); \
+        break;
+                MLA_FOLD_CASE(1) MLA_FOLD_CASE(2) MLA_FOLD_CASE(3) MLA_FOLD_CASE(4)
+                MLA_FOLD_CASE(5) MLA_FOLD_CASE(6) MLA_FOLD_CASE(7) MLA_FOLD_CASE(8)
+                MLA_FOLD_CASE(9) MLA_FOLD_CASE(10) MLA_FOLD_CASE(11) MLA_FOLD_CASE(12)
+                MLA_FOLD_CASE(13) MLA_FOLD_CASE(14) MLA_FOLD_CASE(15) MLA_FOLD_CASE(16)
+#undef MLA_FOLD_CASE
+            }
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        __builtin_nontemporal_store(
+            O * inv, reinterpret_cast<floatx4*>(a.out + ((long long)row * a.H + h) * KV + c));
+        if (a.lse && c == 0)
+            a.lse[(long long)row * a.H + h] = (M + __log2f(L)) * kLn2;
+    }
+}
+
+// Split index of a work item from its descriptor: items cover `split` pages each, the
+// session's last one (ending at its last page) possibly fewer.
+__device__ __forceinline__ int item_split_index(int kl, int p_begin, int p_end, int ns, int PS) {
+    const int need = (kl + PS - 1) / PS;
+    return p_end == need ? ns - 1 : p_begin / (p_end - p_begin);
+}
+
 // decode_page_kernel -- one workgroup of WAVES waves per work item (session, split);
 // wave v owns pages p_begin+v, p_begin+v+WAVES, ... of the item and issues ALL loads
 // of a page (PS tokens, TILED record: every 16-byte lane load reads 1 KB
@@ -82,7 +174,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // device-scope partial stores and loads because the items run on different XCDs,
 // whose L2s do not see each other's writes; measured on config 3 that tail costs
 // 4-8 us against 2-3 us for the separate merge launch.)
-template <typename T, int KV, int RP, int PS, int WAVES, int PPW>
+template <typename T, int KV, int RP, int PS, int WAVES, int PPW, bool FUSED>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(PPW == 1 ? 3 : PPW == 2 ? 2 : 1, 8)))
 void decode_page_kernel(DecodeArgs a) {
     static_assert(KV % 32 == 0 && RP % 8 == 0 && RP <= 32 && PS % 32 == 0, "tile shape");
@@ -120,7 +212,7 @@ void decode_page_kernel(DecodeArgs a) {
     const int s = d[0];
     if (s < 0 || d[7] != 1)
         return;  // past the last item (or a failed build), or not a decode row
-    const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5], w0 = d[6];
+    const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5], slot = d[6];
     const long long rec = (long long)PS * (KV + RP);
     // Rope chunks: lanes with 8g >= RP read a duplicate of a valid chunk of the page
     // (in bounds, no extra traffic); their Q^T operand is zero, so they add nothing.
@@ -332,13 +424,17 @@ void decode_page_kernel(DecodeArgs a) {
                 a.lse[(long long)row * a.H + h] = (mh + __log2f(lh)) * kLn2;
         } else {
             __builtin_nontemporal_store(
-                o, reinterpret_cast<floatx4*>(a.part_o + ((long long)w * a.H + h) * KV + c));
+                o, reinterpret_cast<floatx4*>(a.part_o + ((long long)slot * a.H + h) * KV + c));
             if (c == 0) {
-                a.part_ml[((long long)w * a.H + h) * 2] = mh;
-                a.part_ml[((long long)w * a.H + h) * 2 + 1] = lh;
+                a.part_ml[((long long)slot * a.H + h) * 2] = mh;
+                a.part_ml[((long long)slot * a.H + h) * 2 + 1] = lh;
             }
         }
     }
+    if constexpr (FUSED)
+        if (ns > 1)  // the session's first partial slot: this item's, less its split index
+            fused_merge_tail<KV, THREADS>(a, s, row, ns,
+                                          slot - item_split_index(kl, p_begin, p_end, ns, PS));
 }
 
 // ------------------------------------------------------------- generic ----
@@ -384,10 +480,8 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
     for (int w = blockIdx.x; w < a.max_work; w += gridDim.x) {
         const int32_t* d = a.work_desc + (long long)w * kWorkDescInts;
         const int s = d[0];
-        if (s < 0)
-            break;
-        if (d[7] != 1)
-            continue;
+        if (s < 0 || d[7] != 1)
+            continue;  // an empty slot (the placed work list has them between items)
         const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
         const int t_begin = p_begin * PS, t_end = min(kl, p_end * PS);
         for (int i = tid; i < KV + RP; i += kGenThreads)
@@ -456,11 +550,11 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
             for (int k = 0; k < kGenMaxAcc; ++k) {
                 const int r = tid + k * kGenThreads;
                 if (r < KV)
-                    a.part_o[((long long)w * a.H + h) * KV + r] = acc[k];
+                    a.part_o[((long long)d[6] * a.H + h) * KV + r] = acc[k];
             }
             if (tid == 0) {
-                a.part_ml[((long long)w * a.H + h) * 2] = m_run;
-                a.part_ml[((long long)w * a.H + h) * 2 + 1] = l_run;
+                a.part_ml[((long long)d[6] * a.H + h) * 2] = m_run;
+                a.part_ml[((long long)d[6] * a.H + h) * 2 + 1] = l_run;
             }
         }
         __syncthreads();
@@ -573,10 +667,12 @@ constexpr int kPagesPerWave = MLA_DECODE_PPW;
 
 template <typename T>
 hipError_t launch_page(const DecodeArgs& a, int grid, hipStream_t stream) {
-    if (a.kv_rank == 128 && a.rope_dim == 16 && a.page_size == 64)
-        hipLaunchKernelGGL((decode_page_kernel<T, 128, 16, 64, kPageWaves, kPagesPerWave>),
-                           dim3(grid),
-                           dim3(64 * kPageWaves), 0, stream, a);
+    if (a.kv_rank == 128 && a.rope_dim == 16 && a.page_size == 64 && a.fused_merge)
+        hipLaunchKernelGGL((decode_page_kernel<T, 128, 16, 64, kPageWaves, kPagesPerWave, true>),
+                           dim3(grid), dim3(64 * kPageWaves), 0, stream, a);
+    else if (a.kv_rank == 128 && a.rope_dim == 16 && a.page_size == 64)
+        hipLaunchKernelGGL((decode_page_kernel<T, 128, 16, 64, kPageWaves, kPagesPerWave, false>),
+                           dim3(grid), dim3(64 * kPageWaves), 0, stream, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

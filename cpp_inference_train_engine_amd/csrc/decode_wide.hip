@@ -72,7 +72,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
     const int s = d[0];
     if (s < 0 || d[7] != 1)
         return;  // past the last item (or a failed build), or not a decode row
-    const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5];
+    const int row = d[1], kl = d[2], p_begin = d[3], p_end = d[4], ns = d[5], slot = d[6];
     const int H = a.H;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -317,13 +317,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
             if (a.lse && g == 0)
                 a.lse[(long long)row * H + head] = (m_run[ht] + __log2f(l)) * kLn2;
         } else {
-            float* o = a.part_o + ((long long)w * H + head) * KV;
+            float* o = a.part_o + ((long long)slot * H + head) * KV;
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
                 *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt][ht];
             if (g == 0) {
-                a.part_ml[((long long)w * H + head) * 2] = m_run[ht];
-                a.part_ml[((long long)w * H + head) * 2 + 1] = l;
+                a.part_ml[((long long)slot * H + head) * 2] = m_run[ht];
+                a.part_ml[((long long)slot * H + head) * 2 + 1] = l;
             }
         }
     }

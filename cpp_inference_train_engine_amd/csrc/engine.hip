@@ -270,7 +270,7 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
     if (!st)
         st = mla_build_metadata(E->stream, n, d_ctx, d_q, d_cup, d_ids, E->page_size,
                                 E->max_pages, E->num_pages, kSplitPages, 1024, E->work_cap,
-                                E->max_rows, E->cu_q, E->cu_k, E->table, E->slots, E->nsplit,
+                                E->max_rows, 0, E->cu_q, E->cu_k, E->table, E->slots, E->nsplit,
                                 E->cu_split, E->w_sess, E->w_split, E->w_desc, E->w_pages,
                                 E->info);
     if (!st) {

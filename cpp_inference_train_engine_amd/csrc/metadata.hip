@@ -7,7 +7,10 @@
 #include "mla_common.hpp"
 #include "mla_internal.hpp"
 
+#include <algorithm>
 #include <climits>
+#include <string>
+#include <vector>
 
 namespace mla {
 namespace {
@@ -87,6 +90,65 @@ __device__ __forceinline__ long long ceil_div_nn(long long x, long long d) {
     if (x < 0x80000000LL && d < 0x80000000LL)
         return (long long)(((uint32_t)x + (uint32_t)(d - 1)) / (uint32_t)d);
     return (x + d - 1) / d;
+}
+
+// ------------------------------------------------------------ placement ----
+// XCD placement of the work list (MetadataArgs::placement = n XCDs): every session's
+// items go to one XCD so that a decode kernel's items of one session share an L2 (the
+// fused split merge relies on it).  Sessions are ranked by pages read, largest first
+// (ties: lower session first), and dealt to the XCDs in a snake: ranks 0..n-1 to XCDs
+// 0..n-1, ranks n..2n-1 to XCDs n-1..0, and so on, so each XCD takes one session per
+// round of n ranks and no two XCDs' pages differ by more than the largest session's.  A
+// session's items then take its XCD's next slots: item sp of the session of round q on
+// XCD x lands in slot x + n * (k + sp), k the items of that XCD's sessions of rounds < q.
+__device__ long long wave_scan_incl(long long v);  // inclusive sum over the wave's lanes
+
+struct Placement {
+    int32_t weight[kPlaceMaxSessions], order[kPlaceMaxSessions], bin[kPlaceMaxSessions],
+        k0[kPlaceMaxSessions], cnt[kPlaceMaxXcds];
+};
+
+// All threads call it (B <= kPlaceMaxSessions <= 64 n, 1 <= n <= kPlaceMaxXcds); q(b), ctx(b)
+// and cus(b) read the session inputs and the work-item prefix.  Ends with a barrier.
+template <typename Q, typename C, typename S>
+__device__ void place_sessions(int B, int n, int page_size, Q q, C ctx, S cus, Placement& p) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int b = tid; b < B; b += kMetaThreads)
+        p.weight[b] = q(b) > 0 ? (int32_t)ceil_div_nn((long long)ctx(b) + q(b), page_size) : 0;
+    __syncthreads();
+    // rank by (weight desc, session asc): O(B) per session, B <= 256
+    for (int b = tid; b < B; b += kMetaThreads) {
+        const int wb = p.weight[b];
+        int r = 0;
+        for (int c = 0; c < B; ++c) {
+            const int wc = p.weight[c];
+            r += wc > wb || (wc == wb && c < b);
+        }
+        p.order[r] = b;
+    }
+    __syncthreads();
+    if (wave < n) {  // wave x: lane q holds XCD x's session of round q
+        const int x = wave, qr = lane;
+        const int r = qr * n + ((qr & 1) ? n - 1 - x : x);
+        const int b = r < B ? p.order[r] : 0;
+        const long long items = r < B ? cus(b + 1) - cus(b) : 0;
+        const long long incl = wave_scan_incl(items);
+        if (r < B) {
+            p.bin[b] = x;
+            p.k0[b] = (int32_t)(incl - items);
+        }
+        if (lane == 63)
+            p.cnt[x] = (int32_t)incl;
+    }
+    __syncthreads();
+}
+
+// Slots of the placed work list: the largest item count of one XCD, times n.
+__device__ __forceinline__ long long placed_slots(const Placement& p, int n) {
+    int m = 0;
+    for (int i = 0; i < n; ++i)
+        m = max(m, p.cnt[i]);
+    return (long long)m * n;
 }
 
 // L: the batch fits the LDS mirrors (B <= kMetaLdsCap); the compiler then reads them
@@ -247,15 +309,27 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
     }
     const long long W = carry[0];
     // Phase 3: block-to-session map, work descriptors, slot mapping.
+    __shared__ Placement place[1];
+    const int n = L ? a.placement : 0;
+    if (n > 0) {
+        place_sessions(a.B, n, a.page_size, [&](int b) { return qlen[b]; },
+                       [&](int b) { return ctxl[b]; }, [&](int b) { return cus[b]; }, place[0]);
+        if (placed_slots(place[0], n) > a.max_work) {
+            write_error(a, a.B);  // max_work cannot hold the placed work list
+            return;
+        }
+    }
     for (long long w = tid; w < a.max_work; w += kMetaThreads) {
+        const bool empty = n > 0 ? w / n >= place[0].cnt[w % n] : w >= W;
+        if (empty)
+            a.work_desc[w * kWorkDescInts] = -1;
+    }
+    for (long long u = tid; u < W; u += kMetaThreads) {
+        const int b = upper_index(cus, a.B, u);
+        const int sp = (int)(u - cus[b]);
+        const long long w = n > 0 ? place[0].bin[b] + (long long)n * (place[0].k0[b] + sp) : u;
         int32_t* d = a.work_desc + w * kWorkDescInts;
         int32_t* pg = a.work_pages + w * kWorkPages;
-        if (w >= W) {
-            d[0] = -1;
-            continue;
-        }
-        const int b = upper_index(cus, a.B, w);
-        const int sp = (int)(w - cus[b]);
         const int kl = ctxl[b] + qlen[b];
         const int need = (kl + a.page_size - 1) / a.page_size;
         const int p0 = (int)(sp * split);
@@ -268,7 +342,7 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         d[3] = p0;
         d[4] = p1;
         d[5] = cus[b + 1] - cus[b];
-        d[6] = cus[b];
+        d[6] = (int32_t)u;
         d[7] = qlen[b];
 #pragma unroll
         for (int j = 0; j < kWorkPages; ++j)
@@ -438,6 +512,15 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_lds_kernel(Metada
     }
     const long long total_q = s_tot[0], total_k = s_tot[1], split = s_tot[2];
     const int W = (int)s_tot[3];
+    __shared__ Placement place;
+    if (a.placement > 0) {
+        place_sessions(B, a.placement, a.page_size, [&](int b) { return s_q[b]; },
+                       [&](int b) { return s_ctx[b]; }, [&](int b) { return s_cus[b]; }, place);
+        if (placed_slots(place, a.placement) > a.max_work) {
+            write_error(a, B);  // max_work cannot hold the placed work list
+            return;
+        }
+    }
     // ---- outputs: global stores only from here on ----
     for (int b = tid; b <= B; b += kMetaThreads) {
         a.cu_seqlens_q[b] = s_cuq[b];
@@ -449,13 +532,16 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_lds_kernel(Metada
     for (int e = tid; e < entries; e += kMetaThreads)
         a.page_table[e] = s_pt[e];
     typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const int n = a.placement;
     for (int w = tid; w < a.max_work; w += kMetaThreads) {
-        if (w >= W) {
+        const bool empty = n > 0 ? w / n >= place.cnt[w % n] : w >= W;
+        if (empty)
             a.work_desc[(long long)w * kWorkDescInts] = -1;
-            continue;
-        }
-        const int b = upper_index(s_cus, B, w);
-        const int sp = w - s_cus[b];
+    }
+    for (int u = tid; u < W; u += kMetaThreads) {
+        const int b = upper_index(s_cus, B, u);
+        const int sp = u - s_cus[b];
+        const int w = n > 0 ? place.bin[b] + n * (place.k0[b] + sp) : u;
         const int q = s_q[b], kl = s_ctx[b] + q;
         const int need = (kl + a.page_size - 1) / a.page_size;
         const int p0 = (int)(sp * split);
@@ -464,7 +550,7 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_lds_kernel(Metada
         a.work_split[w] = sp;
         i32x4* d = reinterpret_cast<i32x4*>(a.work_desc + (long long)w * kWorkDescInts);
         d[0] = i32x4{b, s_cuq[b], kl, p0};
-        d[1] = i32x4{p1, s_cus[b + 1] - s_cus[b], s_cus[b], q};
+        d[1] = i32x4{p1, s_cus[b + 1] - s_cus[b], u, q};
         int32_t pg[kWorkPages];
 #pragma unroll
         for (int j = 0; j < kWorkPages; ++j)
@@ -523,6 +609,51 @@ hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(build_metadata_kernel<false>, dim3(1), dim3(kMetaThreads), 0, stream,
                            a);
     return hipGetLastError();
+}
+
+// XCD of each workgroup of a launch (the XCC_ID hardware register), for the placement probe.
+__global__ __launch_bounds__(64) void xcd_probe_kernel(int32_t* out) {
+    if (threadIdx.x == 0) {
+        unsigned x;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+        out[blockIdx.x] = (int32_t)x;
+    }
+}
+
+int xcd_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || n < 1)
+        return 0;
+    return n;
+}
+
+// Whether workgroup w of a launch runs on XCD w % n on the current device: ids of 16
+// rounds of n workgroups, launched twice.  Empty string when it holds, else the reason.
+std::string probe_xcd_placement() {
+    const int n = xcd_count();
+    if (n < 1 || n > kPlaceMaxXcds)
+        return "XCD count " + std::to_string(n) + " outside 1.." + std::to_string(kPlaceMaxXcds);
+    if (n == 1)
+        return "";
+    const int G = 16 * n;
+    int32_t* d = nullptr;
+    std::vector<int32_t> h(G);
+    std::string why;
+    if (hipMalloc(&d, G * sizeof(int32_t)) != hipSuccess)
+        return "probe allocation failed";
+    for (int rep = 0; rep < 2 && why.empty(); ++rep) {
+        hipLaunchKernelGGL(xcd_probe_kernel, dim3(G), dim3(64), 0, nullptr, d);
+        if (hipMemcpy(h.data(), d, G * sizeof(int32_t), hipMemcpyDeviceToHost) != hipSuccess) {
+            why = "probe launch failed";
+            break;
+        }
+        for (int w = 0; w < G && why.empty(); ++w)
+            if (h[w] != h[w % n] || (w < n && std::count(h.begin(), h.begin() + n, h[w]) != 1))
+                why = "workgroup " + std::to_string(w) + " ran on XCD " + std::to_string(h[w]);
+    }
+    (void)hipFree(d);
+    return why;
 }
 
 hipError_t launch_append(const AppendArgs& a, int dtype, hipStream_t stream) {

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <string>
+
 #include <cstddef>
 #include <cstdint>
 
@@ -11,7 +13,9 @@ namespace mla {
 
 // Work descriptor of one split-K work item (kWorkDescInts int32):
 //   {session, first query row, k_len, page_begin, page_end, num_splits of the
-//    session, first work item of the session, q_len}; session -1 = no work.
+//    session, partial slot of the item, q_len}; session -1 = no work.  The partial slot
+//    is cu_splits[session] + the item's split index: a session's partials are
+//    contiguous whatever slot of the work list the item itself occupies.
 // work_pages holds the ids of the item's first kWorkPages pages (-1 past the end).
 constexpr int kWorkDescInts = 8;  // MLA_WORK_DESC_INTS
 constexpr int kWorkPages = 8;     // MLA_WORK_PAGES
@@ -23,7 +27,15 @@ struct MetadataArgs {
     int page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows;
     int32_t *cu_seqlens_q, *cu_seqlens_k, *page_table, *slot_mapping, *num_splits, *cu_splits,
         *work_session, *work_split, *work_desc, *work_pages, *info;
+    // XCD placement of the work list: the number of XCDs n (0 = work items in session
+    // order).  With n > 0 every session's items sit in consecutive slots x + n k of one
+    // XCD x (workgroup w of a launch runs on XCD w % n), sessions dealt to the XCDs by
+    // pages read, largest first, in rounds of n (see place_sessions).
+    // B <= kPlaceMaxSessions.
+    int placement;
 };
+constexpr int kPlaceMaxSessions = 256;  // MLA_PLACE_MAX_SESSIONS
+constexpr int kPlaceMaxXcds = 8;
 
 struct AppendArgs {
     int T, kv_rank, rope_dim, page_size, num_pool_pages;
@@ -41,6 +53,11 @@ struct DecodeArgs {
     const int32_t *cu_q, *page_table, *num_splits, *cu_splits, *work_desc, *work_pages, *info;
     const uint16_t *pages, *q_latent, *q_rope;
     float *out, *lse, *part_o, *part_ml;
+    // Fused merge (decode_page_kernel only): the metadata was built XCD-placed, and the
+    // last item of a split session to finish combines the session's partials itself.
+    // merge_count[B] (in the workspace, zero between launches) counts finished items.
+    int fused_merge;
+    int32_t* merge_count;
 };
 
 // Chunked-prefill attention (sessions with q_len > 1, causal within the chunk).
@@ -53,6 +70,28 @@ struct PrefillArgs {
 };
 
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
+// Workspace of decode attention: the fused merge's per-session counters first, in a block
+// of fixed size (fused calls have placed metadata, B <= kPlaceMaxSessions), so that they
+// keep their place whatever max_work and B a later call on the same buffer has; then the
+// split partials (part_o, then part_ml), 256-byte aligned.
+constexpr size_t kMergeCounterBytes = kPlaceMaxSessions * sizeof(int32_t);
+inline size_t decode_partial_bytes(int max_work, int n_heads, int kv_rank) {
+    const size_t b = (size_t)max_work * n_heads * ((size_t)kv_rank + 2) * sizeof(float);
+    return (b + 255) & ~(size_t)255;
+}
+inline size_t decode_workspace_size(int max_work, int n_heads, int kv_rank) {
+    return kMergeCounterBytes + decode_partial_bytes(max_work, n_heads, kv_rank);
+}
+inline void decode_workspace_layout(void* ws, int max_work, int n_heads, int kv_rank,
+                                    DecodeArgs& a) {
+    a.merge_count = static_cast<int32_t*>(ws);
+    a.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + kMergeCounterBytes);
+    a.part_ml = a.part_o + (size_t)max_work * n_heads * kv_rank;
+}
+// XCDs of the current device (0 if unknown), and whether its dispatch places workgroup w
+// on XCD w % n (empty string) or why not.
+int xcd_count();
+std::string probe_xcd_placement();
 hipError_t launch_append(const AppendArgs& a, int dtype, hipStream_t stream);
 // Decode kernel only (MFMA page kernel, or the generic one when force_generic or the
 // shape is outside it): final rows of one-item sessions, partials of the others.
@@ -61,6 +100,10 @@ hipError_t launch_decode_partials(const DecodeArgs& a, int dtype, bool force_gen
 // Log-sum-exp merge of the partials into the rows of split sessions.
 hipError_t launch_merge(const DecodeArgs& a, hipStream_t stream);
 bool decode_mfma_supported(int H, int kv_rank, int rope_dim, int page_size);
+// Only the MFMA page kernel merges inside its launch; the others leave partials.
+inline bool decode_fuses_merge(const DecodeArgs& a, bool generic) {
+    return !generic && decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size);
+}
 // The DeepSeek-like shape (16 < H <= 128, kv_rank 512, rope 64, 64-token pages).
 bool decode_wide_supported(int H, int kv_rank, int rope_dim, int page_size);
 hipError_t launch_decode_wide(const DecodeArgs& a, int dtype, hipStream_t stream);

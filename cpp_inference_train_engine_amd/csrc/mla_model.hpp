@@ -95,6 +95,7 @@ struct MetaPtrs {
     const int32_t *cu_seqlens_q, *cu_seqlens_k, *page_table, *slot_mapping, *num_splits,
         *cu_splits, *work_desc, *work_pages, *info;
     int max_pages, num_pool_pages, max_work;
+    int flags = 0;  // MLA_DECODE_FUSED_MERGE when the metadata was built XCD-placed
 };
 struct Model;  // model_capi.hip
 // One forward of `rows` new tokens belonging to B sessions (row order = session order,

@@ -372,8 +372,7 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     a.q_rope = M->q_rope;
     a.out = M->ctx;
     a.lse = nullptr;
-    a.part_o = static_cast<float*>(workspace);
-    a.part_ml = a.part_o + (size_t)md.max_work * m.H * m.kv_rank;
+    decode_workspace_layout(workspace, md.max_work, m.H, m.kv_rank, a);
     PrefillArgs pa{};
     pa.B = B;
     pa.H = m.H;
@@ -392,7 +391,9 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     pa.out = M->ctx;
     pa.lse = nullptr;
     const bool generic = (reinterpret_cast<uintptr_t>(workspace) & 15) != 0;
-    const int attn_launches = md.max_work > 0 && B > 0 ? 2 : 0;  // decode partials + merge
+    a.fused_merge = (md.flags & MLA_DECODE_FUSED_MERGE) && decode_fuses_merge(a, generic);
+    // decode (+ the split merge unless the decode launch merges itself)
+    const int attn_launches = md.max_work > 0 && B > 0 ? 2 - a.fused_merge : 0;
     hipError_t e = launch_embed(s, M->layers[0].attn_norm, st);
     uint64_t launched = 1;
     for (int l = 0; l < m.n_layers && e == hipSuccess; ++l) {
@@ -406,7 +407,7 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
         // decode attention for the q_len == 1 sessions (its work items of longer sessions
         // exit at once), then chunked-prefill attention for the others
         e = launch_decode_partials(a, MLA_DTYPE_F16, generic, st);
-        if (e == hipSuccess)
+        if (e == hipSuccess && !a.fused_merge)
             e = launch_merge(a, st);
         if (e == hipSuccess && max_q_len > 1)
             e = launch_prefill(pa, max_q_len, MLA_DTYPE_F16, false, st);
@@ -544,11 +545,13 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
                    const int32_t* slot_mapping, const int32_t* num_splits,
                    const int32_t* cu_splits, const int32_t* work_desc, const int32_t* work_pages,
                    const int32_t* info, int max_work, void* const* pages, void* workspace,
-                   size_t workspace_bytes, float* logits, int32_t* next_tokens) {
+                   size_t workspace_bytes, float* logits, int32_t* next_tokens, int flags) {
     // Every session appends one token: rows are sessions and no prefill attention runs,
     // so cu_seqlens_k is not read.
-    const MetaPtrs md{cu_seqlens_q, nullptr, page_table, slot_mapping, num_splits, cu_splits,
-                      work_desc, work_pages, info, max_pages, num_pool_pages, max_work};
+    const MetaPtrs md{cu_seqlens_q, nullptr,   page_table, slot_mapping,
+                      num_splits,   cu_splits, work_desc,  work_pages,
+                      info,         max_pages, num_pool_pages, max_work,
+                      flags};
     return model_forward(static_cast<Model*>(model), static_cast<hipStream_t>(stream), B, tokens,
                          positions, B, 1, md, pages, workspace, workspace_bytes, logits,
                          next_tokens);
@@ -562,11 +565,13 @@ int mla_model_forward(void* model, void* stream, int rows, const int32_t* tokens
                       const int32_t* cu_splits, const int32_t* work_desc,
                       const int32_t* work_pages, const int32_t* info, int max_work,
                       void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
-                      int32_t* next_tokens) {
+                      int32_t* next_tokens, int flags) {
     if (!cu_seqlens_k && max_q_len > 1)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_model_forward: null cu_seqlens_k");
-    const MetaPtrs md{cu_seqlens_q, cu_seqlens_k, page_table, slot_mapping, num_splits, cu_splits,
-                      work_desc, work_pages, info, max_pages, num_pool_pages, max_work};
+    const MetaPtrs md{cu_seqlens_q, cu_seqlens_k, page_table,     slot_mapping,
+                      num_splits,   cu_splits,    work_desc,      work_pages,
+                      info,         max_pages,    num_pool_pages, max_work,
+                      flags};
     return model_forward(static_cast<Model*>(model), static_cast<hipStream_t>(stream), rows,
                          tokens, positions, B, max_q_len, md, pages, workspace, workspace_bytes,
                          logits, next_tokens);

@@ -13,7 +13,7 @@ import ctypes as C
 import json
 import os
 
-from . import check, lib, ptr, stream_handle
+from . import DECODE_FUSED_MERGE, check, lib, ptr, stream_handle
 
 _FIELDS = ("vocab_size", "max_sequence_length", "n_layers", "d_model", "n_heads",
            "head_dim_nope", "head_dim_rope", "head_dim_value", "q_lora_rank", "kv_lora_rank",
@@ -142,5 +142,5 @@ class HipModel:
             batch.num_pool_pages, ptr(batch.slot_mapping), ptr(batch.num_splits),
             ptr(batch.cu_splits), ptr(batch.work_desc), ptr(batch.work_pages), ptr(batch.info),
             batch.max_work, pools, ptr(workspace), int(workspace.numel()), ptr(logits),
-            ptr(next_tokens)))
+            ptr(next_tokens), DECODE_FUSED_MERGE if batch.placed else 0))
         return logits, next_tokens

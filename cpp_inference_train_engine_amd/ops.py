@@ -11,8 +11,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
-from . import (DTYPE_BF16, DTYPE_F16, MAX_WORK, WORK_DESC_INTS, WORK_PAGES, check, lib, ptr,
-               stream_handle)
+from . import (DECODE_FUSED_MERGE, DTYPE_BF16, DTYPE_F16, MAX_WORK, PLACE_MAX_SESSIONS,
+               WORK_DESC_INTS, WORK_PAGES, check, lib, ptr, stream_handle)
 
 
 def _torch():
@@ -41,6 +41,7 @@ class RaggedBatch:
     work_desc: object
     work_pages: object
     info: object
+    placed: bool = False  # XCD-placed work list (decode merges inside its launch)
     host_info: list = field(default_factory=list)
 
     def read_info(self, stream=None):
@@ -52,12 +53,37 @@ class RaggedBatch:
         return self.host_info
 
 
+def xcd_count() -> int:
+    """XCDs of the current device when it places workgroup w on XCD w % n (the premise of
+    XCD placement), else 0.  The first call per device runs a probe kernel."""
+    return int(lib().mla_xcd_placement_supported())
+
+
+def placed_work_slots(ctx_len, q_len, page_size: int, split_pages: int, n_xcd: int) -> int:
+    """Work-list slots of an XCD-placed build (host arrays of the batch's lengths): n_xcd
+    times the largest item count of one XCD, as mla_build_metadata deals the sessions
+    (by pages read, largest first, in rounds of n_xcd: XCDs 0..n-1, then n-1..0, ..)."""
+    import numpy as np
+    ctx = np.asarray(ctx_len, np.int64)
+    q = np.asarray(q_len, np.int64)
+    pages = np.where(q > 0, -(-(ctx + q) // page_size), 0)
+    items = -(-pages // split_pages)
+    order = np.lexsort((np.arange(len(pages)), -pages))
+    r = np.arange(len(pages))
+    xcd = np.where((r // n_xcd) % 2 == 0, r % n_xcd, n_xcd - 1 - r % n_xcd)
+    cnt = np.bincount(xcd, weights=items[order], minlength=n_xcd)
+    return int(n_xcd * cnt.max()) if len(pages) else 0
+
+
 def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size: int, max_pages: int,
                    num_pool_pages: int, split_pages: int = 0, target_blocks: int = 1024,
                    max_work: int | None = None, max_rows: int | None = None,
-                   stream=None) -> RaggedBatch:
+                   placement: bool = False, stream=None) -> RaggedBatch:
     """(a) Build cu_seqlens, padded page tables, slot mapping and the block-to-session
-    map on the GPU (one launch).  Inputs are device int32 tensors."""
+    map on the GPU (one launch).  Inputs are device int32 tensors.  ``placement``: lay
+    the work list out so that each session's items run on one XCD (B <= 256; max_work
+    must hold ``placed_work_slots``); decode attention over it then merges the split
+    partials inside its launch."""
     torch = _torch()
     dev = ctx_len.device
     B = int(ctx_len.numel())
@@ -75,11 +101,12 @@ def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size: int, max_pages
         cu_splits=torch.empty(B + 1, **i32), work_session=torch.empty(max_work, **i32),
         work_split=torch.empty(max_work, **i32),
         work_desc=torch.empty(max_work * WORK_DESC_INTS, **i32),
-        work_pages=torch.empty(max_work * WORK_PAGES, **i32), info=torch.empty(4, **i32))
+        work_pages=torch.empty(max_work * WORK_PAGES, **i32), info=torch.empty(4, **i32),
+        placed=bool(placement))
     check(lib().mla_build_metadata(
         stream_handle(stream), B, ptr(ctx_len), ptr(q_len), ptr(cu_pages), ptr(page_ids),
         page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows,
-        ptr(rb.cu_seqlens_q), ptr(rb.cu_seqlens_k), ptr(rb.page_table), ptr(rb.slot_mapping),
+        int(bool(placement)), ptr(rb.cu_seqlens_q), ptr(rb.cu_seqlens_k), ptr(rb.page_table), ptr(rb.slot_mapping),
         ptr(rb.num_splits), ptr(rb.cu_splits), ptr(rb.work_session), ptr(rb.work_split),
         ptr(rb.work_desc), ptr(rb.work_pages), ptr(rb.info)))
     return rb
@@ -133,13 +160,17 @@ def decode_workspace(max_work: int, max_sessions: int, n_heads: int, kv_rank: in
 
 
 def _decode_call(fn, batch: RaggedBatch, pages, q_latent, q_rope, scale, kv_rank, rope_dim,
-                 dtype, out, lse, workspace, flags, stream):
+                 dtype, out, lse, workspace, flags, stream, fused=None):
     torch = _torch()
     rows, H = int(q_latent.shape[0]), int(q_latent.shape[1])
     if out is None:
         out = torch.zeros((rows, H, kv_rank), dtype=torch.float32, device=q_latent.device)
     if workspace is None:
         workspace = decode_workspace(batch.max_work, batch.B, H, kv_rank, q_latent.device)
+    if fused is None:
+        fused = batch.placed
+    if fused:
+        flags |= DECODE_FUSED_MERGE
     check(getattr(lib(), fn)(
         stream_handle(stream), batch.B, H, kv_rank, rope_dim, batch.page_size, dtype,
         float(scale), ptr(batch.cu_seqlens_q), ptr(batch.page_table), batch.max_pages,
@@ -151,21 +182,24 @@ def _decode_call(fn, batch: RaggedBatch, pages, q_latent, q_rope, scale, kv_rank
 
 def decode_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
                      kv_rank: int, rope_dim: int, dtype: int = DTYPE_F16, out=None, lse=None,
-                     workspace=None, flags: int = 0, stream=None):
+                     workspace=None, flags: int = 0, stream=None, fused: bool | None = None):
     """(c) Absorbed MLA decode attention for every session with one query row.
     q_latent [rows, H, kv_rank], q_rope [rows, H, rope_dim] in the cache dtype;
-    returns out [rows, H, kv_rank] fp32 (and fills lse [rows, H] if given)."""
+    returns out [rows, H, kv_rank] fp32 (and fills lse [rows, H] if given).  ``fused``
+    (default: whether the metadata is XCD-placed) merges the splits inside the decode
+    launch; it needs placed metadata."""
     return _decode_call("mla_decode_attention", batch, pages, q_latent, q_rope, scale, kv_rank,
-                        rope_dim, dtype, out, lse, workspace, flags, stream)
+                        rope_dim, dtype, out, lse, workspace, flags, stream, fused)
 
 
 def decode_partials(batch: RaggedBatch, pages, q_latent, q_rope, scale: float, *,
                     kv_rank: int, rope_dim: int, dtype: int = DTYPE_F16, out=None, lse=None,
-                    workspace=None, flags: int = 0, stream=None):
+                    workspace=None, flags: int = 0, stream=None, fused: bool = False):
     """First launch of decode_attention: final rows of one-item sessions, split partials
-    of the others in ``workspace`` (pass the same workspace to ``decode_merge``)."""
+    of the others in ``workspace`` (pass the same workspace to ``decode_merge``); with
+    ``fused`` (placed metadata) also the rows of split sessions."""
     return _decode_call("mla_decode_partials", batch, pages, q_latent, q_rope, scale, kv_rank,
-                        rope_dim, dtype, out, lse, workspace, flags, stream)
+                        rope_dim, dtype, out, lse, workspace, flags, stream, fused)
 
 
 def decode_merge(batch: RaggedBatch, n_heads: int, kv_rank: int, out, workspace, lse=None,

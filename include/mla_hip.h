@@ -63,6 +63,7 @@ extern "C" {
 
 /* Decode-attention flags. */
 #define MLA_DECODE_FORCE_GENERIC 1 /* use the portable VALU kernel even when the MFMA one fits */
+#define MLA_DECODE_FUSED_MERGE 2   /* metadata built with placement = 1: merge inside the launch */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* mla_last_error(void);
@@ -81,15 +82,16 @@ int mla_abi_version(void);
  * table), num_pool_pages (valid page ids are [0, num_pool_pages)),
  * split_pages (>0 fixed pages per work item; 0 = auto, ceil(total pages of
  * sessions with q_len>0 / target_blocks)), max_work (<= MLA_MAX_WORK) and
- * max_rows capacities.
+ * max_rows capacities, placement (0: work items in session order; 1: XCD
+ * placement, below).
  * Outputs (device): cu_seqlens_q[B+1], cu_seqlens_k[B+1],
  * page_table[B * max_pages] (-1 padded), slot_mapping[max_rows] (flat slot
  * page*page_size+offset of every appended token), num_splits[B],
  * cu_splits[B+1], work_session[max_work], work_split[max_work] (the
  * block-to-session map), work_desc[max_work * MLA_WORK_DESC_INTS] (per work
  * item: session, first query row, k_len, page_begin, page_end, num_splits of
- * the session, first work item of the session, q_len; session -1 marks every
- * item past the last one, and all items of a failed build),
+ * the session, partial slot = cu_splits[session] + split index, q_len; session
+ * -1 marks every empty slot, and all items of a failed build),
  * work_pages[max_work * MLA_WORK_PAGES] (ids of each item's first pages, -1
  * past its end) and info[4]:
  *     ok:    {W (work items), split_pages used, total_q, total_k}
@@ -99,14 +101,30 @@ int mla_abi_version(void);
  * range, a running total exceeds INT32_MAX, or the work/row capacity is
  * exceeded.  Errors are reported through info (read it with
  * mla_read_metadata_info); every consumer kernel treats info[0] < 0 as an
- * empty batch. */
+ * empty batch.
+ *
+ * XCD placement (placement = 1; no reference counterpart): the work list is laid
+ * out so that all items of a session run on one XCD of the GPU, whose dispatch
+ * puts workgroup w of a launch on XCD w % n (n XCDs; checked once per device by
+ * mla_xcd_placement_supported).  Sessions ranked by pages read, largest first
+ * (ties: lower session), are dealt to the XCDs in rounds of n: rank r to XCD r % n
+ * in even rounds and n - 1 - r % n in odd ones, so no XCD's pages exceed another's
+ * by more than the largest session's.  Item sp of session b goes to slot
+ * x_b + n * (k_b + sp), where k_b counts the items of XCD x_b's sessions of earlier
+ * rounds; slots no item takes are empty
+ * (session -1).  Needs B <= MLA_PLACE_MAX_SESSIONS and max_work >= n times the
+ * largest item count of one XCD (info error {-1, B, 0, 0} otherwise);
+ * MLA_ERR_UNSUPPORTED when the device fails the check.  Decode attention over
+ * placed metadata may then merge the split partials inside its launch
+ * (MLA_DECODE_FUSED_MERGE). */
+#define MLA_PLACE_MAX_SESSIONS 256
 #define MLA_WORK_DESC_INTS 8
 #define MLA_WORK_PAGES 8
 #define MLA_MAX_WORK 65535
 int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
                        int max_pages, int num_pool_pages, int split_pages, int target_blocks,
-                       int max_work, int max_rows, int32_t* cu_seqlens_q,
+                       int max_work, int max_rows, int placement, int32_t* cu_seqlens_q,
                        int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
                        int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
                        int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
@@ -115,6 +133,12 @@ int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_
 /* Synchronises `stream`, copies info[4] to host_info and returns
  * MLA_ERR_INVALID_ARGUMENT (naming the session) if the build failed. */
 int mla_read_metadata_info(void* stream, const int32_t* info, int32_t* host_info);
+
+/* The XCD count n >= 1 of the current device if it dispatches workgroup w of a
+ * launch on XCD w % n (the premise of XCD placement), else 0 with the reason in
+ * mla_last_error().  The first call per device runs a probe kernel and
+ * synchronises: call it before any stream capture that builds placed metadata. */
+int mla_xcd_placement_supported(void);
 
 /* ------------------------------------------------------------------ (b)
  * Paged latent append; refines the reference's contiguous append
@@ -142,10 +166,16 @@ int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_s
  * Work is split over the metadata's work items (split-K over pages); the
  * split partials of a session are merged with a log-sum-exp combine by a
  * second launch on the same stream (the pair is also exposed separately:
- * mla_decode_partials and mla_decode_merge, below).  `workspace` (device) must hold
- * mla_decode_workspace_bytes(max_work, B, H, kv_rank) bytes (partials; no
- * initialisation needed).  Calls that share a workspace must be ordered on
- * one stream.  The production kernel runs one wave per page of a work item,
+ * mla_decode_partials and mla_decode_merge, below).  With MLA_DECODE_FUSED_MERGE
+ * and XCD-placed metadata (mla_build_metadata placement = 1) the MFMA page
+ * kernel merges instead: the last item of a split session to finish combines
+ * the session's partials through its XCD's L2, and the call is one launch (the
+ * flag on metadata that is not placed gives wrong rows).  `workspace` (device)
+ * must hold mla_decode_workspace_bytes(max_work, B, H, kv_rank) bytes: a fixed
+ * block of MLA_PLACE_MAX_SESSIONS int32 counters of the fused merge first (zero
+ * them before the workspace's first fused call; every call leaves them zero),
+ * then the partials.  Calls that share a
+ * workspace must be ordered on one stream.  The production kernel runs one wave per page of a work item,
  * so metadata built with split_pages == MLA_DECODE_SPLIT_PAGES keeps a whole
  * item in flight. */
 #define MLA_DECODE_SPLIT_PAGES 4
@@ -167,7 +197,10 @@ int mla_decode_attention(void* stream, int B, int n_heads, int kv_rank, int rope
  * (same arguments) writes the final rows of sessions with one work item and
  * leaves the other sessions' partials in `workspace`; mla_decode_merge then
  * combines those partials into their rows of `out` (and `lse`).  Both must see
- * the same metadata and workspace, in this order on one stream. */
+ * the same metadata and workspace, in this order on one stream.  With
+ * MLA_DECODE_FUSED_MERGE, mla_decode_partials also writes the rows of split
+ * sessions (when the MFMA page kernel runs; the partials stay in `workspace`, so a
+ * following mla_decode_merge rewrites the same rows). */
 int mla_decode_partials(void* stream, int B, int n_heads, int kv_rank, int rope_dim,
                         int page_size, int dtype, float scale, const int32_t* cu_seqlens_q,
                         const int32_t* page_table, int max_pages, int num_pool_pages,
@@ -285,14 +318,16 @@ int mla_model_update_weights(void* model, const float* params, uint64_t* revisio
  * next_tokens[B] (device int32): the greedy token of sample_token with
  * temperature 0 and no penalty (inference.cpp:345-380: lowest index among the
  * maxima of the ids not banned, see mla_model_set_banned), -1 when a logit is not
- * finite (numerical_error), -2 when every id is banned. */
+ * finite (numerical_error), -2 when every id is banned.  flags: MLA_DECODE_FUSED_MERGE
+ * when the metadata was built XCD-placed (the decode attention of each layer is then
+ * one launch, see mla_decode_attention), else 0. */
 int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
                    const int32_t* positions, const int32_t* cu_seqlens_q,
                    const int32_t* page_table, int max_pages, int num_pool_pages,
                    const int32_t* slot_mapping, const int32_t* num_splits,
                    const int32_t* cu_splits, const int32_t* work_desc, const int32_t* work_pages,
                    const int32_t* info, int max_work, void* const* pages, void* workspace,
-                   size_t workspace_bytes, float* logits, int32_t* next_tokens);
+                   size_t workspace_bytes, float* logits, int32_t* next_tokens, int flags);
 /* One forward of `rows` new tokens of B sessions in one batch (continuous batching with
  * chunked prefill): session b appends q_len = cu_seqlens_q[b+1] - cu_seqlens_q[b] >= 1
  * tokens (rows in session order; rows <= max_batch), token r at positions[r].  Per
@@ -305,7 +340,7 @@ int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
  * The metadata arguments come from one mla_build_metadata call (ctx_len = tokens
  * already cached, q_len as above).  A prompt of n tokens prefilled in chunks through
  * successive calls gives the same rows as one call (causality, tests/test_model.cpp:
- * 65-77). */
+ * 65-77).  flags as for mla_model_step. */
 int mla_model_forward(void* model, void* stream, int rows, const int32_t* tokens,
                       const int32_t* positions, int B, int max_q_len,
                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
@@ -314,7 +349,7 @@ int mla_model_forward(void* model, void* stream, int rows, const int32_t* tokens
                       const int32_t* cu_splits, const int32_t* work_desc,
                       const int32_t* work_pages, const int32_t* info, int max_work,
                       void* const* pages, void* workspace, size_t workspace_bytes, float* logits,
-                      int32_t* next_tokens);
+                      int32_t* next_tokens, int flags);
 /* Token ids the greedy next token of later steps skips: sample_token's `banned`
  * (inference.cpp:345-380), which InferenceEngine::load fills with the special tokens
  * other than <|eos|> and the ids with no bytes (inference.cpp:441-447; see

@@ -83,7 +83,7 @@ def _declare(L):
         "orc_set_threads": (None, [i]),
         "orc_set_blas": (None, [vp, vp]),
         "orc_attention_paged": (i, [i, i, i, i, i, i, vp, vp, vp, i, vp, vp, vp, f, vp, vp]),
-        "orc_build_metadata": (i, [i, vp, vp, vp, vp, i, i, i, i, i, i, i,
+        "orc_build_metadata": (i, [i, vp, vp, vp, vp, i, i, i, i, i, i, i, i,
                                    vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
         "orc_append_paged": (None, [i, i, i, i, i, vp, vp, vp, vp]),
         "orc_greedy": (i, [vp, i, vp, i, f, vp, i]),
@@ -282,7 +282,11 @@ def attention_paged(H, kv_rank, rope_dim, page_size, dtype, cu_q, k_len, page_ta
 
 
 def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num_pool_pages,
-                   split_pages=0, target_blocks=512, max_work=65535, max_rows=1 << 30):
+                   split_pages=0, target_blocks=512, max_work=65535, max_rows=1 << 30,
+                   placement_xcds=0):
+    """The metadata of mla_build_metadata.  Session order (placement_xcds = 0):
+    work_session / work_split are cut to the W items.  XCD placement (n > 0): they keep
+    all max_work slots, meaningful where ``occupied`` (work_desc session >= 0)."""
     ctx_len = np.ascontiguousarray(ctx_len, np.int32)
     q_len = np.ascontiguousarray(q_len, np.int32)
     cu_pages = np.ascontiguousarray(cu_pages, np.int32)
@@ -300,14 +304,16 @@ def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num
         B, _p(ctx_len), _p(q_len), _p(cu_pages), _p(page_ids if page_ids.size else
                                                     np.zeros(1, np.int32)),
         page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows,
-        *(_p(out[k]) for k in ("cu_seqlens_q", "cu_seqlens_k", "page_table", "slot_mapping",
+        placement_xcds, *(_p(out[k]) for k in ("cu_seqlens_q", "cu_seqlens_k", "page_table", "slot_mapping",
                                "num_splits", "cu_splits", "work_session", "work_split",
                                "work_desc", "work_pages", "info")))
     if st:
         raise ValueError(f"invalid metadata input (session {int(out['info'][1])})")
     W = int(out["info"][0])
-    out["work_session"] = out["work_session"][:W]
-    out["work_split"] = out["work_split"][:W]
+    out["occupied"] = out["work_desc"][:, 0] >= 0
+    if placement_xcds == 0:
+        out["work_session"] = out["work_session"][:W]
+        out["work_split"] = out["work_split"][:W]
     return out
 
 

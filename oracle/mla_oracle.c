@@ -757,11 +757,13 @@ static int metadata_error(int max_work, int32_t* work_desc, int32_t* info, int s
 int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
                        int max_pages, int num_pool_pages, int split_pages, int target_blocks,
-                       int max_work, int max_rows, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
-                       int32_t* page_table, int32_t* slot_mapping, int32_t* num_splits,
-                       int32_t* cu_splits, int32_t* work_session, int32_t* work_split,
-                       int32_t* work_desc, int32_t* work_pages, int32_t* info) {
-    if (B < 0 || page_size < 1 || max_pages < 0 || split_pages < 0 || target_blocks < 1)
+                       int max_work, int max_rows, int placement_xcds, int32_t* cu_seqlens_q,
+                       int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
+                       int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
+                       int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
+                       int32_t* info) {
+    if (B < 0 || page_size < 1 || max_pages < 0 || split_pages < 0 || target_blocks < 1 ||
+        placement_xcds < 0)
         return metadata_error(max_work, work_desc, info, -1);
     long long total_q = 0, total_k = 0, total_pages = 0;
     cu_seqlens_q[0] = 0;
@@ -805,11 +807,55 @@ int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
             return metadata_error(max_work, work_desc, info, b);
         cu_splits[b + 1] = (int32_t)w;
     }
+    /* XCD placement (no reference counterpart; the GPU builder's layout, restated):
+     * sessions ranked by pages read (q_len > 0), largest first, ties to the lower
+     * session; rank r goes to XCD r % n in even rounds (r / n) and n - 1 - r % n in odd
+     * ones; item s of session b in slot xcd[b] + n * (first[b] + s), first[b] = items
+     * of the XCD's sessions of earlier rounds. */
+    const int n = placement_xcds;
+    int *xcd = NULL, *first = NULL;
+    long long slots = w;
+    if (n > 0) {
+        xcd = (int*)calloc((size_t)B + 1, sizeof(int));
+        first = (int*)calloc((size_t)B + 1, sizeof(int));
+        int* order = (int*)calloc((size_t)B + 1, sizeof(int));
+        long long* pages = (long long*)calloc((size_t)B + 1, sizeof(long long));
+        long long* count = (long long*)calloc((size_t)n, sizeof(long long));
+        for (int b = 0; b < B; ++b) {
+            const long long kl = (long long)ctx_len[b] + q_len[b];
+            pages[b] = q_len[b] > 0 ? (kl + page_size - 1) / page_size : 0;
+            order[b] = b;
+        }
+        for (int i = 1; i < B; ++i)  /* insertion sort: pages desc, session asc */
+            for (int j = i; j > 0 && pages[order[j - 1]] < pages[order[j]]; --j) {
+                const int t = order[j];
+                order[j] = order[j - 1];
+                order[j - 1] = t;
+            }
+        for (int r = 0; r < B; ++r) {
+            const int b = order[r];
+            const int x = (r / n) % 2 == 0 ? r % n : n - 1 - r % n;
+            xcd[b] = x;
+            first[b] = (int)count[x];
+            count[x] += num_splits[b];
+        }
+        long long most = 0;
+        for (int i = 0; i < n; ++i)
+            most = count[i] > most ? count[i] : most;
+        slots = most * n;
+        free(order), free(pages), free(count);
+        if (slots > max_work) {
+            free(xcd), free(first);
+            return metadata_error(max_work, work_desc, info, B);
+        }
+    }
+    for (long long x = 0; x < max_work; ++x)
+        work_desc[(size_t)x * 8] = -1;
     for (int b = 0; b < B; ++b) {
         const int kl = ctx_len[b] + q_len[b];
         const int need = (kl + page_size - 1) / page_size;
         for (int s = 0; s < num_splits[b]; ++s) {
-            const int w = cu_splits[b] + s;
+            const int w = n > 0 ? xcd[b] + n * (first[b] + s) : cu_splits[b] + s;
             const int p0 = (int)(s * split), p1 = p0 + split < need ? (int)(p0 + split) : need;
             int32_t* d = work_desc + (size_t)w * 8;
             work_session[w] = b;
@@ -820,7 +866,7 @@ int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
             d[3] = p0;
             d[4] = p1;
             d[5] = num_splits[b];
-            d[6] = cu_splits[b];
+            d[6] = cu_splits[b] + s;
             d[7] = q_len[b];
             for (int j = 0; j < 8; ++j)
                 work_pages[(size_t)w * 8 + j] = p0 + j < p1 ? page_ids[cu_pages[b] + p0 + j] : -1;
@@ -831,8 +877,7 @@ int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
                 page_table[(size_t)b * max_pages + pos / page_size] * page_size + pos % page_size;
         }
     }
-    for (long long x = w; x < max_work; ++x)
-        work_desc[(size_t)x * 8] = -1;
+    free(xcd), free(first);
     info[0] = (int32_t)w;
     info[1] = (int32_t)split;
     info[2] = (int32_t)total_q;

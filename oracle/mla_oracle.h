@@ -115,18 +115,22 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
  * page_table[B x max_pages] (-1 padded), slot_mapping[total_q],
  * num_splits[B], cu_splits[B+1], work_session[W], work_split[W],
  * work_desc[max_work x 8] = {session, first query row, k_len, page_begin,
- * page_end, num_splits, first item of the session, q_len} (session -1 for every
- * item >= W and for every item of a failed build), work_pages[max_work x 8] =
+ * page_end, num_splits, partial slot cu_splits[session] + split, q_len} (session -1
+ * for every empty slot and for every item of a failed build), work_pages[max_work x 8] =
  * first 8 page ids of each item (-1 past its end), info[4] =
  * {W, split_pages, total_q, total_k} or {-1, first offending session, 0, 0}.
+ * placement_xcds = n > 0 lays the work list out over n XCDs (each session's items
+ * in slots x, x + n, ..; {-1, B, 0, 0} when max_work cannot hold it); 0 keeps
+ * session order (item w = cu_splits[session] + split).
  * Returns 0, or 1 (invalid argument). */
 int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
                        int max_pages, int num_pool_pages, int split_pages, int target_blocks,
-                       int max_work, int max_rows, int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
-                       int32_t* page_table, int32_t* slot_mapping, int32_t* num_splits,
-                       int32_t* cu_splits, int32_t* work_session, int32_t* work_split,
-                       int32_t* work_desc, int32_t* work_pages, int32_t* info);
+                       int max_work, int max_rows, int placement_xcds, int32_t* cu_seqlens_q,
+                       int32_t* cu_seqlens_k, int32_t* page_table, int32_t* slot_mapping,
+                       int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
+                       int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
+                       int32_t* info);
 
 /* ---- Paged append (refines inference.cpp:100-103): row t of ckv/krope (fp32)
  * is rounded to 16-bit and written to slot slot_mapping[t] of the pool. */

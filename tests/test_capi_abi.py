@@ -39,17 +39,26 @@ def test_invalid_arguments_are_rejected_on_the_host():
     import cpp_inference_train_engine_amd as mla
     L = mla.lib()
     assert L.mla_abi_version() == 1
-    st = L.mla_build_metadata(None, -1, *([None] * 4), 64, 4, 10, 0, 16, 8, 8, *([None] * 11))
+    st = L.mla_build_metadata(None, -1, *([None] * 4), 64, 4, 10, 0, 16, 8, 8, 0, *([None] * 11))
     assert st == 1 and b"invalid" in L.mla_last_error()
-    st = L.mla_build_metadata(None, 4, *([None] * 4), 64, 4, 10, 0, 16, 70000, 8, *([None] * 11))
+    st = L.mla_build_metadata(None, 4, *([None] * 4), 64, 4, 10, 0, 16, 70000, 8, 0,
+                              *([None] * 11))
     assert st == 1  # max_work above MLA_MAX_WORK
+    st = L.mla_build_metadata(None, 4, *([None] * 4), 64, 4, 10, 0, 16, 8, 8, 2, *([None] * 11))
+    assert st == 1  # placement is 0 or 1
+    st = L.mla_build_metadata(None, 257, *([None] * 4), 64, 4, 10, 0, 16, 8, 8, 1,
+                              *([None] * 11))
+    assert st == 3 and b"256 sessions" in L.mla_last_error()  # unsupported: B > 256
     st = L.mla_append_latent(None, 4, 128, 16, 64, 7, None, None, None, 10, None)
     assert st == 1
     st = L.mla_decode_attention(None, 4, 8, 128, 16, 64, 0, 0.125, *([None] * 2), 4, 10,
                                 *([None] * 8), 16, None, None, None, 0, 0)
     assert st == 1  # null buffers
-    # partials [max_work][H][kv_rank + 2] fp32, rounded up to 256 bytes
-    assert L.mla_decode_workspace_bytes(16, 4, 8, 128) == (16 * 8 * 130 * 4 + 255) // 256 * 256
+    # 256 int32 counters of the fused merge, then partials [max_work][H][kv_rank + 2] fp32
+    # rounded up to 256 bytes; the size does not depend on the session count
+    assert L.mla_decode_workspace_bytes(16, 4, 8, 128) == 1024 + (16 * 8 * 130 * 4 + 255) // 256 * 256
+    assert L.mla_decode_workspace_bytes(16, 100, 8, 128) == L.mla_decode_workspace_bytes(16, 4, 8,
+                                                                                          128)
     with pytest.raises(mla.MlaError) as e:
         mla.check(1)
     assert e.value.code == "invalid_argument"

@@ -157,7 +157,7 @@ def _check_step(r, what):
     assert (r["next"] >= 0).all()
 
 
-def _config3_case(seed=0):
+def _config3_case(seed=0, placement=False):
     """Config 3 exactly as bench.py times it: mla36m (max_sequence_length 4608) with
     Model::create-scaled weights from the oracle (seed 0, fp16), 64 sessions whose lengths
     after the append are U[128, 4096] (ragged_decode_batch, reference Rng), 10 layers of
@@ -180,7 +180,7 @@ def _config3_case(seed=0):
     model = mla.HipModel(mla.ModelConfig.from_dict(CFG3), params, max_batch=B, page_size=ps)
     rb = mla.build_metadata(_dev(ctx), _dev(batch.q_len), _dev(batch.cu_pages),
                             _dev(batch.page_ids), ps, batch.max_pages, batch.num_pages,
-                            split_pages=4)
+                            split_pages=4, placement=placement)
     gpu_pages = [_dev(batch.pages[l].view(np.int16)).view(torch.float16) for l in range(L)]
     ws = mla.decode_workspace(rb.max_work, B, H, kv)
     logits, nxt = model.step(rb, _dev(tokens), _dev(ctx), gpu_pages, ws)
@@ -218,6 +218,13 @@ def test_model_step_config3_full_lengths(gpu, orc):
     """The headline step (config 3) at its real lengths: every one of the 64 sessions'
     logits, appended cache rows and greedy token against the oracle's CpuDecoder."""
     _check_step(_config3_case(seed=0), "config3 (64 sessions, U[128,4096])")
+
+
+@pytest.mark.gpu
+def test_model_step_config3_placed(gpu, orc):
+    """The same step over XCD-placed metadata, as bench.py times it: every layer's decode
+    attention merges its splits inside its own launch."""
+    _check_step(_config3_case(seed=0, placement=True), "config3 placed (fused merge)")
 
 
 @pytest.mark.gpu
