@@ -67,21 +67,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // item waits for its own stores to be acknowledged, then bumps the session's counter
 // with an atomic in that L2 (no device-scope traffic); the item that brings it to
 // num_splits knows every partial has landed, resets the counter for the next launch and
-// folds the partials (log-sum-exp, as merge_kernel) into the session's row.  The loads
-// bypass this CU's L1, which never held the lines.  No item waits on another.
-// Folds the partials at rows base, base + H, .., base + (N-1) H of part_ml / part_o
-// (column c of the o rows) into the running log-sum-exp state (M, L, O).
+// folds the partials (log-sum-exp, as merge_kernel) into the session's row.  The partial
+// stores are plain ones so that the lines stay in the L2.  No item waits on another.
+// Folds the partials of head h in slots slot0 .. slot0 + N - 1 (columns c..c+3 of their o
+// rows) into the running log-sum-exp state (M, L, O).  Plain loads: the lines were written
+// in this launch on other CUs of this XCD, and this CU's L1 holds no copy of them (it is
+// invalidated at the launch, part_o slots are whole lines, part_ml slots are padded to
+// whole lines, and only this merge reads them).
 template <int N, int KV>
-__device__ __forceinline__ void fold_partials(const DecodeArgs& a, long long base, int c,
+__device__ __forceinline__ void fold_partials(const DecodeArgs& a, long long slot0, int h, int c,
                                               float& M, float& L, floatx4& O) {
     float m[N], l[N];
     floatx4 o[N];
+    const int mls = part_ml_stride(a.H);
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-        const long long r = base + (long long)j * a.H;
-        m[j] = __builtin_nontemporal_load(a.part_ml + r * 2);
-        l[j] = __builtin_nontemporal_load(a.part_ml + r * 2 + 1);
-        o[j] = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(a.part_o + r * KV + c));
+        const long long sl = slot0 + j;
+        m[j] = a.part_ml[sl * mls + 2 * h];
+        l[j] = a.part_ml[sl * mls + 2 * h + 1];
+        o[j] = *reinterpret_cast<const floatx4*>(a.part_o + (sl * a.H + h) * KV + c);
     }
     float Mn = M;
 #pragma unroll
@@ -125,11 +129,10 @@ __device__ __forceinline__ void fused_merge_tail(const DecodeArgs& a, int s, int
         float M = -INFINITY, L = 0.0f;
         floatx4 O = {0, 0, 0, 0};
         for (int j0 = 0; j0 < ns; j0 += 16) {
-            const long long base = (first + j0) * a.H + h;
             switch (min(ns - j0, 16)) {
 #define MLA_FOLD_CASE(N) \
     case N:                 \
-        fold_partials<N, KV>(a, base, c, M, L, O); \
+        fold_partials<N, KV>(a, first + j0, h, c, M, L, O); \
         break;
                 MLA_FOLD_CASE(1) MLA_FOLD_CASE(2) MLA_FOLD_CASE(3) MLA_FOLD_CASE(4)
                 MLA_FOLD_CASE(5) MLA_FOLD_CASE(6) MLA_FOLD_CASE(7) MLA_FOLD_CASE(8)
@@ -422,12 +425,18 @@ void decode_page_kernel(DecodeArgs a) {
                 o * inv, reinterpret_cast<floatx4*>(a.out + ((long long)row * a.H + h) * KV + c));
             if (a.lse && c == 0)
                 a.lse[(long long)row * a.H + h] = (mh + __log2f(lh)) * kLn2;
+        } else if constexpr (FUSED) {  // plain stores: the partials stay in this XCD's L2
+            *reinterpret_cast<floatx4*>(a.part_o + ((long long)slot * a.H + h) * KV + c) = o;
+            if (c == 0) {
+                a.part_ml[(long long)slot * part_ml_stride(a.H) + 2 * h] = mh;
+                a.part_ml[(long long)slot * part_ml_stride(a.H) + 2 * h + 1] = lh;
+            }
         } else {
             __builtin_nontemporal_store(
                 o, reinterpret_cast<floatx4*>(a.part_o + ((long long)slot * a.H + h) * KV + c));
             if (c == 0) {
-                a.part_ml[((long long)slot * a.H + h) * 2] = mh;
-                a.part_ml[((long long)slot * a.H + h) * 2 + 1] = lh;
+                a.part_ml[(long long)slot * part_ml_stride(a.H) + 2 * h] = mh;
+                a.part_ml[(long long)slot * part_ml_stride(a.H) + 2 * h + 1] = lh;
             }
         }
     }
@@ -553,8 +562,8 @@ __global__ __launch_bounds__(kGenThreads) void decode_generic_kernel(DecodeArgs 
                     a.part_o[((long long)d[6] * a.H + h) * KV + r] = acc[k];
             }
             if (tid == 0) {
-                a.part_ml[((long long)d[6] * a.H + h) * 2] = m_run;
-                a.part_ml[((long long)d[6] * a.H + h) * 2 + 1] = l_run;
+                a.part_ml[(long long)d[6] * part_ml_stride(a.H) + 2 * h] = m_run;
+                a.part_ml[(long long)d[6] * part_ml_stride(a.H) + 2 * h + 1] = l_run;
             }
         }
         __syncthreads();
@@ -599,9 +608,9 @@ __global__ __launch_bounds__(kMergeElems* G) void merge_kernel(DecodeArgs a) {
                     vecV (&oi)[kMergeUnroll]) {
 #pragma unroll
         for (int k = 0; k < kMergeUnroll; ++k) {
-            const long long idx = (long long)(w0 + min(i0 + k, i_hi - 1)) * H + h;
-            mi[k] = a.part_ml[idx * 2];
-            li[k] = a.part_ml[idx * 2 + 1];
+            const long long sl = w0 + min(i0 + k, i_hi - 1), idx = sl * H + h;
+            mi[k] = a.part_ml[sl * part_ml_stride(H) + 2 * h];
+            li[k] = a.part_ml[sl * part_ml_stride(H) + 2 * h + 1];
             oi[k] = *reinterpret_cast<const vecV*>(a.part_o + idx * KV + c);
         }
     };

@@ -322,8 +322,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_wide_kernel(DecodeArgs a) {
             for (int rt = 0; rt < RT; ++rt)
                 *reinterpret_cast<floatx4*>(o + 16 * rt + 4 * g) = acc[rt][ht];
             if (g == 0) {
-                a.part_ml[((long long)slot * H + head) * 2] = m_run[ht];
-                a.part_ml[((long long)slot * H + head) * 2 + 1] = l;
+                a.part_ml[(long long)slot * part_ml_stride(H) + 2 * head] = m_run[ht];
+                a.part_ml[(long long)slot * part_ml_stride(H) + 2 * head + 1] = l;
             }
         }
     }

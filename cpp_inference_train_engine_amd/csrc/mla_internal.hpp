@@ -73,10 +73,14 @@ hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
 // Workspace of decode attention: the fused merge's per-session counters first, in a block
 // of fixed size (fused calls have placed metadata, B <= kPlaceMaxSessions), so that they
 // keep their place whatever max_work and B a later call on the same buffer has; then the
-// split partials (part_o, then part_ml), 256-byte aligned.
+// split partials, 256-byte aligned: part_o [max_work][H][kv_rank] and part_ml, whose
+// (m, l) pairs of one slot take [H][2] floats padded to whole 128-byte lines
+// (part_ml_stride floats per slot), so that no cache line holds two slots' pairs.
 constexpr size_t kMergeCounterBytes = kPlaceMaxSessions * sizeof(int32_t);
+__host__ __device__ inline int part_ml_stride(int n_heads) { return (2 * n_heads + 31) & ~31; }
 inline size_t decode_partial_bytes(int max_work, int n_heads, int kv_rank) {
-    const size_t b = (size_t)max_work * n_heads * ((size_t)kv_rank + 2) * sizeof(float);
+    const size_t b = (size_t)max_work *
+                     ((size_t)n_heads * kv_rank + part_ml_stride(n_heads)) * sizeof(float);
     return (b + 255) & ~(size_t)255;
 }
 inline size_t decode_workspace_size(int max_work, int n_heads, int kv_rank) {

@@ -54,9 +54,11 @@ def test_invalid_arguments_are_rejected_on_the_host():
     st = L.mla_decode_attention(None, 4, 8, 128, 16, 64, 0, 0.125, *([None] * 2), 4, 10,
                                 *([None] * 8), 16, None, None, None, 0, 0)
     assert st == 1  # null buffers
-    # 256 int32 counters of the fused merge, then partials [max_work][H][kv_rank + 2] fp32
-    # rounded up to 256 bytes; the size does not depend on the session count
-    assert L.mla_decode_workspace_bytes(16, 4, 8, 128) == 1024 + (16 * 8 * 130 * 4 + 255) // 256 * 256
+    # 256 int32 counters of the fused merge, then per slot o [H][kv_rank] fp32 and the
+    # (m, l) pairs [H][2] padded to 128 bytes, rounded up to 256 bytes; the size does not
+    # depend on the session count
+    assert L.mla_decode_workspace_bytes(16, 4, 8, 128) == 1024 + 16 * (8 * 128 + 32) * 4
+    assert L.mla_decode_workspace_bytes(3, 4, 17, 128) == 1024 + (3 * (17 * 128 + 64) * 4 + 255) // 256 * 256
     assert L.mla_decode_workspace_bytes(16, 100, 8, 128) == L.mla_decode_workspace_bytes(16, 4, 8,
                                                                                           128)
     with pytest.raises(mla.MlaError) as e:
