@@ -275,8 +275,13 @@ def config4_leg(mla, torch, reps: int = 20, n_pools: int = 4):
     need = (b.k_len + 63) // 64
     mw = int(((need + 3) // 4).sum())
     rows = int(b.q_len.sum())
+    # XCD-placed metadata (128 sessions): the decode call is one launch, merge included
+    n_xcd = mla.xcd_count() if len(b.q_len) <= mla.PLACE_MAX_SESSIONS else 0
+    if n_xcd:
+        mw = mla.placed_work_slots(b.ctx_len, b.q_len, 64, 4, n_xcd)
     rb = mla.build_metadata(dev(b.ctx_len), dev(b.q_len), dev(b.cu_pages), dev(b.page_ids), 64,
-                            b.max_pages, b.num_pages, split_pages=4, max_work=mw, max_rows=rows)
+                            b.max_pages, b.num_pages, split_pages=4, max_work=mw, max_rows=rows,
+                            placement=n_xcd > 0)
     pages = dev(b.pages[0].view(np.int16)).view(torch.float16)
     # Copies of the layer's pool, visited in turn, so the working set (n_pools x ~120 MB)
     # exceeds the 256 MB Infinity Cache and every call reads HBM.
@@ -321,7 +326,8 @@ def config4_leg(mla, torch, reps: int = 20, n_pools: int = 4):
                                "tflops": round(tf, 1), "mfma_peak_tflops": 2500.0,
                                "frac": round(tf / 2500.0, 4)},
             "decode_call": {"us": round(res["decode"], 2), "cached_tokens": dec_tokens,
-                            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+                            "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                            "one_launch": rb.placed}}
 
 
 def config5_leg(mla, torch, reps: int = 5, split: int = 128):

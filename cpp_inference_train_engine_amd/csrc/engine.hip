@@ -42,6 +42,7 @@ struct Engine {
     mla_model_config cfg{};
     int page_size = 0, num_pages = 0, max_rows = 0, max_sessions = 0, max_pages = 0;
     int work_cap = 0;
+    int n_xcd = 0;  // XCDs when the device supports XCD placement of the work list, else 0
     hipStream_t stream = nullptr;
     size_t rec_words = 0;
     uint16_t* pool = nullptr;  // [n_layers][num_pages][rec_words]
@@ -140,6 +141,28 @@ hipError_t copy_page(Engine* E, int32_t dst, int32_t src) {
 // order).  Logits of each session's last new row go to `logits` [n x vocab] (host,
 // may be null), greedy tokens to `next` [n] (host, may be null).  Lengths advance only
 // on success.
+// Whether this step's work list is built XCD-placed (each layer's decode attention then one
+// launch): the device supports it, the batch has at most MLA_PLACE_MAX_SESSIONS sessions,
+// and the placed list fits the work capacity.  The slot count repeats mla_build_metadata's
+// deal (sessions by pages read, largest first, snake rounds over the XCDs) on the host's
+// lengths, so the build never fails for want of room.
+bool placed_fits(const Engine* E, int n, const int32_t* ctx, const int32_t* q) {
+    if (E->n_xcd < 1 || n > MLA_PLACE_MAX_SESSIONS)
+        return false;
+    std::vector<int> pages(n), order(n);
+    for (int b = 0; b < n; ++b) {
+        pages[b] = q[b] > 0 ? ceil_div((long long)ctx[b] + q[b], E->page_size) : 0;
+        order[b] = b;
+    }
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return pages[a] > pages[b]; });
+    std::vector<long long> items(E->n_xcd, 0);
+    for (int r = 0; r < n; ++r) {
+        const int x = (r / E->n_xcd) % 2 == 0 ? r % E->n_xcd : E->n_xcd - 1 - r % E->n_xcd;
+        items[x] += ceil_div(pages[order[r]], kSplitPages);
+    }
+    return (long long)E->n_xcd * *std::max_element(items.begin(), items.end()) <= E->work_cap;
+}
+
 int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* tokens,
          float* logits, int32_t* next, const char* fn, bool all_rows = false) {
     const mla_model_config& c = E->cfg;
@@ -267,16 +290,18 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
     int32_t *d_ctx = E->d_in, *d_q = d_ctx + n, *d_cup = d_ctx + 2 * n, *d_tok = d_ctx + 3 * n + 1;
     int32_t *d_pos = d_tok + rows, *d_ids = d_pos + rows;
     int st = gpu_status(e, fn);
+    const bool placed = placed_fits(E, n, h_ctx, h_q);
     if (!st)
         st = mla_build_metadata(E->stream, n, d_ctx, d_q, d_cup, d_ids, E->page_size,
                                 E->max_pages, E->num_pages, kSplitPages, 1024, E->work_cap,
-                                E->max_rows, 0, E->cu_q, E->cu_k, E->table, E->slots, E->nsplit,
+                                E->max_rows, placed ? 1 : 0, E->cu_q, E->cu_k, E->table, E->slots, E->nsplit,
                                 E->cu_split, E->w_sess, E->w_split, E->w_desc, E->w_pages,
                                 E->info);
     if (!st) {
-        const MetaPtrs md{E->cu_q,     E->cu_k,   E->table,  E->slots,   E->nsplit,
-                          E->cu_split, E->w_desc, E->w_pages, E->info,    E->max_pages,
-                          E->num_pages, E->work_cap};
+        const MetaPtrs md{E->cu_q,     E->cu_k,    E->table,   E->slots,
+                          E->nsplit,   E->cu_split, E->w_desc, E->w_pages,
+                          E->info,     E->max_pages, E->num_pages, E->work_cap,
+                          placed ? MLA_DECODE_FUSED_MERGE : 0};
         st = model_forward(static_cast<Model*>(E->model), E->stream, (int)rows, d_tok, d_pos, n,
                            max_q, md, E->layer_pools.data(), E->workspace, E->ws_bytes,
                            d_logits, d_next, all_rows);
@@ -362,8 +387,14 @@ int mla_engine_create(const mla_model_config* config, const float* params, int m
     E->max_rows = max_rows;
     E->max_sessions = max_sessions;
     E->max_pages = ceil_div(config->max_sequence_length, page_size);
+    // XCD placement (each layer's decode attention in one launch) needs room for the placed
+    // work list: every XCD holds at most ceil(sessions / n) sessions' items.
+    E->n_xcd = mla_xcd_placement_supported();
+    const long long per_session = ceil_div(E->max_pages, kSplitPages);
+    const long long placed_cap =
+        E->n_xcd > 0 ? (long long)E->n_xcd * ceil_div(max_sessions, E->n_xcd) * per_session : 0;
     E->work_cap = (int)std::min<long long>(
-        kMaxWork, (long long)max_sessions * ceil_div(E->max_pages, kSplitPages));
+        kMaxWork, std::max((long long)max_sessions * per_session, placed_cap));
     E->rec_words = (size_t)page_size * (config->kv_lora_rank + config->head_dim_rope);
     E->refs.assign(num_pages, 0);
     for (int p = num_pages - 1; p >= 0; --p)
@@ -398,6 +429,8 @@ int mla_engine_create(const mla_model_config* config, const float* params, int m
         e = E->dalloc(w, E->ws_bytes);
         E->workspace = w;
     }
+    if (e == hipSuccess)  // the fused merge's counters start at zero
+        e = hipMemset(E->workspace, 0, E->ws_bytes);
     if (e == hipSuccess) e = E->halloc(E->h_in, E->in_cap);
     if (e == hipSuccess) e = E->halloc(E->h_logits, S * V);
     if (e == hipSuccess) e = E->halloc(E->h_out, 4 + S);

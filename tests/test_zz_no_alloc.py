@@ -3,7 +3,9 @@ split partials live in the library's per-GPU scratch array), checked against
 mla_decode_attention with a caller workspace on the same inputs -- the same kernels, so
 the outputs must be bit-identical.  Two calls in a row, the second with a smaller batch
 (the scratch keeps the first call's partials; nothing of them may leak into the second),
-then a size beyond the scratch maximum, rejected on the host before any launch."""
+the same two over XCD-placed metadata with the merge inside the decode launch (its
+counters live in the scratch as well), then a size beyond the scratch maximum, rejected on
+the host before any launch."""
 import ctypes as C
 import sys
 
@@ -26,15 +28,15 @@ def _entry(lib):
     return f
 
 
-def _call(gpu, f, B, seed, max_len):
+def _call(gpu, f, B, seed, max_len, placed=False):
     import torch
     from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
     batch = ragged_decode_batch(B=B, min_len=1, max_len=max_len, seed=seed)
-    _say(f"noalloc call: B={B} seed={seed} tokens={int(batch.k_len.sum())}")
+    _say(f"noalloc call: B={B} seed={seed} tokens={int(batch.k_len.sum())} placed={placed}")
     dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     rb = gpu.build_metadata(dev(batch.ctx_len), dev(batch.q_len), dev(batch.cu_pages),
                             dev(batch.page_ids), 64, batch.max_pages, batch.num_pages,
-                            split_pages=4)
+                            split_pages=4, placement=placed)
     pages = dev(batch.pages[0].view(np.int16)).view(torch.float16)
     ql = dev(batch.q_latent.view(np.int16)).view(torch.float16)
     qr = dev(batch.q_rope.view(np.int16)).view(torch.float16)
@@ -46,7 +48,8 @@ def _call(gpu, f, B, seed, max_len):
     gpu.check(f(gpu.stream_handle(), B, 8, 128, 16, 64, gpu.DTYPE_F16, 0.125,
                 p(rb.cu_seqlens_q), p(rb.page_table), rb.max_pages, rb.num_pool_pages,
                 p(pages), p(ql), p(qr), p(rb.num_splits), p(rb.cu_splits), p(rb.work_desc),
-                p(rb.work_pages), p(rb.info), rb.max_work, p(out), p(lse), 0))
+                p(rb.work_pages), p(rb.info), rb.max_work, p(out), p(lse),
+                gpu.DECODE_FUSED_MERGE if placed else 0))
     torch.cuda.synchronize()
     info = rb.read_info()
     assert info[0] > B, "the case must have split sessions, whose partials use the scratch"
@@ -59,6 +62,9 @@ def test_noalloc_decode_equals_workspace_decode(gpu):
     assert gpu.lib().mla_noalloc_scratch_bytes() == 16 << 20
     _call(gpu, f, 64, 0, 4096)  # config 3's size: 570 work items
     _call(gpu, f, 9, 1, 1500)   # then a smaller batch on the same scratch
+    # the one-launch decode over XCD-placed metadata (merge counters in the scratch too)
+    _call(gpu, f, 64, 2, 4096, placed=True)
+    _call(gpu, f, 9, 3, 1500, placed=True)
     # partials beyond the scratch: rejected on the host, nothing launched
     st = f(None, 64, 128, 512, 64, 64, gpu.DTYPE_BF16, 0.1, None, None, 1, 1,
            *([None] * 8), 6000, None, None, 0)
