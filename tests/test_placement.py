@@ -140,3 +140,21 @@ def test_fused_decode_config3_and_reuse(gpu, orc):
     got = _attn(gpu, rbs, small, 0, True, ws, None)
     want, _ = _oracle_decode(orc, small)
     _check(got, want, "fused edge lengths")
+
+
+@pytest.mark.parametrize("n_heads", [16, 5])
+def test_fused_decode_other_head_counts(gpu, orc, n_heads):
+    """The MFMA page kernel serves up to 16 heads: the fused merge with two elements per
+    thread (16 heads) and with an odd head count (the (m, l) blocks padded to whole lines)."""
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    from test_gpu_kernels import _oracle_decode
+    batch = ragged_decode_batch(B=40, min_len=1, max_len=3000, n_heads=n_heads, seed=11)
+    n = gpu.xcd_count()
+    slots = gpu.placed_work_slots(batch.ctx_len, batch.q_len, 64, 4, n)
+    ws = gpu.decode_workspace(slots, 40, n_heads, batch.kv_rank)
+    rb = _placed(gpu, batch.ctx_len, batch.q_len, batch.cu_pages, batch.page_ids, 64,
+                 batch.max_pages, batch.num_pages, 4, slots)
+    _say(f"fused decode H={n_heads} items={rb.read_info()[0]}")
+    got = _attn(gpu, rb, batch, 0, True, ws, None)
+    want, _ = _oracle_decode(orc, batch)
+    _check(got, want, f"fused H={n_heads}")
