@@ -61,8 +61,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the config-2, config-4 and config-5 legs")
-    ap.add_argument("--cpu-seconds", type=float, default=6.0,
-                    help="seconds of CPU work per baseline leg (all threads, then 1 thread)")
+    ap.add_argument("--cpu-seconds", type=float, default=5.0,
+                    help="seconds of CPU timing per baseline leg (all cores, 1 thread; half "
+                         "of it for the non-absorbed fallback)")
     ap.add_argument("--flags", type=int, default=0)
     ap.add_argument("--only", choices=["config2", "config4", "config5", "serve"], default=None,
                     help="run only this secondary leg and print its JSON (for profiling)")
@@ -94,86 +95,210 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(batch, params, seconds: float, config2_trace=None):
+def time_it(warmup: int, reps: int, prepare, operation):
+    """The reference's timing (apps/bench_main.cpp:12-30): `warmup` untimed runs, then
+    `reps` timed ones, prepare() outside the clock; returns the sorted samples in ms."""
+    samples = []
+    for i in range(-warmup, reps):
+        prepare()
+        t0 = time.perf_counter()
+        operation()
+        dt = (time.perf_counter() - t0) * 1e3
+        if i >= 0:
+            samples.append(dt)
+    return sorted(samples)
+
+
+def median_p95(samples):
+    """Median and p95 of sorted samples as bench_main.cpp:26-29 takes them (the element
+    at n / 2, and at ceil(0.95 n) - 1)."""
+    n = len(samples)
+    return samples[n // 2], samples[min(n - 1, int(np.ceil(n * 0.95)) - 1)]
+
+
+def cpu_baseline(batch, params, seconds: float, traces=None):
     """The reference CPU path for the same step: the oracle's fp32 restatement of
     CpuDecoder::decode (inference.cpp:69-174: projections, absorbed attention over the
-    session's contiguous cache, FFN, tied logits) on a bounded sample of the batch's
-    sessions, one session per thread (forks decode concurrently, inference.cpp:238),
-    repeated for `seconds`; then the same sample on one thread.  Its products run on the
-    CBLAS numpy ships (OpenBLAS, one thread per call) in place of the reference's
-    Accelerate calls.  With `config2_trace` (the GPU's config-2 run), the CPU path also
-    replays config 2 on the same fp16 weights and tokens and reports the GPU's logit
-    error against it, as the reference's decode bench records (apps/bench_main.cpp:
-    378-396)."""
-    import concurrent.futures as cf
+    session's contiguous cache, FFN, tied logits), timed like apps/bench_main.cpp:12-30
+    and 395-408: per decode call, with warmup, median and p95; `prepare` rewinds the
+    session to its config-3 length.  A bounded sample of the batch's sessions (spread over
+    its lengths) decodes one session per thread on every visible core (forks decode
+    concurrently, inference.cpp:238), then the same sessions one after another on 1 thread,
+    then with the non-absorbed K/V reconstruction (CpuDecoder::set_absorbed(false),
+    bench_main.cpp:400-408: baseline_median_ms and speedup).  The products run on the CBLAS
+    numpy ships (OpenBLAS, one thread per call) in place of the reference's Accelerate.
+
+    `traces` (the GPU legs' inputs and outputs) are checked here, with the oracle as the
+    checker, as the reference's benches record a correctness error next to each timing
+    (bench_main.cpp:378-396)."""
+    import threading
     import oracle
     from cpp_inference_train_engine_amd.workloads import MLA36M
     blas = oracle.use_blas(True)
     cfg = oracle.Config.from_dict(MLA36M)
     visible = len(os.sched_getaffinity(0))
-    # A one-GPU box allots 16 host cores to its GPU; more threads than that would time
-    # contention with other jobs, not the CPU path.
-    cores = max(1, min(16, visible))
-    pick = np.argsort(batch.k_len)[np.linspace(0, len(batch.k_len) - 1, cores).astype(int)]
-    decs = []
+    n_sess = max(1, min(visible, len(batch.k_len)))
+    pick = np.argsort(batch.k_len)[np.linspace(0, len(batch.k_len) - 1, n_sess).astype(int)]
     proj = oracle.output_projection(cfg, params)  # prepare_projections, once per model
-    for b in pick:  # each sampled session at its config-3 length (cache contents N(0,1))
-        d = oracle.Decoder(cfg, params, absorbed=True, proj=proj)
-        n = int(batch.ctx_len[b])
-        gen = np.random.default_rng(int(b))
-        d.latent[:, :n] = gen.standard_normal((cfg.n_layers, n, cfg.kv_lora_rank), np.float32)
-        d.rope[:, :n] = gen.standard_normal((cfg.n_layers, n, cfg.head_dim_rope), np.float32)
-        decs.append((d, n))
 
-    def one(i):
-        d, n = decs[i]
-        d.position = n
-        d.decode(1)
+    def decoders(absorbed):
+        out = []
+        for b in pick:  # each sampled session at its config-3 length (cache contents N(0,1))
+            d = oracle.Decoder(cfg, params, absorbed=absorbed, proj=proj)
+            n = int(batch.ctx_len[b])
+            gen = np.random.default_rng(int(b))
+            d.latent[:, :n] = gen.standard_normal((cfg.n_layers, n, cfg.kv_lora_rank),
+                                                  np.float32)
+            d.rope[:, :n] = gen.standard_normal((cfg.n_layers, n, cfg.head_dim_rope),
+                                                np.float32)
+            out.append((d, n))
+        return out
 
-    def run(threads):
-        done, t0 = 0, time.perf_counter()
-        with cf.ThreadPoolExecutor(threads) as ex:
-            while True:
-                list(ex.map(one, range(len(decs))))
-                done += len(decs)
-                if time.perf_counter() - t0 >= seconds:
-                    break
-        return done / (time.perf_counter() - t0), done
+    def rewind(dn):
+        dn[0].position = dn[1]
 
-    many, n_many = run(cores)
-    single, n_single = run(1)
-    mean_ctx = float(np.mean([n for _, n in decs]))
-    out = {"value": round(many, 2), "unit": "tok/s", "cores": cores, "kind": "port",
-           "one_core_value": round(single, 2),
+    decs = decoders(True)
+    # Per-call cost estimate from one untimed call per session (sizes the repetitions).
+    est = []
+    for dn in decs:
+        est.append(time_it(0, 1, lambda: rewind(dn), lambda: dn[0].decode(1))[0])
+    longest = max(est) * 1e-3
+    # all cores: one session per thread, `reps` timed calls each after 2 warmup calls
+    reps = int(np.clip(seconds / longest, 5, 5000))
+    samples, lock = [], threading.Lock()
+    ready = threading.Barrier(len(decs) + 1)
+
+    def worker(dn):
+        time_it(2, 0, lambda: rewind(dn), lambda: dn[0].decode(1))
+        ready.wait()
+        got = time_it(0, reps, lambda: rewind(dn), lambda: dn[0].decode(1))
+        with lock:
+            samples.extend(got)
+
+    threads = [threading.Thread(target=worker, args=(dn,)) for dn in decs]
+    for t in threads:
+        t.start()
+    ready.wait()
+    t0 = time.perf_counter()
+    for t in threads:
+        t.join()
+    wall = time.perf_counter() - t0
+    samples.sort()
+    many_med, many_p95 = median_p95(samples)
+    many = len(samples) / wall
+    # 1 thread: the same sessions in turn
+    per = max(2, int(seconds / (sum(est) * 1e-3)))
+    one = []
+    t0 = time.perf_counter()
+    for dn in decs:
+        one += time_it(1, per, lambda: rewind(dn), lambda: dn[0].decode(1))
+    one.sort()
+    one_med, one_p95 = median_p95(one)
+    single = len(one) / sum(one) * 1e3
+    # 1 thread, non-absorbed (the reference's fallback baseline)
+    del decs
+    base = []
+    per_b = max(2, int(0.5 * seconds / (sum(est) * 1e-3)))
+    for dn in decoders(False):
+        base += time_it(1, per_b, lambda: rewind(dn), lambda: dn[0].decode(1))
+    base.sort()
+    base_med, base_p95 = median_p95(base)
+    mean_ctx = float(np.mean(batch.ctx_len[pick]))
+    out = {"value": round(many, 2), "unit": "tok/s", "cores": len(pick), "kind": "port",
+           "timing": "time_it (apps/bench_main.cpp:12-30): per decode call, warmup untimed, "
+                     "median and p95; value = timed calls / wall clock of the timed phase",
+           "median_ms": round(many_med, 3), "p95_ms": round(many_p95, 3),
+           "one_core": {"value": round(single, 2), "median_ms": round(one_med, 3),
+                        "p95_ms": round(one_p95, 3), "calls": len(one)},
+           "non_absorbed_one_core": {"baseline_median_ms": round(base_med, 3),
+                                     "p95_ms": round(base_p95, 3), "calls": len(base),
+                                     "speedup": round(base_med / one_med, 3)},
            "cpu_model": cpu_model(), "host_cores_visible": visible,
            "blas": f"{blas} (numpy's scipy_openblas64, standing in for Accelerate)"
                    if blas else "none found: unblocked C loops",
-           "sample": f"full decode step (oracle CpuDecoder restatement, fp32) of {len(decs)} "
+           "sample": f"full decode step (oracle CpuDecoder restatement, fp32) of {len(pick)} "
                      f"sessions spread over the batch's lengths (mean context {mean_ctx:.0f}): "
-                     f"{n_many} tokens on {cores} threads, one session per thread; "
-                     f"{n_single} tokens on 1 thread"}
-    if config2_trace is not None:
-        p16 = oracle.bits_to_f32(oracle.round_f16(params))
-        d = oracle.Decoder(cfg, p16, round_cache=True)
-        t0 = time.perf_counter()
-        want = d.prefill(config2_trace["prompt"])
-        prefill_s = time.perf_counter() - t0
-        pre_err = float(np.abs(config2_trace["prefill_logits"] - want).max())
-        dec_err, times = 0.0, []
-        for tok, got in zip(config2_trace["tokens"], config2_trace["decode_logits"]):
-            t0 = time.perf_counter()
-            want = d.decode(int(tok))
-            times.append(time.perf_counter() - t0)
-            dec_err = max(dec_err, float(np.abs(got - want).max()))
-        out["config2"] = {"prefill_max_abs_err": round(pre_err, 6),
-                          "decode_max_abs_err": round(dec_err, 6),
-                          "cpu_prefill_ms": round(prefill_s * 1e3, 1),
-                          "cpu_decode_ms_median": round(float(np.median(times)) * 1e3, 3),
-                          "sample": "config 2 replayed on the CPU path (1 thread): the same "
-                                    "1024-token prompt and the GPU run's 64 decode tokens, "
-                                    "fp16-rounded weights and cache"}
+                     f"{len(samples)} timed calls on {len(pick)} threads, one session per "
+                     f"thread; {len(one)} on 1 thread; {len(base)} non-absorbed on 1 thread"}
+    traces = traces or {}
+    acc = {}
+    if "config2" in traces:
+        acc["config2"] = check_config2(oracle, cfg, params, traces["config2"])
+    if "config3" in traces:
+        acc["config3"] = check_config3(oracle, cfg, params, batch, traces["config3"])
+    if "config4" in traces:
+        acc["config4"] = check_attention(oracle, traces["config4"], visible)
+    if "config5" in traces:
+        acc["config5"] = check_attention(oracle, traces["config5"], visible)
+    out["accuracy"] = acc
     oracle.use_blas(False)
     return out
+
+
+def check_config2(oracle, cfg, params, trace):
+    """Config 2 replayed on the CPU path (1 thread): the same prompt and the GPU run's
+    decode tokens on fp16-rounded weights and cache; the GPU logits' max error."""
+    p16 = oracle.bits_to_f32(oracle.round_f16(params))
+    d = oracle.Decoder(cfg, p16, round_cache=True)
+    t0 = time.perf_counter()
+    want = d.prefill(trace["prompt"])
+    prefill_s = time.perf_counter() - t0
+    pre_err = float(np.abs(trace["prefill_logits"] - want).max())
+    dec_err, times = 0.0, []
+    for tok, got in zip(trace["tokens"], trace["decode_logits"]):
+        t0 = time.perf_counter()
+        want = d.decode(int(tok))
+        times.append(time.perf_counter() - t0)
+        dec_err = max(dec_err, float(np.abs(got - want).max()))
+    return {"prefill_max_abs_err": round(pre_err, 6), "decode_max_abs_err": round(dec_err, 6),
+            "cpu_prefill_ms": round(prefill_s * 1e3, 1),
+            "cpu_decode_ms_median": round(float(np.median(times)) * 1e3, 3),
+            "sample": "config 2 replayed on the CPU path (1 thread): the same 1024-token "
+                      "prompt and the GPU run's 64 decode tokens, fp16-rounded weights and "
+                      "cache"}
+
+
+def check_config3(oracle, cfg, params, batch, trace):
+    """The timed config-3 step's logits for a sample of sessions against the CPU path's
+    decode of the same token over the same cache words and fp16-rounded weights."""
+    from cpp_inference_train_engine_amd.ops import latent_word, rope_word
+    p16 = oracle.bits_to_f32(oracle.round_f16(params))
+    proj = oracle.output_projection(cfg, p16)
+    ps, kv, rp = batch.page_size, batch.kv_rank, batch.rope_dim
+    lw = latent_word(np.arange(ps)[:, None], np.arange(kv)[None, :], ps, kv, rp)
+    rw = rope_word(np.arange(ps)[:, None], np.arange(rp)[None, :], ps, kv, rp)
+    err, greedy_same = 0.0, 0
+    for b, got in zip(trace["sessions"], trace["logits"]):
+        ids = batch.page_ids[batch.cu_pages[b]:batch.cu_pages[b + 1]]
+        n = int(batch.ctx_len[b])
+        t = np.arange(n)
+        d = oracle.Decoder(cfg, p16, absorbed=True, round_cache=True, proj=proj)
+        d.latent[:, :n] = oracle.bits_to_f32(batch.pages[:, ids[t // ps][:, None], lw[t % ps]])
+        d.rope[:, :n] = oracle.bits_to_f32(batch.pages[:, ids[t // ps][:, None], rw[t % ps]])
+        d.position = n
+        want = d.decode(int(trace["tokens"][b]))
+        err = max(err, float(np.abs(got - want).max()))
+        greedy_same += int(np.argmax(got) == np.argmax(want))
+    return {"logits_max_abs_err": round(err, 6), "sessions_checked": len(trace["sessions"]),
+            "greedy_equal": greedy_same,
+            "sample": "one more step of the benched graph's kernels after the timed loop; "
+                      f"{len(trace['sessions'])} of the 64 sessions spread over the lengths, "
+                      "each against the CPU path's decode (fp16 weights and cache words)"}
+
+
+def check_attention(oracle, trace, threads):
+    """Attention rows of a kernel leg against the oracle's paged attention over the same
+    16-bit words: max |gpu - cpu| and the tolerance excess (north star: 2e-3 + 1e-3|x|)."""
+    want = oracle.attention_paged(trace["H"], trace["kv"], trace["rope"], 64, trace["dtype"],
+                                  trace["cu_q"], trace["k_len"], trace["table"], trace["pages"],
+                                  oracle.bits_to_f32(trace["q_latent"], trace["dtype"]),
+                                  oracle.bits_to_f32(trace["q_rope"], trace["dtype"]),
+                                  trace["scale"], threads=threads)
+    got = trace["out"]
+    excess = float((np.abs(got - want) - (2e-3 + 1e-3 * np.abs(want))).max())
+    return {"max_abs_err": round(float(np.abs(got - want).max()), 6),
+            "max_tolerance_excess": round(excess, 6), "within_tolerance": excess <= 0,
+            "rows_checked": int(got.shape[0]), "sample": trace["sample"]}
 
 
 def config2_leg(mla, params, steps: int = 64, prompt_len: int = 1024):
@@ -313,10 +438,23 @@ def config4_leg(mla, torch, reps: int = 20, n_pools: int = 4):
         torch.cuda.synchronize()
         res[kind] = e0.elapsed_time(e1) * 1e3 / reps
     rb.read_info()
+    status = mla.decode_status(ws)
     tf = flops / res["prefill"] / 1e6
     gbs = dec_tokens * 288 / res["decode"] / 1e3
     pool_mb = pages.numel() * 2 / 1e6
     del pools
+    # The last calls' rows (decode rows from the one-launch decode, prefill rows from the
+    # chunked-prefill kernel) for the CPU leg's check, with the words they read.
+    table = np.full((len(b.q_len), b.max_pages), -1, np.int32)
+    for i in range(len(b.q_len)):
+        lst = b.page_ids[b.cu_pages[i]:b.cu_pages[i + 1]]
+        table[i, :len(lst)] = lst
+    trace = {"H": 8, "kv": 128, "rope": 16, "dtype": 0, "scale": 0.125,
+             "cu_q": np.concatenate([[0], np.cumsum(b.q_len)]).astype(np.int32),
+             "k_len": b.k_len.astype(np.int32), "table": table, "pages": b.pages[0],
+             "q_latent": b.q_latent, "q_rope": b.q_rope, "out": out.cpu().numpy(),
+             "sample": "every row of the last timed calls (4,096 prefill rows, 120 decode "
+                       "rows) against the oracle's paged attention"}
     return {"workload": "config 4 (one layer): 8 x 512-token chunks on contexts U[0,2048] + "
                         "120 log-normal decode sessions (median 2048, sigma 1, cap 16384), "
                         "4-page prefix shared by 64 sessions, fp16",
@@ -327,7 +465,7 @@ def config4_leg(mla, torch, reps: int = 20, n_pools: int = 4):
                                "frac": round(tf / 2500.0, 4)},
             "decode_call": {"us": round(res["decode"], 2), "cached_tokens": dec_tokens,
                             "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                            "one_launch": rb.placed}}
+                            "one_launch": rb.placed, "fused_merge_status": status}}, trace
 
 
 def config5_leg(mla, torch, reps: int = 5, split: int = 128):
@@ -368,13 +506,34 @@ def config5_leg(mla, torch, reps: int = 5, split: int = 128):
     tokens = int(shape.k_len.sum())
     gbs = tokens * 1152 / us / 1e3
     tf = tokens * 128 * 1088 * 2 / us / 1e6
+    # 8 sessions spread over the length range (the shortest and the longest included), read
+    # back with the pages they attend to, for the CPU leg's check.
+    order = np.argsort(shape.k_len)
+    picks = sorted(set(int(order[i]) for i in np.linspace(0, B - 1, 8).astype(int)))
+    lists = [shape.page_ids[shape.cu_pages[i]:shape.cu_pages[i + 1]] for i in picks]
+    flat = torch.from_numpy(np.concatenate(lists).astype(np.int64)).cuda()
+    table = np.full((len(picks), max(len(x) for x in lists)), -1, np.int32)
+    off = 0
+    for i, x in enumerate(lists):
+        table[i, :len(x)] = np.arange(off, off + len(x), dtype=np.int32)
+        off += len(x)
+    sel = torch.tensor(picks, device="cuda")
+    bits = lambda t: t[sel].view(torch.int16).cpu().numpy().view(np.uint16)
+    trace = {"H": 128, "kv": 512, "rope": 64, "dtype": 1, "scale": scale,
+             "cu_q": np.arange(len(picks) + 1, dtype=np.int32),
+             "k_len": shape.k_len[picks].astype(np.int32), "table": table,
+             "pages": pages[flat].view(torch.int16).cpu().numpy().view(np.uint16),
+             "q_latent": bits(ql), "q_rope": bits(qr), "out": out[sel].cpu().numpy(),
+             "sample": f"{len(picks)} of the 256 sessions spread over the lengths "
+                       f"({int(shape.k_len[picks].min())}..{int(shape.k_len[picks].max())} "
+                       "tokens) against the oracle's paged attention"}
     del pages, ws
     return {"workload": "config 5 (kernel only): H=128, kv_rank 512, rope 64, bf16 64-token "
                         "pages, 256 sessions, len U[8192,32768], N(0,1) contents",
             "kernels": "decode_wide_kernel + merge_kernel (mla_decode_attention)",
             "split_pages": split, "work_items": mw, "cached_tokens": tokens,
             "us": round(us, 1), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "tflops": round(tf, 1), "mfma_frac": round(tf / 2500.0, 4)}
+            "tflops": round(tf, 1), "mfma_frac": round(tf / 2500.0, 4)}, trace
 
 
 def copy_probe(torch, mib: int):
@@ -409,8 +568,8 @@ def main():
     from cpp_inference_train_engine_amd.workloads import MLA36M, model_params
     if args.only:
         legs = {"config2": lambda: config2_leg(mla, model_params(MLA36M, seed=0))[0],
-                "config4": lambda: config4_leg(mla, torch),
-                "config5": lambda: config5_leg(mla, torch),
+                "config4": lambda: config4_leg(mla, torch)[0],
+                "config5": lambda: config5_leg(mla, torch)[0],
                 "serve": lambda: {"greedy": serve_leg(mla, model_params(MLA36M, seed=0), 0.0),
                                   "sampled": serve_leg(mla, model_params(MLA36M, seed=0), 0.8)}}
         print(json.dumps({args.only: legs[args.only]()}), flush=True)
@@ -520,6 +679,20 @@ def main():
         torch.cuda.synchronize()
         us[k] = e0.elapsed_time(e1) * 1e3 / (args.kernel_reps * calls_per_replay)
     rb.read_info()
+    # One more step of the same kernels, eager, for the CPU leg's check of the logits.
+    step_tokens = tokens.cpu().numpy().copy()
+    rb = step()
+    torch.cuda.synchronize()
+    # Every fused merge of the timed steps, the attention replays and this step found its
+    # premises (the workspace's status word is sticky until cleared), else no number here
+    # is trusted.
+    status = mla.decode_status(ws)
+    if status:
+        raise SystemExit(f"decode status {status}: a fused merge's check failed; rerun with "
+                         "--no-placement")
+    sample3 = np.argsort(batch.k_len)[np.linspace(0, B - 1, 16).astype(int)]
+    trace3 = {"tokens": step_tokens, "sessions": [int(b) for b in sample3],
+              "logits": logits[torch.from_numpy(sample3).cuda()].cpu().numpy()}
     bytes_layer = batch.cache_bytes_per_layer()
     gbs = {k: bytes_layer / (v * 1e-6) / 1e9 for k, v in us.items()}
     # The dominant kernel as the step runs it: with placement, decode_page_kernel with the
@@ -547,6 +720,15 @@ def main():
                    "sessions": B, "cached_tokens_per_layer": int(batch.k_len.sum()),
                    "split_pages": info[1], "work_items": info[0],
                    "xcd_placement": placed, "work_slots": max_work,
+                   "fused_merge_status": status,
+                   "cache_bytes": int(cache.pages.numel()) * 2,
+                   "cache_bytes_read_per_step": N_LAYERS * bytes_layer,
+                   "cache_bytes_note": "cache_bytes: the 10 layer page pools (64-token fp16 "
+                                       "pages); the reference's decode record gives "
+                                       "n_layers x max_sequence_length x kv_width x 2 per "
+                                       "session (bench_main.cpp:410-415), "
+                                       f"{N_LAYERS * MLA36M['max_sequence_length'] * 144 * 2} "
+                                       "B for this model",
                    "timing": "eager" if args.no_graph else "hip graph"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -567,18 +749,23 @@ def main():
             "frac": round(gbs["two_launch"] / HBM_PEAK_GBS, 4)},
     }
     model.close()
-    trace = None
+    traces = {"config3": trace3}
     if not args.no_secondary:
-        result["config2"], trace = config2_leg(mla, params)
-        result["config4"] = config4_leg(mla, torch)
-        result["config5"] = config5_leg(mla, torch)
+        result["config2"], traces["config2"] = config2_leg(mla, params)
+        result["config4"], traces["config4"] = config4_leg(mla, torch)
+        result["config5"], traces["config5"] = config5_leg(mla, torch)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(batch, params, args.cpu_seconds, trace)
-        if trace is not None:  # the CPU path's verdict on config 2's logits
-            c2 = result["cpu_baseline"].pop("config2")
+        result["cpu_baseline"] = cpu_baseline(batch, params, args.cpu_seconds, traces)
+        # The CPU path's verdict on each timed leg's outputs, beside its timing.
+        acc = result["cpu_baseline"].pop("accuracy")
+        result["accuracy"] = acc.pop("config3")
+        if "config2" in acc:
+            c2 = acc.pop("config2")
             result["config2"]["decode_max_abs_err"] = c2["decode_max_abs_err"]
             result["config2"]["prefill_max_abs_err"] = c2["prefill_max_abs_err"]
             result["config2"]["cpu_path"] = c2
+        for k, v in acc.items():
+            result[k]["accuracy"] = v
     print(json.dumps(result), flush=True)
 
 

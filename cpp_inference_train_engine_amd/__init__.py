@@ -18,9 +18,11 @@ MLA_OK = 0
 ERROR_NAMES = {1: "invalid_argument", 2: "io_error", 3: "unsupported", 4: "out_of_memory",
                5: "gpu_error", 6: "numerical_error", 7: "unavailable"}
 DTYPE_F16, DTYPE_BF16 = 0, 1
-WORK_DESC_INTS, WORK_PAGES, MAX_WORK = 8, 8, 65535
+WORK_DESC_INTS, WORK_PAGES, MAX_WORK, INFO_INTS = 8, 8, 65535, 8
 DECODE_FORCE_GENERIC = 1
 DECODE_FUSED_MERGE = 2
+DECODE_STATUS_XCD, DECODE_STATUS_UNPLACED = 1, 2
+DECODE_WORKSPACE_HEAD, DECODE_STATUS_OFFSET = 1280, 1024
 PLACE_MAX_SESSIONS = 256
 
 
@@ -40,8 +42,12 @@ _SIGNATURES = {
     "mla_abi_version": (C.c_int, []),
     "mla_build_metadata": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 4 +
                            [C.c_int] * 8 + [C.c_void_p] * 11),
+    "mla_build_metadata_placed": (C.c_int, [C.c_void_p, C.c_int] + [C.c_void_p] * 4 +
+                                  [C.c_int] * 8 + [C.c_void_p] * 11),
     "mla_xcd_placement_supported": (C.c_int, []),
+    "mla_testing_fail_decode_status": (C.c_int, [C.c_int]),
     "mla_read_metadata_info": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "mla_decode_status": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]),
     "mla_append_latent": (C.c_int, [C.c_void_p] + [C.c_int] * 5 + [C.c_void_p] * 3 +
                           [C.c_int, C.c_void_p]),
     "mla_decode_workspace_bytes": (C.c_size_t, [C.c_int] * 4),
@@ -174,8 +180,8 @@ def stream_handle(stream=None) -> int | None:
 
 from .ops import (  # noqa: E402  (re-exported operator interface)
     PagedLatentCache, RaggedBatch, append_latent, build_metadata, decode_attention,
-    decode_merge, decode_partials, decode_workspace, decode_workspace_bytes, placed_work_slots,
-    prefill_attention, xcd_count)
+    decode_merge, decode_partials, decode_status, decode_workspace, decode_workspace_bytes,
+    placed_work_slots, prefill_attention, xcd_count)
 from . import ops  # noqa: E402
 
 from .model import (HipModel, ModelConfig, config_hash, config_parameter_count,  # noqa: E402

@@ -4,6 +4,7 @@
 #include "mla_hip.h"
 #include "mla_internal.hpp"
 
+#include <atomic>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -28,11 +29,85 @@ int gpu_status(hipError_t e, const char* what) {
 
 using namespace mla;
 
+static_assert(MLA_INFO_INTS == kInfoInts && MLA_DECODE_WORKSPACE_HEAD == kMergeCounterBytes &&
+                  MLA_DECODE_STATUS_OFFSET == kStatusOffset &&
+                  MLA_DECODE_STATUS_XCD == kStatusXcd &&
+                  MLA_DECODE_STATUS_UNPLACED == kStatusUnplaced &&
+                  MLA_PLACE_MAX_SESSIONS == kPlaceMaxSessions,
+              "mla_hip.h and mla_internal.hpp agree");
+
 extern "C" {
 
 const char* mla_last_error(void) { return g_last_error.c_str(); }
 
-int mla_abi_version(void) { return 1; }
+int mla_abi_version(void) { return 2; }
+
+}  // extern "C"
+
+namespace {
+
+// Shared by mla_build_metadata and mla_build_metadata_placed: n_xcd = 0 (session order)
+// or the XCD count the work list is laid out for.
+int build_metadata(const char* fn, void* stream, int B, const int32_t* ctx_len,
+                   const int32_t* q_len, const int32_t* cu_pages, const int32_t* page_ids,
+                   int page_size, int max_pages, int num_pool_pages, int split_pages,
+                   int target_blocks, int max_work, int max_rows, int n_xcd,
+                   int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int32_t* page_table,
+                   int32_t* slot_mapping, int32_t* num_splits, int32_t* cu_splits,
+                   int32_t* work_session, int32_t* work_split, int32_t* work_desc,
+                   int32_t* work_pages, int32_t* info) {
+    if (!info || !cu_seqlens_q || !cu_seqlens_k || !cu_splits || !cu_pages ||
+        (B > 0 && (!ctx_len || !q_len || !num_splits || (max_pages > 0 && !page_table))) ||
+        (max_work > 0 && (!work_session || !work_split || !work_desc || !work_pages)) ||
+        (max_rows > 0 && !slot_mapping))
+        return fail(MLA_ERR_INVALID_ARGUMENT, std::string(fn) + ": null buffer");
+    if ((long long)B * max_pages > (1LL << 40))
+        return fail(MLA_ERR_INVALID_ARGUMENT, std::string(fn) + ": page table too large");
+    MetadataArgs a{B, ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num_pool_pages,
+                   split_pages, target_blocks, max_work, max_rows, cu_seqlens_q, cu_seqlens_k,
+                   page_table, slot_mapping, num_splits, cu_splits, work_session, work_split,
+                   work_desc, work_pages, info, n_xcd};
+    return gpu_status(launch_build_metadata(a, static_cast<hipStream_t>(stream)), fn);
+}
+
+bool scalars_ok(int B, int page_size, int max_pages, int num_pool_pages, int split_pages,
+                int target_blocks, int max_work, int max_rows) {
+    return B >= 0 && page_size >= 1 && max_pages >= 0 && num_pool_pages >= 0 &&
+           split_pages >= 0 && target_blocks >= 1 && max_work >= 0 && max_work <= kMaxWork &&
+           max_rows >= 0;
+}
+
+// Per device: 0 unknown, else 1 + the XCD count (1 = the probe failed), and the reason of
+// a failure.
+std::mutex g_place_mu;
+int g_place_known[64];
+std::string g_place_reason[64];
+
+// Status reads still to be failed on purpose (mla_testing_fail_decode_status).
+std::atomic<int> g_forced_failures{0};
+
+}  // namespace
+
+namespace mla {
+
+int32_t decode_head_status(const int32_t* head) {
+    int32_t st = head[kStatusOffset / sizeof(int32_t)];
+    for (int i = 0; i < kPlaceMaxSessions; ++i)
+        if (head[i] != 0) {  // a session nobody merged (or merged early from a stale count)
+            st |= kStatusXcd;
+            break;
+        }
+    for (int f = g_forced_failures.load(); f > 0;)
+        if (g_forced_failures.compare_exchange_weak(f, f - 1)) {
+            st |= kStatusXcd;
+            break;
+        }
+    return st;
+}
+
+}  // namespace mla
+
+extern "C" {
 
 int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
                        const int32_t* cu_pages, const int32_t* page_ids, int page_size,
@@ -42,8 +117,8 @@ int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_
                        int32_t* num_splits, int32_t* cu_splits, int32_t* work_session,
                        int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
                        int32_t* info) {
-    if (B < 0 || page_size < 1 || max_pages < 0 || num_pool_pages < 0 || split_pages < 0 ||
-        target_blocks < 1 || max_work < 0 || max_work > kMaxWork || max_rows < 0 ||
+    if (!scalars_ok(B, page_size, max_pages, num_pool_pages, split_pages, target_blocks,
+                    max_work, max_rows) ||
         (placement != 0 && placement != 1))
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: invalid scalar argument");
     int n_xcd = 0;
@@ -57,47 +132,67 @@ int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_
                         "mla_build_metadata: XCD placement unavailable on this device (" +
                             g_last_error + ")");
     }
-    if (!info || !cu_seqlens_q || !cu_seqlens_k || !cu_splits || !cu_pages ||
-        (B > 0 && (!ctx_len || !q_len || !num_splits || (max_pages > 0 && !page_table))) ||
-        (max_work > 0 && (!work_session || !work_split || !work_desc || !work_pages)) ||
-        (max_rows > 0 && !slot_mapping))
-        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: null buffer");
-    if ((long long)B * max_pages > (1LL << 40))
-        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_build_metadata: page table too large");
-    MetadataArgs a{B, ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num_pool_pages,
-                   split_pages, target_blocks, max_work, max_rows, cu_seqlens_q, cu_seqlens_k,
-                   page_table, slot_mapping, num_splits, cu_splits, work_session, work_split,
-                   work_desc, work_pages, info, n_xcd};
-    return gpu_status(launch_build_metadata(a, static_cast<hipStream_t>(stream)),
-                      "mla_build_metadata");
+    return build_metadata("mla_build_metadata", stream, B, ctx_len, q_len, cu_pages, page_ids,
+                          page_size, max_pages, num_pool_pages, split_pages, target_blocks,
+                          max_work, max_rows, n_xcd, cu_seqlens_q, cu_seqlens_k, page_table,
+                          slot_mapping, num_splits, cu_splits, work_session, work_split,
+                          work_desc, work_pages, info);
+}
+
+int mla_build_metadata_placed(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
+                              const int32_t* cu_pages, const int32_t* page_ids, int page_size,
+                              int max_pages, int num_pool_pages, int split_pages,
+                              int target_blocks, int max_work, int max_rows, int n_xcds,
+                              int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int32_t* page_table,
+                              int32_t* slot_mapping, int32_t* num_splits, int32_t* cu_splits,
+                              int32_t* work_session, int32_t* work_split, int32_t* work_desc,
+                              int32_t* work_pages, int32_t* info) {
+    if (!scalars_ok(B, page_size, max_pages, num_pool_pages, split_pages, target_blocks,
+                    max_work, max_rows) ||
+        n_xcds < 1 || n_xcds > kPlaceMaxXcds)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "mla_build_metadata_placed: invalid scalar argument (n_xcds in 1.." +
+                        std::to_string(kPlaceMaxXcds) + ")");
+    if (B > kPlaceMaxSessions)
+        return fail(MLA_ERR_UNSUPPORTED, "mla_build_metadata_placed: XCD placement takes at most " +
+                                             std::to_string(kPlaceMaxSessions) + " sessions");
+    return build_metadata("mla_build_metadata_placed", stream, B, ctx_len, q_len, cu_pages,
+                          page_ids, page_size, max_pages, num_pool_pages, split_pages,
+                          target_blocks, max_work, max_rows, n_xcds, cu_seqlens_q, cu_seqlens_k,
+                          page_table, slot_mapping, num_splits, cu_splits, work_session,
+                          work_split, work_desc, work_pages, info);
 }
 
 int mla_xcd_placement_supported(void) {
-    static std::mutex mu;
-    static int known[64];  // per device: 0 unknown, else 1 + the XCD count (0 = fails)
-    static std::string reason[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
         fail(MLA_ERR_GPU, "mla_xcd_placement_supported: no current device");
         return 0;
     }
-    std::lock_guard<std::mutex> lk(mu);
-    if (!known[dev]) {
-        reason[dev] = probe_xcd_placement();
-        known[dev] = 1 + (reason[dev].empty() ? xcd_count() : 0);
+    std::lock_guard<std::mutex> lk(g_place_mu);
+    if (!g_place_known[dev]) {
+        g_place_reason[dev] = probe_xcd_placement();
+        g_place_known[dev] = 1 + (g_place_reason[dev].empty() ? xcd_count() : 0);
     }
-    if (known[dev] == 1) {
-        fail(MLA_ERR_UNSUPPORTED, reason[dev]);
+    if (g_place_known[dev] == 1) {
+        fail(MLA_ERR_UNSUPPORTED, g_place_reason[dev]);
         return 0;
     }
-    return known[dev] - 1;
+    return g_place_known[dev] - 1;
+}
+
+int mla_testing_fail_decode_status(int count) {
+    if (count < 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_testing_fail_decode_status: count < 0");
+    g_forced_failures.store(count);
+    return MLA_OK;
 }
 
 int mla_read_metadata_info(void* stream, const int32_t* info, int32_t* host_info) {
     if (!info || !host_info)
         return fail(MLA_ERR_INVALID_ARGUMENT, "mla_read_metadata_info: null buffer");
     auto s = static_cast<hipStream_t>(stream);
-    int st = gpu_status(hipMemcpyAsync(host_info, info, 4 * sizeof(int32_t),
+    int st = gpu_status(hipMemcpyAsync(host_info, info, kInfoInts * sizeof(int32_t),
                                        hipMemcpyDeviceToHost, s),
                         "mla_read_metadata_info");
     if (st)
@@ -131,6 +226,30 @@ size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, i
     if (max_work <= 0 || max_sessions < 0 || n_heads <= 0 || kv_rank <= 0)
         return 0;
     return decode_workspace_size(max_work, n_heads, kv_rank);
+}
+
+int mla_decode_status(void* stream, void* workspace, size_t workspace_bytes, int clear,
+                      int32_t* status) {
+    if (!status)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_status: invalid argument");
+    if (!workspace && workspace_bytes == 0)  // the no-allocation array of this device
+        if (int st = noalloc_scratch(&workspace, &workspace_bytes))
+            return st;
+    if (!workspace || workspace_bytes < kMergeCounterBytes)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "mla_decode_status: invalid argument");
+    auto s = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    int32_t head[kStatusOffset / sizeof(int32_t) + 1];
+    hipError_t e = hipMemcpyAsync(head, ws, sizeof(head), hipMemcpyDeviceToHost, s);
+    // A failed check can leave counts in the merge counters: clearing resets both.
+    if (e == hipSuccess && clear)
+        e = hipMemsetAsync(ws, 0, kMergeCounterBytes, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (int st = gpu_status(e, "mla_decode_status"))
+        return st;
+    *status = decode_head_status(head);
+    return MLA_OK;
 }
 
 }  // extern "C"
@@ -197,6 +316,30 @@ bool use_generic(const DecodeArgs& a, const void* workspace, int flags) {
 
 }  // namespace
 
+namespace mla {
+
+// MLA_DECODE_FUSED_MERGE needs placed metadata, which holds at most kPlaceMaxSessions
+// sessions on a device that passed the placement probe; the kernel then checks that the
+// metadata was placed for this device's XCD count (a.xcd_n).
+int fused_checks(DecodeArgs& a, int flags, const char* fn) {
+    if (!(flags & MLA_DECODE_FUSED_MERGE))
+        return MLA_OK;
+    if (a.B > kPlaceMaxSessions)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": MLA_DECODE_FUSED_MERGE takes at most " +
+                        std::to_string(kPlaceMaxSessions) + " sessions (placed metadata)");
+    if (!a.fused_merge)
+        return MLA_OK;  // a kernel that leaves the merge to merge_kernel: any metadata works
+    a.xcd_n = mla_xcd_placement_supported();
+    if (a.xcd_n < 1)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    std::string(fn) + ": MLA_DECODE_FUSED_MERGE needs XCD placement, which this "
+                                      "device does not support (" + g_last_error + ")");
+    return MLA_OK;
+}
+
+}  // namespace mla
+
 extern "C" {
 
 #define MLA_DECODE_PARAMS                                                                       \
@@ -220,6 +363,8 @@ int mla_decode_attention(MLA_DECODE_PARAMS) {
     const auto s = static_cast<hipStream_t>(stream);
     const bool generic = use_generic(a, workspace, flags);
     a.fused_merge = (flags & MLA_DECODE_FUSED_MERGE) && decode_fuses_merge(a, generic);
+    if (int st = fused_checks(a, flags, "mla_decode_attention"))
+        return st;
     if (int st = gpu_status(launch_decode_partials(a, dtype, generic, s), "mla_decode_attention"))
         return st;
     if (a.fused_merge)
@@ -235,6 +380,8 @@ int mla_decode_partials(MLA_DECODE_PARAMS) {
         return MLA_OK;
     const bool generic = use_generic(a, workspace, flags);
     a.fused_merge = (flags & MLA_DECODE_FUSED_MERGE) && decode_fuses_merge(a, generic);
+    if (int st = fused_checks(a, flags, "mla_decode_partials"))
+        return st;
     return gpu_status(launch_decode_partials(a, dtype, generic, static_cast<hipStream_t>(stream)),
                       "mla_decode_partials");
 }

@@ -66,9 +66,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // so all items of the session ran on this XCD and their partials sit in its L2: each
 // item waits for its own stores to be acknowledged, then bumps the session's counter
 // with an atomic in that L2 (no device-scope traffic); the item that brings it to
-// num_splits knows every partial has landed, resets the counter for the next launch and
-// folds the partials (log-sum-exp, as merge_kernel) into the session's row.  The partial
-// stores are plain ones so that the lines stay in the L2.  No item waits on another.
+// num_splits knows every partial has landed, takes the session's counts back out of the
+// counter for the next launch and folds the partials (log-sum-exp, as merge_kernel) into
+// the session's row.  The partial stores are plain ones so that the lines stay in the L2.
+// No item waits on another.
 // Folds the partials of head h in slots slot0 .. slot0 + N - 1 (columns c..c+3 of their o
 // rows) into the running log-sum-exp state (M, L, O).  Plain loads: the lines were written
 // in this launch on other CUs of this XCD, and this CU's L1 holds no copy of them (it is
@@ -103,6 +104,11 @@ __device__ __forceinline__ void fold_partials(const DecodeArgs& a, long long slo
     M = Mn;
 }
 
+// Sets `bit` of the decode status word (read by the host through mla_decode_status).
+__device__ __forceinline__ void raise_status(const DecodeArgs& a, int bit) {
+    __hip_atomic_fetch_or(a.status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int KV, int THREADS>
 __device__ __forceinline__ void fused_merge_tail(const DecodeArgs& a, int s, int row, int ns,
                                                  long long first) {
@@ -111,12 +117,19 @@ __device__ __forceinline__ void fused_merge_tail(const DecodeArgs& a, int s, int
     __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are in L2
     __syncthreads();
     if (tid == 0) {
+        // If the items of a session ran on several XCDs (the dispatch did not keep slots of
+        // one residue mod n on one XCD), no L2 counts all of them: nobody merges and the
+        // counter stays nonzero after the launch, which is what the host's status check
+        // (mla_decode_status) looks for.
         const int old = __hip_atomic_fetch_add(a.merge_count + s, 1, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_WORKGROUP);
         s_last = old == ns - 1;
+        // Take the session's ns counts back out (an atomic add, not a store of 0: a count
+        // that was already wrong when the launch began must survive it, so the host's check
+        // still sees it, and no increment racing with the reset can be erased).
         if (old == ns - 1)
-            __hip_atomic_store(a.merge_count + s, 0, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_fetch_add(a.merge_count + s, -ns, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     __syncthreads();
     if (!s_last)
@@ -147,6 +160,25 @@ __device__ __forceinline__ void fused_merge_tail(const DecodeArgs& a, int s, int
         if (a.lse && c == 0)
             a.lse[(long long)row * a.H + h] = (M + __log2f(L)) * kLn2;
     }
+}
+
+// The fused flag over metadata that is not placed for this device (info[4] != xcd_n): the
+// session's items ran on several XCDs, so they do not merge.  Each leaves its partial (as
+// the two-launch path does: mla_decode_merge completes the rows), the first item sets the
+// session's rows to NaN so that no stale row passes for a result, and the call is flagged.
+template <int KV, int THREADS>
+__device__ __forceinline__ void unplaced_tail(const DecodeArgs& a, int row, bool first_item) {
+    const int tid = threadIdx.x;
+    if (tid == 0)
+        raise_status(a, kStatusUnplaced);
+    if (!first_item)
+        return;
+    const float nan = __builtin_nanf("");
+    for (int e = tid; e < a.H * KV; e += THREADS)
+        a.out[(long long)row * a.H * KV + e] = nan;
+    if (a.lse)
+        for (int h = tid; h < a.H; h += THREADS)
+            a.lse[(long long)row * a.H + h] = nan;
 }
 
 // Split index of a work item from its descriptor: items cover `split` pages each, the
@@ -211,7 +243,9 @@ void decode_page_kernel(DecodeArgs a) {
     const int H = a.H, npool = a.num_pool_pages;
     const uint16_t* const pool = a.pages;
     const float scale_log2 = a.scale_log2;
-    asm volatile("" ::"s"(pid[0]), "s"(H), "s"(npool), "s"(pool), "s"(scale_log2));
+    // The XCD count the metadata was placed for (the fused merge's premise, checked at the end).
+    const int placed_n = FUSED ? a.info[kInfoPlacement] : 0;
+    asm volatile("" ::"s"(pid[0]), "s"(H), "s"(npool), "s"(pool), "s"(scale_log2), "s"(placed_n));
     const int s = d[0];
     if (s < 0 || d[7] != 1)
         return;  // past the last item (or a failed build), or not a decode row
@@ -441,9 +475,13 @@ void decode_page_kernel(DecodeArgs a) {
         }
     }
     if constexpr (FUSED)
-        if (ns > 1)  // the session's first partial slot: this item's, less its split index
-            fused_merge_tail<KV, THREADS>(a, s, row, ns,
-                                          slot - item_split_index(kl, p_begin, p_end, ns, PS));
+        if (ns > 1) {  // the session's first partial slot: this item's, less its split index
+            const int sp = item_split_index(kl, p_begin, p_end, ns, PS);
+            if (placed_n == a.xcd_n)
+                fused_merge_tail<KV, THREADS>(a, s, row, ns, slot - sp);
+            else
+                unplaced_tail<KV, THREADS>(a, row, sp == 0);
+        }
 }
 
 // ------------------------------------------------------------- generic ----

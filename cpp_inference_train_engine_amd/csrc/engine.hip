@@ -28,6 +28,10 @@ namespace mla {
 namespace {
 
 constexpr int kSplitPages = 4;  // MLA_DECODE_SPLIT_PAGES
+// The pinned host words a step reads back: the metadata info, the decode workspace's head
+// (merge counters and status word), then the greedy token of each session.
+constexpr int kHeadInts = MLA_DECODE_STATUS_OFFSET / 4 + 1;
+constexpr int kHostInfo = 0, kHostHead = MLA_INFO_INTS, kHostNext = kHostHead + kHeadInts + 7;
 
 struct Session {
     bool active = false;
@@ -69,7 +73,8 @@ struct Engine {
     int32_t* h_in = nullptr;
     float* h_logits = nullptr;
     float* h_logits_all = nullptr;  // [max_rows x vocab] pinned, with d_logits_all
-    int32_t* h_out = nullptr;  // info[4] then next tokens[max_sessions]
+    int32_t* h_out = nullptr;  // info, decode status, next tokens (kHostInfo .. kHostNext)
+    uint64_t reruns = 0;       // steps rerun through the two-launch path (failed fused check)
     std::vector<void*> dev_allocs, host_allocs;
 
     ~Engine() {
@@ -290,43 +295,64 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
     int32_t *d_ctx = E->d_in, *d_q = d_ctx + n, *d_cup = d_ctx + 2 * n, *d_tok = d_ctx + 3 * n + 1;
     int32_t *d_pos = d_tok + rows, *d_ids = d_pos + rows;
     int st = gpu_status(e, fn);
+    // Metadata build, forward and read-back of one attempt; placed: the work list XCD-placed
+    // and each layer's decode attention one launch.
+    auto attempt = [&](bool placed) {
+        int rc = mla_build_metadata(E->stream, n, d_ctx, d_q, d_cup, d_ids, E->page_size,
+                                    E->max_pages, E->num_pages, kSplitPages, 1024, E->work_cap,
+                                    E->max_rows, placed ? 1 : 0, E->cu_q, E->cu_k, E->table,
+                                    E->slots, E->nsplit, E->cu_split, E->w_sess, E->w_split,
+                                    E->w_desc, E->w_pages, E->info);
+        if (!rc) {
+            const MetaPtrs md{E->cu_q,     E->cu_k,    E->table,   E->slots,
+                              E->nsplit,   E->cu_split, E->w_desc, E->w_pages,
+                              E->info,     E->max_pages, E->num_pages, E->work_cap,
+                              placed ? MLA_DECODE_FUSED_MERGE : 0};
+            rc = model_forward(static_cast<Model*>(E->model), E->stream, (int)rows, d_tok, d_pos,
+                               n, max_q, md, E->layer_pools.data(), E->workspace, E->ws_bytes,
+                               d_logits, d_next, all_rows);
+        }
+        if (rc)
+            return rc;
+        hipError_t err = hipMemcpyAsync(E->h_out + kHostInfo, E->info,
+                                        MLA_INFO_INTS * sizeof(int32_t), hipMemcpyDeviceToHost,
+                                        E->stream);
+        if (err == hipSuccess && placed)
+            err = hipMemcpyAsync(E->h_out + kHostHead, E->workspace, kHeadInts * sizeof(int32_t),
+                                 hipMemcpyDeviceToHost, E->stream);
+        if (err == hipSuccess && !all_rows)
+            err = hipMemcpyAsync(E->h_out + kHostNext, d_next, n * sizeof(int32_t),
+                                 hipMemcpyDeviceToHost, E->stream);
+        if (err == hipSuccess && logits)
+            err = hipMemcpyAsync(h_logits, d_logits,
+                                 (size_t)out_rows * c.vocab_size * sizeof(float),
+                                 hipMemcpyDeviceToHost, E->stream);
+        if (err == hipSuccess)
+            err = hipStreamSynchronize(E->stream);
+        E->meta_launches += 1;
+        E->copies += 2 + placed + !all_rows + (logits != nullptr);
+        E->host_waits += 1;
+        return gpu_status(err, fn);
+    };
     const bool placed = placed_fits(E, n, h_ctx, h_q);
     if (!st)
-        st = mla_build_metadata(E->stream, n, d_ctx, d_q, d_cup, d_ids, E->page_size,
-                                E->max_pages, E->num_pages, kSplitPages, 1024, E->work_cap,
-                                E->max_rows, placed ? 1 : 0, E->cu_q, E->cu_k, E->table, E->slots, E->nsplit,
-                                E->cu_split, E->w_sess, E->w_split, E->w_desc, E->w_pages,
-                                E->info);
-    if (!st) {
-        const MetaPtrs md{E->cu_q,     E->cu_k,    E->table,   E->slots,
-                          E->nsplit,   E->cu_split, E->w_desc, E->w_pages,
-                          E->info,     E->max_pages, E->num_pages, E->work_cap,
-                          placed ? MLA_DECODE_FUSED_MERGE : 0};
-        st = model_forward(static_cast<Model*>(E->model), E->stream, (int)rows, d_tok, d_pos, n,
-                           max_q, md, E->layer_pools.data(), E->workspace, E->ws_bytes,
-                           d_logits, d_next, all_rows);
+        st = attempt(placed);
+    if (!st && placed && decode_head_status(E->h_out + kHostHead) != 0) {
+        // A fused merge's premise failed (a session's items did not meet in one L2: this
+        // device does not dispatch as probed).  Stop placing, clear the workspace head
+        // (status and merge counters) and run the step again through the two-launch path;
+        // its appends rewrite the same values into the same slots.
+        E->n_xcd = 0;
+        ++E->reruns;
+        st = gpu_status(hipMemsetAsync(E->workspace, 0, MLA_DECODE_WORKSPACE_HEAD, E->stream),
+                        fn);
+        if (!st)
+            st = attempt(false);
     }
-    if (!st) {
-        e = hipMemcpyAsync(E->h_out, E->info, 4 * sizeof(int32_t), hipMemcpyDeviceToHost,
-                           E->stream);
-        if (e == hipSuccess && !all_rows)
-            e = hipMemcpyAsync(E->h_out + 4, d_next, n * sizeof(int32_t),
-                               hipMemcpyDeviceToHost, E->stream);
-        if (e == hipSuccess && logits)
-            e = hipMemcpyAsync(h_logits, d_logits,
-                               (size_t)out_rows * c.vocab_size * sizeof(float),
-                               hipMemcpyDeviceToHost, E->stream);
-        if (e == hipSuccess)
-            e = hipStreamSynchronize(E->stream);
-        E->meta_launches += 1;
-        E->copies += 2 + !all_rows + (logits != nullptr);
-        E->host_waits += 1;
-        st = gpu_status(e, fn);
-    }
-    if (!st && E->h_out[0] < 0)
+    if (!st && E->h_out[kHostInfo] < 0)
         st = fail(MLA_ERR_INVALID_ARGUMENT,
                   std::string(fn) + ": ragged metadata rejected session " +
-                      std::to_string(E->h_out[1]));
+                      std::to_string(E->h_out[kHostInfo + 1]));
     if (st) {
         (void)hipStreamSynchronize(E->stream);
         rollback();
@@ -340,10 +366,10 @@ int step(Engine* E, int n, const int* ids, const int* counts, const uint16_t* to
         S.revision = E->revision;
         if (all_rows)
             continue;
-        finite = finite && E->h_out[4 + i] != -1;
-        open = open && E->h_out[4 + i] != -2;
+        finite = finite && E->h_out[kHostNext + i] != -1;
+        open = open && E->h_out[kHostNext + i] != -2;
         if (next)
-            next[i] = E->h_out[4 + i];
+            next[i] = E->h_out[kHostNext + i];
     }
     if (logits && logits != h_logits)
         std::memcpy(logits, h_logits, (size_t)out_rows * c.vocab_size * sizeof(float));
@@ -421,7 +447,7 @@ int mla_engine_create(const mla_model_config* config, const float* params, int m
     if (e == hipSuccess) e = E->dalloc(E->w_split, E->work_cap);
     if (e == hipSuccess) e = E->dalloc(E->w_desc, (size_t)E->work_cap * MLA_WORK_DESC_INTS);
     if (e == hipSuccess) e = E->dalloc(E->w_pages, (size_t)E->work_cap * MLA_WORK_PAGES);
-    if (e == hipSuccess) e = E->dalloc(E->info, 4);
+    if (e == hipSuccess) e = E->dalloc(E->info, MLA_INFO_INTS);
     if (e == hipSuccess) e = E->dalloc(E->d_next, S);
     if (e == hipSuccess) e = E->dalloc(E->d_logits, S * V);
     if (e == hipSuccess) {
@@ -433,7 +459,7 @@ int mla_engine_create(const mla_model_config* config, const float* params, int m
         e = hipMemset(E->workspace, 0, E->ws_bytes);
     if (e == hipSuccess) e = E->halloc(E->h_in, E->in_cap);
     if (e == hipSuccess) e = E->halloc(E->h_logits, S * V);
-    if (e == hipSuccess) e = E->halloc(E->h_out, 4 + S);
+    if (e == hipSuccess) e = E->halloc(E->h_out, kHostNext + S);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess)
         return bail(gpu_status(e, "mla_engine_create"));
@@ -620,6 +646,7 @@ int mla_engine_stats(void* engine, uint64_t* stats) {
     stats[2] = E->meta_launches + model_launches(static_cast<Model*>(E->model));
     stats[3] = E->copies;
     stats[4] = E->revision;
+    stats[5] = E->reruns;
     return MLA_OK;
 }
 

@@ -77,12 +77,8 @@ constexpr int kMetaUnroll = 16;  // page-table entries whose loads a thread issu
 __device__ void write_error(const MetadataArgs& a, int session) {
     for (int w = threadIdx.x; w < a.max_work; w += kMetaThreads)
         a.work_desc[(long long)w * kWorkDescInts] = -1;
-    if (threadIdx.x == 0) {
-        a.info[0] = -1;
-        a.info[1] = session;
-        a.info[2] = 0;
-        a.info[3] = 0;
-    }
+    if (threadIdx.x < kInfoInts)
+        a.info[threadIdx.x] = threadIdx.x == 0 ? -1 : threadIdx.x == 1 ? session : 0;
 }
 
 // ceil(x / d) for x >= 0 and d >= 1, in 32-bit arithmetic when both are below 2^31.
@@ -101,6 +97,8 @@ __device__ __forceinline__ long long ceil_div_nn(long long x, long long d) {
 // round of n ranks and no two XCDs' pages differ by more than the largest session's.  A
 // session's items then take its XCD's next slots: item sp of the session of round q on
 // XCD x lands in slot x + n * (k + sp), k the items of that XCD's sessions of rounds < q.
+// There are ceil(B / n) rounds (up to 256 when n = 1); wave x takes them 64 at a time,
+// one lane per round, carrying the running item count from pass to pass.
 __device__ long long wave_scan_incl(long long v);  // inclusive sum over the wave's lanes
 
 struct Placement {
@@ -108,8 +106,8 @@ struct Placement {
         k0[kPlaceMaxSessions], cnt[kPlaceMaxXcds];
 };
 
-// All threads call it (B <= kPlaceMaxSessions <= 64 n, 1 <= n <= kPlaceMaxXcds); q(b), ctx(b)
-// and cus(b) read the session inputs and the work-item prefix.  Ends with a barrier.
+// All threads call it (B <= kPlaceMaxSessions, 1 <= n <= kPlaceMaxXcds <= kMetaWaves); q(b),
+// ctx(b) and cus(b) read the session inputs and the work-item prefix.  Ends with a barrier.
 template <typename Q, typename C, typename S>
 __device__ void place_sessions(int B, int n, int page_size, Q q, C ctx, S cus, Placement& p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -127,18 +125,24 @@ __device__ void place_sessions(int B, int n, int page_size, Q q, C ctx, S cus, P
         p.order[r] = b;
     }
     __syncthreads();
-    if (wave < n) {  // wave x: lane q holds XCD x's session of round q
-        const int x = wave, qr = lane;
-        const int r = qr * n + ((qr & 1) ? n - 1 - x : x);
-        const int b = r < B ? p.order[r] : 0;
-        const long long items = r < B ? cus(b + 1) - cus(b) : 0;
-        const long long incl = wave_scan_incl(items);
-        if (r < B) {
-            p.bin[b] = x;
-            p.k0[b] = (int32_t)(incl - items);
+    if (wave < n) {  // wave x: lane l holds XCD x's session of round q0 + l
+        const int x = wave;
+        long long carry = 0;  // items of XCD x's sessions of earlier passes
+        for (int q0 = 0; q0 * n < B; q0 += 64) {
+            const int qr = q0 + lane;
+            const int r = qr * n + ((qr & 1) ? n - 1 - x : x);
+            const bool real = r < B;  // rounds past the last, or the last round's gaps
+            const int b = real ? p.order[r] : 0;
+            const long long items = real ? cus(b + 1) - cus(b) : 0;
+            const long long incl = carry + wave_scan_incl(items);
+            if (real) {
+                p.bin[b] = x;
+                p.k0[b] = (int32_t)(incl - items);
+            }
+            carry = __shfl(incl, 63, 64);
         }
-        if (lane == 63)
-            p.cnt[x] = (int32_t)incl;
+        if (lane == 0)
+            p.cnt[x] = (int32_t)carry;
     }
     __syncthreads();
 }
@@ -362,6 +366,9 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_kernel(MetadataAr
         a.info[1] = (int32_t)split;
         a.info[2] = (int32_t)total_q;
         a.info[3] = (int32_t)total_k;
+        a.info[kInfoPlacement] = n;
+        for (int k = kInfoPlacement + 1; k < kInfoInts; ++k)
+            a.info[k] = 0;
     }
 }
 
@@ -570,6 +577,9 @@ __global__ __launch_bounds__(kMetaThreads) void build_metadata_lds_kernel(Metada
         a.info[1] = (int32_t)split;
         a.info[2] = (int32_t)total_q;
         a.info[3] = (int32_t)total_k;
+        a.info[kInfoPlacement] = n;
+        for (int k = kInfoPlacement + 1; k < kInfoInts; ++k)
+            a.info[k] = 0;
     }
 }
 
@@ -628,14 +638,15 @@ int xcd_count() {
     return n;
 }
 
-// Whether workgroup w of a launch runs on XCD w % n on the current device: ids of 16
-// rounds of n workgroups, launched twice.  Empty string when it holds, else the reason.
+// Whether the workgroups w of a launch with one residue w % n run on one XCD, and the n
+// residues on n different XCDs, on the current device: ids of 16 rounds of n workgroups,
+// launched twice.  Empty string when it holds, else the reason.  (Which XCD takes
+// residue 0 differs between hardware queues: each queue starts its round-robin on an XCD
+// of its own, which placement does not depend on.)
 std::string probe_xcd_placement() {
     const int n = xcd_count();
     if (n < 1 || n > kPlaceMaxXcds)
         return "XCD count " + std::to_string(n) + " outside 1.." + std::to_string(kPlaceMaxXcds);
-    if (n == 1)
-        return "";
     const int G = 16 * n;
     int32_t* d = nullptr;
     std::vector<int32_t> h(G);
@@ -649,7 +660,8 @@ std::string probe_xcd_placement() {
             break;
         }
         for (int w = 0; w < G && why.empty(); ++w)
-            if (h[w] != h[w % n] || (w < n && std::count(h.begin(), h.begin() + n, h[w]) != 1))
+            if (h[w] != h[w % n] || (w < n && std::count(h.begin(), h.begin() + n, h[w]) != 1) ||
+                h[w] < 0 || h[w] > 15)
                 why = "workgroup " + std::to_string(w) + " ran on XCD " + std::to_string(h[w]);
     }
     (void)hipFree(d);

@@ -20,6 +20,10 @@ namespace mla {
 constexpr int kWorkDescInts = 8;  // MLA_WORK_DESC_INTS
 constexpr int kWorkPages = 8;     // MLA_WORK_PAGES
 constexpr int kMaxWork = 65535;   // MLA_MAX_WORK
+// info[kInfoInts] of a build: {W, split, total_q, total_k, n (the XCD count the work list
+// is placed for, 0 = session order), 0, 0, 0}, or {-1, first bad session, 0, ...}.
+constexpr int kInfoInts = 8;      // MLA_INFO_INTS
+constexpr int kInfoPlacement = 4;
 
 struct MetadataArgs {
     int B;
@@ -30,8 +34,8 @@ struct MetadataArgs {
     // XCD placement of the work list: the number of XCDs n (0 = work items in session
     // order).  With n > 0 every session's items sit in consecutive slots x + n k of one
     // XCD x (workgroup w of a launch runs on XCD w % n), sessions dealt to the XCDs by
-    // pages read, largest first, in rounds of n (see place_sessions).
-    // B <= kPlaceMaxSessions.
+    // pages read, largest first, in rounds of n (see place_sessions); info[4] records n.
+    // B <= kPlaceMaxSessions, n <= kPlaceMaxXcds.
     int placement;
 };
 constexpr int kPlaceMaxSessions = 256;  // MLA_PLACE_MAX_SESSIONS
@@ -58,7 +62,16 @@ struct DecodeArgs {
     // merge_count[B] (in the workspace, zero between launches) counts finished items.
     int fused_merge;
     int32_t* merge_count;
+    // What the fused kernel checks: the metadata must record placement for this device's
+    // xcd_n XCDs (info[4]); otherwise it raises kStatusUnplaced in *status and does not merge.
+    int xcd_n;
+    int32_t* status;
 };
+// Bits of the decode status (MLA_DECODE_STATUS_*).  kStatusXcd is not raised by a kernel:
+// the host derives it from merge counters left nonzero after a call (see
+// decode_head_status).
+constexpr int kStatusXcd = 1;       // a split session's items did not all meet in one L2
+constexpr int kStatusUnplaced = 2;  // fused flag over metadata not placed for this device
 
 // Chunked-prefill attention (sessions with q_len > 1, causal within the chunk).
 struct PrefillArgs {
@@ -70,13 +83,15 @@ struct PrefillArgs {
 };
 
 hipError_t launch_build_metadata(const MetadataArgs& a, hipStream_t stream);
-// Workspace of decode attention: the fused merge's per-session counters first, in a block
-// of fixed size (fused calls have placed metadata, B <= kPlaceMaxSessions), so that they
-// keep their place whatever max_work and B a later call on the same buffer has; then the
-// split partials, 256-byte aligned: part_o [max_work][H][kv_rank] and part_ml, whose
-// (m, l) pairs of one slot take [H][2] floats padded to whole 128-byte lines
-// (part_ml_stride floats per slot), so that no cache line holds two slots' pairs.
-constexpr size_t kMergeCounterBytes = kPlaceMaxSessions * sizeof(int32_t);
+// Workspace of decode attention: a head block of fixed size first -- the fused merge's
+// per-session counters (fused calls have placed metadata, B <= kPlaceMaxSessions), then
+// the status word on a line of its own -- so that both keep their place whatever max_work
+// and B a later call on the same buffer has; then the split partials, 256-byte aligned:
+// part_o [max_work][H][kv_rank] and part_ml, whose (m, l) pairs of one slot take [H][2]
+// floats padded to whole 128-byte lines (part_ml_stride floats per slot), so that no
+// cache line holds two slots' pairs.
+constexpr size_t kStatusOffset = kPlaceMaxSessions * sizeof(int32_t);  // MLA_DECODE_STATUS_OFFSET
+constexpr size_t kMergeCounterBytes = kStatusOffset + 256;
 __host__ __device__ inline int part_ml_stride(int n_heads) { return (2 * n_heads + 31) & ~31; }
 inline size_t decode_partial_bytes(int max_work, int n_heads, int kv_rank) {
     const size_t b = (size_t)max_work *
@@ -89,13 +104,17 @@ inline size_t decode_workspace_size(int max_work, int n_heads, int kv_rank) {
 inline void decode_workspace_layout(void* ws, int max_work, int n_heads, int kv_rank,
                                     DecodeArgs& a) {
     a.merge_count = static_cast<int32_t*>(ws);
+    a.status = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + kStatusOffset);
     a.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + kMergeCounterBytes);
     a.part_ml = a.part_o + (size_t)max_work * n_heads * kv_rank;
 }
-// XCDs of the current device (0 if unknown), and whether its dispatch places workgroup w
-// on XCD w % n (empty string) or why not.
+// XCDs of the current device (0 if unknown), and whether its dispatch keeps the
+// workgroups w of a launch with one residue w % n on one XCD (empty string) or why not.
 int xcd_count();
 std::string probe_xcd_placement();
+// The decode status of a workspace head copied to the host (kMergeCounterBytes / 4
+// words): the status word, plus kStatusXcd when a merge counter was left nonzero (capi.hip).
+int32_t decode_head_status(const int32_t* head);
 hipError_t launch_append(const AppendArgs& a, int dtype, hipStream_t stream);
 // Decode kernel only (MFMA page kernel, or the generic one when force_generic or the
 // shape is outside it): final rows of one-item sessions, partials of the others.

@@ -392,6 +392,8 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     pa.lse = nullptr;
     const bool generic = (reinterpret_cast<uintptr_t>(workspace) & 15) != 0;
     a.fused_merge = (md.flags & MLA_DECODE_FUSED_MERGE) && decode_fuses_merge(a, generic);
+    if (int bad = fused_checks(a, md.flags, "model forward"))
+        return bad;
     // decode (+ the split merge unless the decode launch merges itself)
     const int attn_launches = md.max_work > 0 && B > 0 ? 2 - a.fused_merge : 0;
     hipError_t e = launch_embed(s, M->layers[0].attn_norm, st);

@@ -12,9 +12,11 @@
 
 constexpr size_t kScratchBytes = (size_t)MLA_NOALLOC_SCRATCH_MIB << 20;
 
-// Partials (o[kv_rank] and (m, l) per work item and head).  Every value a merge reads is
-// written first by its work item in the same call, so nothing needs clearing.  In host
-// code this name is not a device address: kernels get the address from scratch_on().
+// The workspace of the decode: a head of merge counters and the status word (zero at
+// load, and every fused call without a failed check leaves the counters zero), then the
+// partials (o[kv_rank] and (m, l) per work item and head), which every merge reads only
+// after its work items wrote them in the same call.  In host code this name is not a
+// device address: kernels get the address from scratch_on().
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
@@ -43,6 +45,20 @@ int scratch_on(int device, void** out) {
 }
 
 }  // namespace
+
+namespace mla {
+
+// The no-allocation array of the current device (its head holds the fused merge's
+// counters and the decode status word, as a workspace's does).
+int noalloc_scratch(void** out, size_t* bytes) {
+    int device = -1;
+    if (hipError_t e = hipGetDevice(&device); e != hipSuccess)
+        return gpu_status(e, "mla_decode_status");
+    *bytes = kScratchBytes;
+    return scratch_on(device, out);
+}
+
+}  // namespace mla
 
 extern "C" {
 

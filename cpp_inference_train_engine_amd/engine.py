@@ -101,9 +101,10 @@ class HipEngine:
 
     def stats(self) -> dict:
         """mla_engine_stats: Execution::stats's counters (execution.hpp:25-27), engine-wide."""
-        v = (C.c_uint64 * 5)()
+        v = (C.c_uint64 * 6)()
         check(lib().mla_engine_stats(self.handle, v))
-        keys = ("graph_submissions", "host_waits", "kernel_submissions", "copies", "revision")
+        keys = ("graph_submissions", "host_waits", "kernel_submissions", "copies", "revision",
+                "fused_reruns")
         return dict(zip(keys, [int(x) for x in v]))
 
     def forward(self, ids, batch: int, sequence: int) -> np.ndarray:

@@ -158,7 +158,7 @@ Status HipEngine::update_weights(std::span<const float> params) {
 }
 
 ExecutionStats HipEngine::stats() const {
-    std::uint64_t v[5] = {};
+    std::uint64_t v[6] = {};
     if (mla_engine_stats(h_, v) != MLA_OK)
         return {};
     return ExecutionStats{v[0], v[1], v[2]};

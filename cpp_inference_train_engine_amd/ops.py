@@ -11,8 +11,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
-from . import (DECODE_FUSED_MERGE, DTYPE_BF16, DTYPE_F16, MAX_WORK, PLACE_MAX_SESSIONS,
-               WORK_DESC_INTS, WORK_PAGES, check, lib, ptr, stream_handle)
+from . import (DECODE_FUSED_MERGE, DTYPE_BF16, DTYPE_F16, INFO_INTS, MAX_WORK,
+               PLACE_MAX_SESSIONS, WORK_DESC_INTS, WORK_PAGES, check, lib, ptr, stream_handle)
 
 
 def _torch():
@@ -41,13 +41,14 @@ class RaggedBatch:
     work_desc: object
     work_pages: object
     info: object
-    placed: bool = False  # XCD-placed work list (decode merges inside its launch)
+    placed: bool = False  # XCD-placed for this device (decode merges inside its launch)
     host_info: list = field(default_factory=list)
 
     def read_info(self, stream=None):
-        """Synchronise and return [W, split, total_q, total_k]; raises on a bad batch."""
+        """Synchronise and return [W, split, total_q, total_k, n_xcd placed for, 0, 0, 0];
+        raises on a bad batch."""
         import numpy as np
-        h = np.zeros(4, np.int32)
+        h = np.zeros(INFO_INTS, np.int32)
         check(lib().mla_read_metadata_info(stream_handle(stream), ptr(self.info), h.ctypes.data))
         self.host_info = h.tolist()
         return self.host_info
@@ -78,12 +79,15 @@ def placed_work_slots(ctx_len, q_len, page_size: int, split_pages: int, n_xcd: i
 def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size: int, max_pages: int,
                    num_pool_pages: int, split_pages: int = 0, target_blocks: int = 1024,
                    max_work: int | None = None, max_rows: int | None = None,
-                   placement: bool = False, stream=None) -> RaggedBatch:
+                   placement: bool = False, placement_xcds: int | None = None,
+                   stream=None) -> RaggedBatch:
     """(a) Build cu_seqlens, padded page tables, slot mapping and the block-to-session
     map on the GPU (one launch).  Inputs are device int32 tensors.  ``placement``: lay
     the work list out so that each session's items run on one XCD (B <= 256; max_work
     must hold ``placed_work_slots``); decode attention over it then merges the split
-    partials inside its launch."""
+    partials inside its launch.  ``placement_xcds``: the placed layout for that many XCDs
+    instead of this device's (mla_build_metadata_placed; no fused merge over it unless
+    the count is the device's)."""
     torch = _torch()
     dev = ctx_len.device
     B = int(ctx_len.numel())
@@ -101,14 +105,19 @@ def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size: int, max_pages
         cu_splits=torch.empty(B + 1, **i32), work_session=torch.empty(max_work, **i32),
         work_split=torch.empty(max_work, **i32),
         work_desc=torch.empty(max_work * WORK_DESC_INTS, **i32),
-        work_pages=torch.empty(max_work * WORK_PAGES, **i32), info=torch.empty(4, **i32),
-        placed=bool(placement))
-    check(lib().mla_build_metadata(
+        work_pages=torch.empty(max_work * WORK_PAGES, **i32),
+        info=torch.empty(INFO_INTS, **i32),
+        placed=bool(placement) or (placement_xcds is not None and placement_xcds == xcd_count()))
+    if placement_xcds is not None:
+        fn, place = lib().mla_build_metadata_placed, int(placement_xcds)
+    else:
+        fn, place = lib().mla_build_metadata, int(bool(placement))
+    check(fn(
         stream_handle(stream), B, ptr(ctx_len), ptr(q_len), ptr(cu_pages), ptr(page_ids),
         page_size, max_pages, num_pool_pages, split_pages, target_blocks, max_work, max_rows,
-        int(bool(placement)), ptr(rb.cu_seqlens_q), ptr(rb.cu_seqlens_k), ptr(rb.page_table), ptr(rb.slot_mapping),
-        ptr(rb.num_splits), ptr(rb.cu_splits), ptr(rb.work_session), ptr(rb.work_split),
-        ptr(rb.work_desc), ptr(rb.work_pages), ptr(rb.info)))
+        place, ptr(rb.cu_seqlens_q), ptr(rb.cu_seqlens_k), ptr(rb.page_table),
+        ptr(rb.slot_mapping), ptr(rb.num_splits), ptr(rb.cu_splits), ptr(rb.work_session),
+        ptr(rb.work_split), ptr(rb.work_desc), ptr(rb.work_pages), ptr(rb.info)))
     return rb
 
 
@@ -153,10 +162,22 @@ def decode_workspace_bytes(max_work: int, max_sessions: int, n_heads: int, kv_ra
 
 def decode_workspace(max_work: int, max_sessions: int, n_heads: int, kv_rank: int,
                      device="cuda"):
-    """Decode workspace (split partials)."""
+    """Decode workspace (head block of merge counters and status word, split partials),
+    zeroed."""
     torch = _torch()
     n = max(decode_workspace_bytes(max_work, max_sessions, n_heads, kv_rank), 4)
     return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def decode_status(workspace, clear: bool = False, stream=None) -> int:
+    """Synchronise and return the decode status word of ``workspace`` (OR of
+    DECODE_STATUS_XCD / DECODE_STATUS_UNPLACED raised by fused calls since it was last
+    cleared; 0 when every fused merge's premises held).  ``clear`` also zeroes the head."""
+    import numpy as np
+    h = np.zeros(1, np.int32)
+    check(lib().mla_decode_status(stream_handle(stream), ptr(workspace), int(workspace.numel()),
+                                  int(bool(clear)), h.ctypes.data))
+    return int(h[0])
 
 
 def _decode_call(fn, batch: RaggedBatch, pages, q_latent, q_rope, scale, kv_rank, rope_dim,
@@ -169,6 +190,9 @@ def _decode_call(fn, batch: RaggedBatch, pages, q_latent, q_rope, scale, kv_rank
         workspace = decode_workspace(batch.max_work, batch.B, H, kv_rank, q_latent.device)
     if fused is None:
         fused = batch.placed
+    if fused and not batch.placed:
+        raise ValueError("fused decode needs metadata placed for this device's XCDs "
+                         "(build_metadata(..., placement=True))")
     if fused:
         flags |= DECODE_FUSED_MERGE
     check(getattr(lib(), fn)(
@@ -233,8 +257,8 @@ def prefill_attention(batch: RaggedBatch, pages, q_latent, q_rope, scale: float,
 
 
 __all__ = ["RaggedBatch", "build_metadata", "PagedLatentCache", "append_latent",
-           "decode_workspace_bytes", "decode_workspace", "decode_attention", "decode_partials",
-           "decode_merge", "prefill_attention", "DTYPE_F16", "DTYPE_BF16"]
+           "decode_workspace_bytes", "decode_workspace", "decode_status", "decode_attention",
+           "decode_partials", "decode_merge", "prefill_attention", "DTYPE_F16", "DTYPE_BF16"]
 
 
 # ---------------------------------------------------------------- page layout ----

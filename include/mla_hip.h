@@ -67,7 +67,10 @@ extern "C" {
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* mla_last_error(void);
-/* ABI version of this library. */
+/* ABI version of this library: 2.  Version 1 had info[4], no placement argument of
+ * mla_build_metadata, no `flags` of mla_model_step / mla_model_forward, and a decode
+ * workspace without the head block (counters and status word) described at
+ * mla_decode_attention; a caller built against version 1 must not bind version 2. */
 int mla_abi_version(void);
 
 /* ------------------------------------------------------------------ (a)
@@ -93,9 +96,10 @@ int mla_abi_version(void);
  * the session, partial slot = cu_splits[session] + split index, q_len; session
  * -1 marks every empty slot, and all items of a failed build),
  * work_pages[max_work * MLA_WORK_PAGES] (ids of each item's first pages, -1
- * past its end) and info[4]:
- *     ok:    {W (work items), split_pages used, total_q, total_k}
- *     error: {-1, first offending session, 0, 0}
+ * past its end) and info[MLA_INFO_INTS]:
+ *     ok:    {W (work items), split_pages used, total_q, total_k,
+ *             n (XCDs the work list is placed for, 0 = session order), 0, 0, 0}
+ *     error: {-1, first offending session, 0, 0, 0, 0, 0, 0}
  * A session is invalid when q_len<0, ctx_len<0, it lists more than
  * max_pages pages or fewer than ceil((ctx+q)/page_size), a page id is out of
  * range, a running total exceeds INT32_MAX, or the work/row capacity is
@@ -118,6 +122,7 @@ int mla_abi_version(void);
  * placed metadata may then merge the split partials inside its launch
  * (MLA_DECODE_FUSED_MERGE). */
 #define MLA_PLACE_MAX_SESSIONS 256
+#define MLA_INFO_INTS 8
 #define MLA_WORK_DESC_INTS 8
 #define MLA_WORK_PAGES 8
 #define MLA_MAX_WORK 65535
@@ -130,13 +135,28 @@ int mla_build_metadata(void* stream, int B, const int32_t* ctx_len, const int32_
                        int32_t* work_split, int32_t* work_desc, int32_t* work_pages,
                        int32_t* info);
 
-/* Synchronises `stream`, copies info[4] to host_info and returns
+/* mla_build_metadata with the work list placed for an explicit count of n_xcds XCDs
+ * (1..8) instead of the current device's, and without the device probe: for tests of
+ * the layout and for hosts that prepare work for another device.  Decode attention with
+ * MLA_DECODE_FUSED_MERGE refuses to merge over metadata placed for another count than the
+ * device's (see mla_decode_status).  No reference counterpart. */
+int mla_build_metadata_placed(void* stream, int B, const int32_t* ctx_len, const int32_t* q_len,
+                              const int32_t* cu_pages, const int32_t* page_ids, int page_size,
+                              int max_pages, int num_pool_pages, int split_pages,
+                              int target_blocks, int max_work, int max_rows, int n_xcds,
+                              int32_t* cu_seqlens_q, int32_t* cu_seqlens_k, int32_t* page_table,
+                              int32_t* slot_mapping, int32_t* num_splits, int32_t* cu_splits,
+                              int32_t* work_session, int32_t* work_split, int32_t* work_desc,
+                              int32_t* work_pages, int32_t* info);
+
+/* Synchronises `stream`, copies info[MLA_INFO_INTS] to host_info and returns
  * MLA_ERR_INVALID_ARGUMENT (naming the session) if the build failed. */
 int mla_read_metadata_info(void* stream, const int32_t* info, int32_t* host_info);
 
-/* The XCD count n >= 1 of the current device if it dispatches workgroup w of a
- * launch on XCD w % n (the premise of XCD placement), else 0 with the reason in
- * mla_last_error().  The first call per device runs a probe kernel and
+/* The XCD count n >= 1 of the current device if its dispatch keeps the workgroups w of a
+ * launch with one residue w % n on one XCD, the n residues on n XCDs (the premise of XCD
+ * placement; which XCD takes residue 0 may differ between hardware queues), else 0 with
+ * the reason in mla_last_error().  The first call per device runs a probe kernel and
  * synchronises: call it before any stream capture that builds placed metadata. */
 int mla_xcd_placement_supported(void);
 
@@ -169,17 +189,46 @@ int mla_append_latent(void* stream, int T, int kv_rank, int rope_dim, int page_s
  * mla_decode_partials and mla_decode_merge, below).  With MLA_DECODE_FUSED_MERGE
  * and XCD-placed metadata (mla_build_metadata placement = 1) the MFMA page
  * kernel merges instead: the last item of a split session to finish combines
- * the session's partials through its XCD's L2, and the call is one launch (the
- * flag on metadata that is not placed gives wrong rows).  `workspace` (device)
- * must hold mla_decode_workspace_bytes(max_work, B, H, kv_rank) bytes: a fixed
- * block of MLA_PLACE_MAX_SESSIONS int32 counters of the fused merge first (zero
- * them before the workspace's first fused call; every call leaves them zero),
- * then the partials.  Calls that share a
+ * the session's partials through its XCD's L2, and the call is one launch.  The flag
+ * needs B <= MLA_PLACE_MAX_SESSIONS and a device that passes
+ * mla_xcd_placement_supported (MLA_ERR_INVALID_ARGUMENT otherwise).  Its premises are
+ * checked, and a failed check never passes silently (mla_decode_status reports it):
+ *   - metadata not placed for this device's XCD count (info[4]) is not merged: the kernel
+ *     sets the rows of split sessions to NaN, leaves their partials for mla_decode_merge
+ *     and raises MLA_DECODE_STATUS_UNPLACED in the workspace's status word;
+ *   - items of one session that ran on several XCDs (a dispatch that broke the premise
+ *     mla_xcd_placement_supported checked) cannot all count in one L2, so no item merges
+ *     the session and its merge counter stays nonzero after the call: reported as
+ *     MLA_DECODE_STATUS_XCD.  Rerun the call without the flag after clearing the
+ *     workspace head (mla_decode_status with clear = 1).
+ * `workspace` (device) must hold mla_decode_workspace_bytes(max_work, B, H, kv_rank)
+ * bytes: a head block of MLA_DECODE_WORKSPACE_HEAD bytes (MLA_PLACE_MAX_SESSIONS int32
+ * counters of the fused merge, then the status word at byte MLA_DECODE_STATUS_OFFSET;
+ * zero the head before the workspace's first call; every call whose checks pass leaves
+ * the counters zero), then the partials.  Calls that share a
  * workspace must be ordered on one stream.  The production kernel runs one wave per page of a work item,
  * so metadata built with split_pages == MLA_DECODE_SPLIT_PAGES keeps a whole
  * item in flight. */
 #define MLA_DECODE_SPLIT_PAGES 4
+#define MLA_DECODE_WORKSPACE_HEAD 1280
+#define MLA_DECODE_STATUS_OFFSET 1024
+#define MLA_DECODE_STATUS_XCD 1      /* a split session's items did not meet in one L2 */
+#define MLA_DECODE_STATUS_UNPLACED 2 /* fused flag over metadata not placed for this device */
 size_t mla_decode_workspace_bytes(int max_work, int max_sessions, int n_heads, int kv_rank);
+/* Synchronises `stream` and returns in *status the decode status of `workspace` since it
+ * was last cleared (0: every fused merge's premises held): the MLA_DECODE_STATUS_UNPLACED
+ * bit the kernels raised, and MLA_DECODE_STATUS_XCD when a merge counter is nonzero.
+ * clear = 1 also zeroes the workspace head (status and merge counters), stream-ordered.
+ * workspace = NULL with workspace_bytes = 0 reads the current device's array of
+ * mla_decode_attention_noalloc.  Not for use under stream capture.  No reference
+ * counterpart; the reference turns backend failures into gpu_error
+ * (mps_backend.mm:1050-1062). */
+int mla_decode_status(void* stream, void* workspace, size_t workspace_bytes, int clear,
+                      int32_t* status);
+/* Test hook for the callers' recovery paths (the engine's rerun of a step): the next
+ * `count` reads of a decode status -- mla_decode_status and the engine's check after each
+ * placed step -- report MLA_DECODE_STATUS_XCD besides what the device left.  0 disarms. */
+int mla_testing_fail_decode_status(int count);
 /* The metadata arguments (cu_seqlens_q, page_table, num_splits, cu_splits,
  * work_desc, work_pages, info, max_work) are the outputs of one
  * mla_build_metadata call for this batch. */
@@ -320,7 +369,9 @@ int mla_model_update_weights(void* model, const float* params, uint64_t* revisio
  * maxima of the ids not banned, see mla_model_set_banned), -1 when a logit is not
  * finite (numerical_error), -2 when every id is banned.  flags: MLA_DECODE_FUSED_MERGE
  * when the metadata was built XCD-placed (the decode attention of each layer is then
- * one launch, see mla_decode_attention), else 0. */
+ * one launch, see mla_decode_attention: check mla_decode_status on `workspace` after
+ * the step, and rerun it without the flag if a bit is set -- the step's appends are
+ * idempotent), else 0. */
 int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
                    const int32_t* positions, const int32_t* cu_seqlens_q,
                    const int32_t* page_table, int max_pages, int num_pool_pages,
@@ -432,9 +483,10 @@ int mla_engine_set_banned(void* engine, const uint16_t* ids, size_t n);
  * restarts it.  Empty sessions and new prompts are unaffected. */
 int mla_engine_update_weights(void* engine, const float* params);
 /* Execution::stats (include/mini_mla/execution.hpp:25-27,33), engine-wide counters since
- * creation: stats[5] = {model forwards submitted (graph_submissions), host waits on the
+ * creation: stats[6] = {model forwards submitted (graph_submissions), host waits on the
  * engine's stream (host_waits), kernels launched (metal_kernel_submissions), copies
- * issued, weight revision}. */
+ * issued, weight revision, steps rerun through the two-launch decode because a fused
+ * merge's check failed (after the first such step the engine stops placing work)}. */
 int mla_engine_stats(void* engine, uint64_t* stats);
 /* Execution::forward(ids, batch, sequence) (execution.hpp:38-39) for inference: the
  * logits of EVERY position of `batch` independent sequences of `sequence` tokens (ids

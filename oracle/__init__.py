@@ -299,7 +299,7 @@ def build_metadata(ctx_len, q_len, cu_pages, page_ids, page_size, max_pages, num
         num_splits=np.zeros(B, np.int32), cu_splits=np.zeros(B + 1, np.int32),
         work_session=np.zeros(max_work, np.int32), work_split=np.zeros(max_work, np.int32),
         work_desc=np.zeros((max_work, 8), np.int32), work_pages=np.zeros((max_work, 8), np.int32),
-        info=np.zeros(4, np.int32))
+        info=np.zeros(8, np.int32))
     st = lib().orc_build_metadata(
         B, _p(ctx_len), _p(q_len), _p(cu_pages), _p(page_ids if page_ids.size else
                                                     np.zeros(1, np.int32)),

@@ -748,9 +748,10 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
 static int metadata_error(int max_work, int32_t* work_desc, int32_t* info, int session) {
     for (int w = 0; w < max_work; ++w)
         work_desc[(size_t)w * 8] = -1;
+    for (int k = 0; k < 8; ++k)
+        info[k] = 0;
     info[0] = -1;
     info[1] = session;
-    info[2] = info[3] = 0;
     return 1;
 }
 
@@ -882,6 +883,8 @@ int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,
     info[1] = (int32_t)split;
     info[2] = (int32_t)total_q;
     info[3] = (int32_t)total_k;
+    info[4] = n; /* the XCD count the work list is placed for (0: session order) */
+    info[5] = info[6] = info[7] = 0;
     return 0;
 }
 

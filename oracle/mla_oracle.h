@@ -117,10 +117,11 @@ int orc_attention_paged(int B, int H, int kv_rank, int rope_dim, int page_size, 
  * work_desc[max_work x 8] = {session, first query row, k_len, page_begin,
  * page_end, num_splits, partial slot cu_splits[session] + split, q_len} (session -1
  * for every empty slot and for every item of a failed build), work_pages[max_work x 8] =
- * first 8 page ids of each item (-1 past its end), info[4] =
- * {W, split_pages, total_q, total_k} or {-1, first offending session, 0, 0}.
+ * first 8 page ids of each item (-1 past its end), info[8] =
+ * {W, split_pages, total_q, total_k, placement_xcds, 0, 0, 0} or
+ * {-1, first offending session, 0, ...}.
  * placement_xcds = n > 0 lays the work list out over n XCDs (each session's items
- * in slots x, x + n, ..; {-1, B, 0, 0} when max_work cannot hold it); 0 keeps
+ * in slots x, x + n, ..; {-1, B, 0, ...} when max_work cannot hold it); 0 keeps
  * session order (item w = cu_splits[session] + split).
  * Returns 0, or 1 (invalid argument). */
 int orc_build_metadata(int B, const int32_t* ctx_len, const int32_t* q_len,

@@ -308,6 +308,41 @@ def test_batched_step_equals_single_sessions(gpu):
 
 
 @pytest.mark.gpu
+def test_failed_fused_check_reruns_the_step_unplaced(gpu):
+    """A placed step whose decode status comes back nonzero (forced from the host with
+    mla_testing_fail_decode_status: the state a broken XCD placement leaves) is rerun by the
+    engine through the two-launch decode: the same logits as an engine whose checks passed,
+    one rerun counted, and placement off for the engine's later steps."""
+    _, params, _ = _models(MLA36M, seed=5)
+    prompts = [_prompt(n, 16384, seed=n) for n in (700, 1300, 90, 2000)]
+    engines = [_engine(gpu, MLA36M, params, max_sessions=4, max_rows=4096, num_pages=120)
+               for _ in range(2)]
+    sess = [[e.session() for _ in prompts] for e in engines]
+    for e, ss in zip(engines, sess):
+        e.step(ss, [list(p) for p in prompts])
+    nxt = [[11], [12], [13], [14]]
+    want, _ = engines[0].step(sess[0], nxt)
+    assert engines[0].stats()["fused_reruns"] == 0
+    gpu.check(gpu.lib().mla_testing_fail_decode_status(1))
+    try:
+        _say("engine step with a failed fused check")
+        got, _ = engines[1].step(sess[1], nxt)
+    finally:
+        gpu.check(gpu.lib().mla_testing_fail_decode_status(0))
+    assert engines[1].stats()["fused_reruns"] == 1
+    # The two-launch merge sums the partials in another order, and the step's fp16
+    # activations carry that last-bit difference to the logits: the engines' parity bound.
+    np.testing.assert_allclose(got, want, rtol=0, atol=LOGIT_ATOL)
+    assert (np.argmax(got, 1) == np.argmax(want, 1)).all()
+    want2, _ = engines[0].step(sess[0], [[21], [22], [23], [24]])
+    got2, _ = engines[1].step(sess[1], [[21], [22], [23], [24]])
+    assert engines[0].stats()["fused_reruns"] == 0 and engines[1].stats()["fused_reruns"] == 1
+    np.testing.assert_allclose(got2, want2, rtol=0, atol=LOGIT_ATOL)
+    for e in engines:
+        e.close()
+
+
+@pytest.mark.gpu
 def test_fork_shares_pages_and_copies_on_write(gpu):
     """A forked session shares its source's pages; the first append into the shared
     partial page copies it, so both sessions continue as if prefilled separately."""

@@ -133,7 +133,7 @@ def test_metadata_errors_match_oracle(gpu, orc, case):
 
 def test_metadata_empty_batch(gpu):
     rb = _gpu_metadata(gpu, [], [], [0], [], 64, 4, 10, 0, 16, 8, 8)
-    assert rb.read_info() == [0, 1, 0, 0]
+    assert rb.read_info() == [0, 1, 0, 0, 0, 0, 0, 0]
 
 
 # -------------------------------------------------------------- append ----

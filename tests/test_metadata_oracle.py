@@ -70,7 +70,8 @@ def py_metadata(ctx, q, cu_pages, page_ids, ps, max_pages, pool, split_pages, ta
             slots.append(ids[pos // ps] * ps + pos % ps)
     return dict(cu_seqlens_q=cuq, cu_seqlens_k=cuk, num_splits=ns, cu_splits=cus,
                 work_session=ws, work_split=wsp, page_table=table, slot_mapping=slots,
-                work_desc=desc, work_pages=wpages, info=[cus[-1], split, cuq[-1], cuk[-1]],
+                work_desc=desc, work_pages=wpages,
+                info=[cus[-1], split, cuq[-1], cuk[-1], n_xcd, 0, 0, 0],
                 slot_of=slot_of)
 
 
@@ -129,7 +130,8 @@ def test_metadata_invariants(orc):
     rng = np.random.default_rng(11)
     ctx, q, cu_pages, ids, P, max_pages = random_batch(rng, 64, share_prefix=True)
     md = orc.build_metadata(ctx, q, cu_pages, ids, 64, max_pages, P, 0, 512, 65535)
-    W, split, total_q, total_k = md["info"].tolist()
+    W, split, total_q, total_k, placed_for, *rest = md["info"].tolist()
+    assert placed_for == 0 and rest == [0, 0, 0]
     assert total_q == q.sum() and total_k == (ctx + q).sum()
     assert np.all(np.diff(md["cu_seqlens_k"]) == ctx + q)
     need = -(-(ctx + q) // 64)
@@ -177,7 +179,7 @@ def test_metadata_errors_name_first_bad_session(orc, case):
 def test_metadata_empty_batch(orc):
     md = orc.build_metadata(np.zeros(0), np.zeros(0), np.zeros(1), np.zeros(0), 64, 4, 10, 0,
                             16, 8)
-    assert md["info"].tolist() == [0, 1, 0, 0]
+    assert md["info"].tolist() == [0, 1, 0, 0, 0, 0, 0, 0]
 
 
 @pytest.mark.parametrize("seed", range(6))

@@ -185,7 +185,10 @@ def _config3_case(seed=0, placement=False):
     ws = mla.decode_workspace(rb.max_work, B, H, kv)
     logits, nxt = model.step(rb, _dev(tokens), _dev(ctx), gpu_pages, ws)
     torch.cuda.synchronize()
-    rb.read_info()
+    info = rb.read_info()
+    assert info[4] == (mla.xcd_count() if placement else 0)  # the count placed for
+    # every fused merge of the step found its premises (placed metadata, items on their XCD)
+    assert mla.decode_status(ws) == 0
     got_pages = np.stack([p.view(torch.int16).cpu().numpy().view(np.uint16) for p in gpu_pages])
     model.close()
     del gpu_pages

@@ -158,3 +158,176 @@ def test_fused_decode_other_head_counts(gpu, orc, n_heads):
     got = _attn(gpu, rb, batch, 0, True, ws, None)
     want, _ = _oracle_decode(orc, batch)
     _check(got, want, f"fused H={n_heads}")
+
+
+@pytest.mark.parametrize("n_xcd, B, seed", [(1, 256, 0), (1, 70, 1), (2, 256, 2), (2, 129, 3),
+                                            (3, 200, 4), (3, 256, 5), (5, 256, 6), (8, 256, 7)])
+def test_placed_metadata_any_xcd_count(gpu, orc, n_xcd, B, seed):
+    """The placed layout for an explicit XCD count (mla_build_metadata_placed), bit-exact
+    against the oracle's placement up to 256 sessions: with n = 1..3 there are more than 64
+    rounds of n sessions, which the builder deals 64 rounds per pass."""
+    from test_metadata_oracle import random_batch
+    rng = np.random.default_rng(700 + seed)
+    ctx, q, cu_pages, ids, P, mp = random_batch(rng, B, decode=seed % 2 == 0, max_ctx=2000)
+    max_work = gpu.placed_work_slots(ctx, q, 64, 4, n_xcd) + 3
+    _say(f"placed metadata n_xcd={n_xcd} B={B} max_work={max_work}")
+    want = orc.build_metadata(ctx, q, cu_pages, ids, 64, mp, P, 4, 512, max_work,
+                              placement_xcds=n_xcd)
+    rb = gpu.build_metadata(_dev(np.asarray(ctx, np.int32)), _dev(np.asarray(q, np.int32)),
+                            _dev(np.asarray(cu_pages, np.int32)), _dev(np.asarray(ids, np.int32)),
+                            64, mp, P, split_pages=4, max_work=max_work, max_rows=1 << 16,
+                            placement_xcds=n_xcd)
+    assert rb.read_info() == want["info"].tolist() and want["info"][4] == n_xcd
+    occ = want["occupied"]
+    desc = rb.work_desc.cpu().numpy().reshape(-1, 8)
+    np.testing.assert_array_equal(desc[:, 0] >= 0, occ)
+    np.testing.assert_array_equal(desc[occ], want["work_desc"][occ])
+    np.testing.assert_array_equal(rb.work_pages.cpu().numpy().reshape(-1, 8)[occ],
+                                  want["work_pages"][occ])
+
+
+def test_fused_decode_config4_as_benched(gpu, orc):
+    """Config 4 exactly as bench.py's config-4 leg runs it: XCD-placed metadata for the 128
+    sessions, the one-launch decode (merge inside the launch; decode sessions of up to
+    16,384 tokens, i.e. up to 64 splits folded 16 at a time), then the chunked-prefill
+    kernel into the same output.  Every row and its lse against the oracle."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import mixed_prefill_batch
+    from test_prefill import _check as _check_rows, _oracle
+    b = mixed_prefill_batch(seed=0)
+    n = gpu.xcd_count()
+    mw = gpu.placed_work_slots(b.ctx_len, b.q_len, 64, 4, n)
+    rows = int(b.q_len.sum())
+    rb = gpu.build_metadata(_dev(b.ctx_len), _dev(b.q_len), _dev(b.cu_pages), _dev(b.page_ids),
+                            64, b.max_pages, b.num_pages, split_pages=4, max_work=mw,
+                            max_rows=rows, placement=True)
+    nsp = -(-((b.k_len + 63) // 64) // 4)
+    _say(f"fused decode config4: max_work={mw} max splits={int(nsp.max())}")
+    assert nsp[b.q_len == 1].max() > 32  # sessions past two groups of 16 splits
+    pages = _dev(b.pages[0].view(np.int16)).view(torch.float16)
+    ql = _dev(b.q_latent.view(np.int16)).view(torch.float16)
+    qr = _dev(b.q_rope.view(np.int16)).view(torch.float16)
+    out = torch.full((rows, 8, 128), float("nan"), dtype=torch.float32, device="cuda")
+    lse = torch.full((rows, 8), float("nan"), dtype=torch.float32, device="cuda")
+    ws = gpu.decode_workspace(mw, len(b.q_len), 8, 128)
+    gpu.decode_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16, out=out, lse=lse,
+                         workspace=ws)
+    gpu.prefill_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16, max_q_len=512,
+                          out=out, lse=lse)
+    torch.cuda.synchronize()
+    assert rb.read_info()[4] == n and rb.placed
+    assert gpu.decode_status(ws) == 0
+    want, want_lse = _oracle(orc, b)
+    got = out.cpu().numpy()
+    _check_rows(got, want, "config4 fused decode + prefill")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, rtol=1e-4, atol=1e-3)
+
+
+def test_fused_decode_every_fold_group_size(gpu, orc):
+    """Sessions whose split counts are 1, 2, 15, 16, 17, 32, 33 and 64 (16,384 tokens): the
+    merging item folds its session's partials 16 at a time, so every group size of the fold
+    (full groups and a remainder of 1) runs.  NaN in the unused slots of every last page."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    from test_gpu_kernels import _oracle_decode
+    lens = [100, 300, 3800, 4096, 4097, 8192, 8193, 16384, 64, 16383]
+    batch = ragged_decode_batch(lengths=lens, seed=21)
+    ps = 64
+    for b, k in enumerate(batch.k_len):  # garbage past each session's end
+        last = batch.page_ids[batch.cu_pages[b + 1] - 1]
+        from cpp_inference_train_engine_amd.ops import latent_word, rope_word
+        slots = np.arange(int(k) % ps or ps, ps)
+        if slots.size:
+            lw = latent_word(slots[:, None], np.arange(128)[None, :], ps, 128, 16)
+            rw = rope_word(slots[:, None], np.arange(16)[None, :], ps, 128, 16)
+            batch.pages[0, last, lw] = 0x7E00
+            batch.pages[0, last, rw] = 0x7E00
+    nsp = -(-((batch.k_len + 63) // 64) // 4)
+    assert sorted(set(nsp.tolist())) == [1, 2, 15, 16, 17, 32, 33, 64]
+    n = gpu.xcd_count()
+    mw = gpu.placed_work_slots(batch.ctx_len, batch.q_len, 64, 4, n)
+    rb = _placed(gpu, batch.ctx_len, batch.q_len, batch.cu_pages, batch.page_ids, 64,
+                 batch.max_pages, batch.num_pages, 4, mw)
+    ws = gpu.decode_workspace(mw, len(lens), 8, 128)
+    _say(f"fused decode fold groups: splits {nsp.tolist()}")
+    lse = torch.zeros((len(lens), 8), dtype=torch.float32, device="cuda")
+    got = _attn(gpu, rb, batch, 0, True, ws, lse)
+    want, want_lse = _oracle_decode(orc, batch)
+    _check(got, want, "fused fold groups")
+    np.testing.assert_allclose(lse.cpu().numpy(), want_lse, rtol=1e-4, atol=1e-3)
+    assert gpu.decode_status(ws) == 0
+    assert int(ws[:1024].view(torch.int32).abs().sum()) == 0  # counters back to zero
+
+
+def test_fused_flag_over_unplaced_metadata_is_flagged_not_wrong(gpu, orc):
+    """MLA_DECODE_FUSED_MERGE through the C ABI over metadata in session order, and over
+    metadata placed for another XCD count: the kernel does not merge, sets the session rows
+    of split sessions to NaN (one-item sessions are final), leaves the partials, and raises
+    MLA_DECODE_STATUS_UNPLACED; mla_decode_merge then completes every row."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    from test_gpu_kernels import _oracle_decode
+    batch = ragged_decode_batch(B=24, min_len=1, max_len=2500, seed=13)
+    want, _ = _oracle_decode(orc, batch)
+    one_item = -(-((batch.k_len + 63) // 64) // 4) == 1
+    assert one_item.any() and not one_item.all()
+    n = gpu.xcd_count()
+    for label, kw in (("session order", {}), ("placed for 3 XCDs", {"placement_xcds": 3})):
+        mw = gpu.placed_work_slots(batch.ctx_len, batch.q_len, 64, 4, 3) + 64
+        rb = gpu.build_metadata(_dev(batch.ctx_len), _dev(batch.q_len), _dev(batch.cu_pages),
+                                _dev(batch.page_ids), 64, batch.max_pages, batch.num_pages,
+                                split_pages=4, max_work=mw, max_rows=64, **kw)
+        assert not rb.placed and rb.read_info()[4] == kw.get("placement_xcds", 0) != n
+        ws = gpu.decode_workspace(mw, 24, 8, 128)
+        rb.placed = True  # get past the wrapper's guard to the kernel's own check
+        _say(f"fused flag over unplaced metadata: {label}")
+        out = torch.zeros((24, 8, 128), dtype=torch.float32, device="cuda")
+        pages = _dev(batch.pages[0].view(np.int16)).view(torch.float16)
+        ql = _dev(batch.q_latent.view(np.int16)).view(torch.float16)
+        qr = _dev(batch.q_rope.view(np.int16)).view(torch.float16)
+        gpu.decode_attention(rb, pages, ql, qr, 0.125, kv_rank=128, rope_dim=16, out=out,
+                             workspace=ws, fused=True)
+        torch.cuda.synchronize()
+        assert gpu.decode_status(ws) == gpu.DECODE_STATUS_UNPLACED
+        got = out.cpu().numpy()
+        assert np.isnan(got[~one_item]).all()
+        _check(got[one_item], want[one_item], f"{label}: one-item rows")
+        gpu.decode_merge(rb, 8, 128, out, ws)
+        torch.cuda.synchronize()
+        _check(out.cpu().numpy(), want, f"{label}: after mla_decode_merge")
+        assert gpu.decode_status(ws, clear=True) == gpu.DECODE_STATUS_UNPLACED
+        assert gpu.decode_status(ws) == 0
+
+
+def test_stale_merge_counts_are_reported(gpu, orc):
+    """What a broken placement leaves behind -- a session whose items ran on several XCDs
+    counts in several L2s, nobody merges it and its counter stays nonzero -- is reported as
+    MLA_DECODE_STATUS_XCD.  Planted here from the host (a stale count in the workspace head),
+    it stays visible after further fused calls until the head is cleared; with a clean head
+    the status is 0 and the rows are the oracle's."""
+    import torch
+    from cpp_inference_train_engine_amd.workloads import ragged_decode_batch
+    from test_gpu_kernels import _oracle_decode
+    batch = ragged_decode_batch(B=16, min_len=300, max_len=3000, seed=17)
+    n = gpu.xcd_count()
+    mw = gpu.placed_work_slots(batch.ctx_len, batch.q_len, 64, 4, n)
+    rb = _placed(gpu, batch.ctx_len, batch.q_len, batch.cu_pages, batch.page_ids, 64,
+                 batch.max_pages, batch.num_pages, 4, mw)
+    ws = gpu.decode_workspace(mw, 16, 8, 128)
+    want, _ = _oracle_decode(orc, batch)
+    got = _attn(gpu, rb, batch, 0, True, ws, None)
+    assert gpu.decode_status(ws) == 0
+    _check(got, want, "clean head")
+    ns = -(-((batch.k_len + 63) // 64) // 4)
+    s = int(np.argmax(ns))
+    assert ns[s] > 1
+    ws[:1024].view(torch.int32)[s] = 1  # a count left by an earlier call
+    _say(f"fused decode over a stale count of session {s} ({int(ns[s])} splits)")
+    _attn(gpu, rb, batch, 0, True, ws, None)
+    assert gpu.decode_status(ws) == gpu.DECODE_STATUS_XCD
+    _attn(gpu, rb, batch, 0, True, ws, None)
+    assert gpu.decode_status(ws, clear=True) == gpu.DECODE_STATUS_XCD
+    assert gpu.decode_status(ws) == 0
+    got = _attn(gpu, rb, batch, 0, True, ws, None)
+    assert gpu.decode_status(ws) == 0
+    _check(got, want, "after clearing")
