@@ -9,9 +9,7 @@
 namespace mla {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -24,7 +22,6 @@ constexpr float kLn2 = 0.6931471805599453f;
 struct F16 {
     using scalar = _Float16;
     using vec8 = half8;
-    using vec4 = half4;
     static constexpr int code = 0;
     // Softmax probabilities enter the P.C MFMA as one fp16 operand (2^-11 relative).
     static constexpr bool split_p = false;
@@ -38,15 +35,11 @@ struct F16 {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
     __device__ static vec8 ones8() { return vec8{1, 1, 1, 1, 1, 1, 1, 1}; }
-    __device__ static floatx4 mma16(vec4 a, vec4 b, floatx4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
-    }
 };
 
 struct BF16 {
     using scalar = __bf16;
     using vec8 = bf8;
-    using vec4 = bf4;
     static constexpr int code = 1;
     // bf16 keeps 8 mantissa bits: probabilities enter the P.C MFMA as hi + lo bf16
     // parts (two MFMAs, about 16 bits), so the output stays within the fp32 tolerance.
@@ -67,9 +60,6 @@ struct BF16 {
     __device__ static vec8 ones8() {
         const __bf16 one = __builtin_bit_cast(__bf16, static_cast<uint16_t>(0x3f80));
         return vec8{one, one, one, one, one, one, one, one};
-    }
-    __device__ static floatx4 mma16(vec4 a, vec4 b, floatx4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
     }
 };
 
