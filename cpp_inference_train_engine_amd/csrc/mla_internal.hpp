@@ -33,7 +33,7 @@ struct MetadataArgs {
         *work_session, *work_split, *work_desc, *work_pages, *info;
     // XCD placement of the work list: the number of XCDs n (0 = work items in session
     // order).  With n > 0 every session's items sit in consecutive slots x + n k of one
-    // XCD x (workgroup w of a launch runs on XCD w % n), sessions dealt to the XCDs by
+    // XCD (the workgroups w of a launch with one residue w % n share an XCD), dealt to the XCDs by
     // pages read, largest first, in rounds of n (see place_sessions); info[4] records n.
     // B <= kPlaceMaxSessions, n <= kPlaceMaxXcds.
     int placement;

@@ -109,8 +109,8 @@ int mla_abi_version(void);
  *
  * XCD placement (placement = 1; no reference counterpart): the work list is laid
  * out so that all items of a session run on one XCD of the GPU, whose dispatch
- * puts workgroup w of a launch on XCD w % n (n XCDs; checked once per device by
- * mla_xcd_placement_supported).  Sessions ranked by pages read, largest first
+ * puts the workgroups w of a launch with one residue w % n on one XCD (n XCDs; checked
+ * once per device by mla_xcd_placement_supported).  Sessions ranked by pages read, largest first
  * (ties: lower session), are dealt to the XCDs in rounds of n: rank r to XCD r % n
  * in even rounds and n - 1 - r % n in odd ones, so no XCD's pages exceed another's
  * by more than the largest session's.  Item sp of session b goes to slot
