@@ -56,8 +56,8 @@ class RaggedBatch:
 
 def xcd_count() -> int:
     """XCDs of the current device when it keeps the workgroups w with one residue w % n on one
-    XCD (the premise of
-    XCD placement), else 0.  The first call per device runs a probe kernel."""
+    XCD (the premise of XCD placement), else 0.  The first call per device runs a probe
+    kernel."""
     return int(lib().mla_xcd_placement_supported())
 
 
