@@ -73,13 +73,23 @@ struct StepArgs {
     float* ss_res;  // [m_pad x d_pad/16] of res (g4) -> ffn_norm (g5)
 };
 
+// The decode attention's pages, read ahead into L2 by extra workgroups of the qkv launch
+// that precedes it on the stream (page_prefetch, model.hip).  max_work = 0: none.
+struct PagePrefetch {
+    const int32_t *work_desc, *work_pages;  // the attention's work list
+    int max_work;   // work items (the attention's grid), 0 = no read-ahead
+    int pages;      // leading pages of each work item read ahead, <= kWorkPages
+    int page_size;  // tokens per page
+    int record;     // 16-bit words per page record
+};
+
 int g7_parts(const ModelDims& m);
 size_t qkv_lds_bytes(const ModelDims& m);
 hipError_t model_kernel_attributes(const ModelDims& m);
 // first_norm: attn_norm of layer 0
 hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t st);
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
-                            hipStream_t st);  // qkv_kernel (which appends to `pool`)
+                            const PagePrefetch& pf, hipStream_t st);  // qkv_kernel (which appends to `pool`)
 // next_norm: attn_norm of the next layer, or final_norm after the last one; next: the
 // next layer's weights (their qkv blocks are prefetched into L2), or null
 hipError_t launch_layer_post(const StepArgs& s, const LayerWeights& w, const float* next_norm,

@@ -85,6 +85,49 @@ __device__ __forceinline__ void l2_prefetch(int n, F&& addr, uint16_t* scratch, 
         copy_block_to_lds(addr(k), lane * 16, scratch);
 }
 
+// ---- the decode attention's pages, read ahead during qkv_kernel ----------------------
+// qkv_kernel occupies a few dozen CUs for several microseconds, and the attention that
+// follows it on the stream starts its 40 MB page stream only when qkv ends.  The attention
+// runs work item w with residue w % 8 (decode_page_kernel: one workgroup per item), so the
+// qkv launch gets one more block of 8 columns, and its workgroups of residue x copy the
+// leading pf.pages pages of the items x, x + 8, ... into LDS scratch: the lines land in
+// that XCD's L2, where the attention's page loads then hit.  The page that a decode
+// session's new token is appended to in this same launch (index (k_len - 1) / page_size)
+// is skipped: a copy taken before the append lands would be stale.  Items of prefill
+// sessions (q_len > 1), whose chunk is appended here too, are skipped whole.  Each wave
+// reads the descriptors of its items once (one vector load round), then issues the
+// copies of each valid page, 1 KB per instruction; nothing waits for them.
+__device__ void page_prefetch(const PagePrefetch& pf, const uint16_t* pool, int npool,
+                              uint16_t* scratch, int x, int gw, int nw) {
+    const int lane = threadIdx.x & 63;
+    const int items = x < pf.max_work ? (pf.max_work - 1 - x) / kXcds + 1 : 0;
+    const int pairs = items * pf.pages, bytes = pf.record * 2;
+    const uint32_t lds = lds_u32(scratch + (threadIdx.x >> 6) * 512);
+    for (int r0 = gw; r0 < pairs; r0 += 64 * nw) {
+        const int p = r0 + nw * lane;  // this lane's (item, page) pair of the round
+        bool ok = false;
+        int page = 0;
+        if (p < pairs) {
+            const int t = p / pf.pages, j = p % pf.pages, w = x + kXcds * t;
+            const int32_t* d = pf.work_desc + (long long)w * kWorkDescInts;
+            const int sess = d[0], kl = d[2], first = d[3], end = d[4], q_len = d[7];
+            page = pf.work_pages[(long long)w * kWorkPages + j];
+            ok = sess >= 0 && q_len == 1 && first + j < end &&
+                 first + j != (kl - 1) / pf.page_size && (unsigned)page < (unsigned)npool;
+        }
+        // The ids are read here, once: a wait for them inside the loop below would also
+        // wait for the copies already issued (vmcnt retires in order).
+        asm volatile("" ::"v"(page));
+        for (uint64_t m = __ballot(ok); m; m &= m - 1) {
+            const int pg = __builtin_amdgcn_readlane(page, __builtin_ctzll(m));
+            const uint16_t* base = pool + (long long)pg * pf.record;
+            for (int b = 0; b * 1024 < bytes; ++b)
+                if (b * 1024 + lane * 16 < bytes)
+                    copy_block_to_lds_at(base + b * 512, lane * 16, lds);
+        }
+    }
+}
+
 // Sums over aligned groups of G = 4, 8 or 16 lanes of a 16-lane row, left in every lane
 // of the group, on DPP lane moves (VALU) instead of LDS permutes: the two quad swaps give
 // every lane its quad's sum, then the half-row mirror pairs the quads of each half and the
@@ -365,7 +408,7 @@ __host__ __device__ inline QkvLds qkv_lds(const ModelDims& m) {
 // KC: chunks of two k-steps per wave (KT <= 16 * KC); NT >= the workgroup's column tiles.
 template <int KC, int NT>
 __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWeights L,
-                                                             uint16_t* pool) {
+                                                             uint16_t* pool, PagePrefetch pf) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const ModelDims& m = s.dims;
     const QkvLds lay = qkv_lds(m);
@@ -377,8 +420,13 @@ __global__ __launch_bounds__(64 * kQkvWaves) void qkv_kernel(StepArgs s, LayerWe
     __shared__ float inv_x[kQkvRows];
 
     const int h = blockIdx.x, row0 = blockIdx.y * kQkvRows;
-    if (h > m.H)
-        return;  // the grid's columns are padded to a multiple of 8 (head h: residue h % 8)
+    if (h > m.H) {  // the heads' columns are padded to a multiple of 8 (head h: residue h % 8)
+        if (h >= (m.H + kXcds) / kXcds * kXcds)  // the read-ahead block past them
+            page_prefetch(pf, pool, s.num_pool_pages, reinterpret_cast<uint16_t*>(smem),
+                          block_xcd(), blockIdx.y * kQkvWaves + (threadIdx.x >> 6),
+                          gridDim.y * kQkvWaves);
+        return;
+    }
     const bool kv = h == m.H;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int KT = m.d_pad / 32, q_tiles = m.q_pad / 16;
@@ -975,16 +1023,19 @@ hipError_t launch_embed(const StepArgs& s, const float* first_norm, hipStream_t 
 }
 
 hipError_t launch_layer_pre(const StepArgs& s, const LayerWeights& w, uint16_t* pool,
-                            hipStream_t st) {
+                            const PagePrefetch& pf, hipStream_t st) {
     const ModelDims& m = s.dims;
-    const dim3 grid(round_up_to(m.H + 1, kXcds), ceil_div(s.B, kQkvRows));  // see l2_prefetch
     const size_t lds = qkv_lds_bytes(m);
+    // heads padded to 8 columns (see l2_prefetch), then 8 read-ahead columns (page_prefetch,
+    // 1 KB of the LDS per wave)
+    const bool ahead = pf.max_work > 0 && pf.pages > 0 && lds >= kQkvWaves * 1024;
+    const dim3 grid(round_up_to(m.H + 1, kXcds) + (ahead ? kXcds : 0), ceil_div(s.B, kQkvRows));
     const int nt = max(m.q_pad, m.kvw_pad) / 16;  // <= 16 (mla_model_create checks)
     const int tiles = nt <= 4 ? 4 : nt <= 8 ? 8 : nt <= 12 ? 12 : 16;
     // d_pad <= 512: one chunk of two k-steps per wave; <= 1024: two
     const int kc = m.d_pad / 32 <= 2 * kQkvWaves ? 1 : 2;
 #define MLA_QKV(KC, NT)                                                                         \
-    hipLaunchKernelGGL((qkv_kernel<KC, NT>), grid, dim3(64 * kQkvWaves), lds, st, s, w, pool)
+    hipLaunchKernelGGL((qkv_kernel<KC, NT>), grid, dim3(64 * kQkvWaves), lds, st, s, w, pool, pf)
     if (kc == 1) {
         if (tiles == 4) MLA_QKV(1, 4); else if (tiles == 8) MLA_QKV(1, 8);
         else if (tiles == 12) MLA_QKV(1, 12); else MLA_QKV(1, 16);

@@ -18,6 +18,11 @@ namespace {
 
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
+// Leading pages of each decode work item that qkv_kernel reads ahead into L2 (page_prefetch).
+// Config 3 (570 items of 4 pages): 1 page took the step from 0.3854 to 0.3816 ms; 2 and 3
+// pages (20 and 30 MB) outlast qkv_kernel (14.8 and 20 us) and slowed the step.
+constexpr int kReadAheadPages = 1;
+
 // ModelConfig::validate (src/model/config.cpp:20-48) and parameter_count (:7-19).
 size_t parameter_count(const mla_model_config& c) {
     const size_t d = c.d_model, h = c.n_heads, q = c.q_lora_rank, kv = c.kv_lora_rank;
@@ -396,12 +401,23 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
         return bad;
     // decode (+ the split merge unless the decode launch merges itself)
     const int attn_launches = md.max_work > 0 && B > 0 ? 2 - a.fused_merge : 0;
+    // The MFMA page kernel's leading pages are read ahead into L2 during qkv_kernel.
+    PagePrefetch pf{};
+    if (attn_launches > 0 && !generic &&
+        decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size)) {
+        pf.work_desc = md.work_desc;
+        pf.work_pages = md.work_pages;
+        pf.max_work = md.max_work;
+        pf.pages = kReadAheadPages;
+        pf.page_size = m.page_size;
+        pf.record = m.page_size * (m.kv_rank + m.rope);
+    }
     hipError_t e = launch_embed(s, M->layers[0].attn_norm, st);
     uint64_t launched = 1;
     for (int l = 0; l < m.n_layers && e == hipSuccess; ++l) {
         const float* next_norm = l + 1 < m.n_layers ? M->layers[l + 1].attn_norm : M->final_norm;
         uint16_t* pool = static_cast<uint16_t*>(pages[l]);
-        e = launch_layer_pre(s, M->layers[l], pool, st);
+        e = launch_layer_pre(s, M->layers[l], pool, pf, st);
         if (e != hipSuccess)
             break;
         a.pages = pool;
