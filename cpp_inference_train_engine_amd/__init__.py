@@ -21,6 +21,7 @@ DTYPE_F16, DTYPE_BF16 = 0, 1
 WORK_DESC_INTS, WORK_PAGES, MAX_WORK, INFO_INTS = 8, 8, 65535, 8
 DECODE_FORCE_GENERIC = 1
 DECODE_FUSED_MERGE = 2
+STEP_NO_READ_AHEAD = 4
 DECODE_STATUS_XCD, DECODE_STATUS_UNPLACED = 1, 2
 DECODE_WORKSPACE_HEAD, DECODE_STATUS_OFFSET = 1280, 1024
 PLACE_MAX_SESSIONS = 256

@@ -403,7 +403,7 @@ int model_forward(Model* M, hipStream_t st, int rows, const int32_t* tokens,
     const int attn_launches = md.max_work > 0 && B > 0 ? 2 - a.fused_merge : 0;
     // The MFMA page kernel's leading pages are read ahead into L2 during qkv_kernel.
     PagePrefetch pf{};
-    if (attn_launches > 0 && !generic &&
+    if (attn_launches > 0 && !generic && !(md.flags & MLA_STEP_NO_READ_AHEAD) &&
         decode_mfma_supported(a.H, a.kv_rank, a.rope_dim, a.page_size)) {
         pf.work_desc = md.work_desc;
         pf.work_pages = md.work_pages;

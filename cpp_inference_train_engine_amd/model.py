@@ -13,7 +13,7 @@ import ctypes as C
 import json
 import os
 
-from . import DECODE_FUSED_MERGE, check, lib, ptr, stream_handle
+from . import DECODE_FUSED_MERGE, STEP_NO_READ_AHEAD, check, lib, ptr, stream_handle
 
 _FIELDS = ("vocab_size", "max_sequence_length", "n_layers", "d_model", "n_heads",
            "head_dim_nope", "head_dim_rope", "head_dim_value", "q_lora_rank", "kv_lora_rank",
@@ -124,10 +124,12 @@ class HipModel:
         self.close()
 
     def step(self, batch, tokens, positions, pages, workspace, logits=None, next_tokens=None,
-             stream=None):
+             stream=None, read_ahead=True):
         """One decode step.  ``batch`` is the RaggedBatch of mla_build_metadata (q_len = 1,
         ctx_len = positions); ``pages`` is the list of per-layer page pools; tokens and
-        positions are device int32 [B].  Returns (logits [B x vocab] fp32, next_tokens [B])."""
+        positions are device int32 [B].  read_ahead=False turns off the L2 read-ahead of
+        the attention's pages (MLA_STEP_NO_READ_AHEAD: same results, other timing).
+        Returns (logits [B x vocab] fp32, next_tokens [B])."""
         import torch
         B = int(tokens.numel())
         dev = tokens.device
@@ -142,5 +144,6 @@ class HipModel:
             batch.num_pool_pages, ptr(batch.slot_mapping), ptr(batch.num_splits),
             ptr(batch.cu_splits), ptr(batch.work_desc), ptr(batch.work_pages), ptr(batch.info),
             batch.max_work, pools, ptr(workspace), int(workspace.numel()), ptr(logits),
-            ptr(next_tokens), DECODE_FUSED_MERGE if batch.placed else 0))
+            ptr(next_tokens),
+            (DECODE_FUSED_MERGE if batch.placed else 0) | (0 if read_ahead else STEP_NO_READ_AHEAD)))
         return logits, next_tokens

@@ -64,6 +64,10 @@ extern "C" {
 /* Decode-attention flags. */
 #define MLA_DECODE_FORCE_GENERIC 1 /* use the portable VALU kernel even when the MFMA one fits */
 #define MLA_DECODE_FUSED_MERGE 2   /* metadata built with placement = 1: merge inside the launch */
+/* mla_model_step / mla_model_forward: no read-ahead of the decode attention's pages into L2
+ * during each layer's projection kernel (the results are the same bit for bit; the
+ * read-ahead only changes timing). */
+#define MLA_STEP_NO_READ_AHEAD 4
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* mla_last_error(void);

@@ -253,3 +253,41 @@ def test_model_step_mla36m_matches_oracle(gpu, orc, B, max_ctx, seed):
     """mla36m (config 2/3 model): MFMA attention path; B=70 spans two 64-row chunks."""
     r = _step_case(dict(MLA36M, max_sequence_length=1024), B=B, max_ctx=max_ctx, seed=seed)
     _check_step(r, f"mla36m B={B}")
+
+
+@pytest.mark.gpu
+def test_model_step_read_ahead_changes_no_bit(gpu):
+    """The L2 read-ahead of the attention's pages during qkv_kernel (default) against the
+    same config-3 placed step without it (MLA_STEP_NO_READ_AHEAD), on identical copies of
+    the pools: logits, greedy tokens and every page of every layer (the appended rows
+    included) equal bit for bit.  A read-ahead copy of the page being appended to would
+    make the attention miss the new token."""
+    import torch
+    import oracle
+    import cpp_inference_train_engine_amd as mla
+    from cpp_inference_train_engine_amd.workloads import MLA36M as CFG3, ragged_decode_batch
+    ocfg = oracle.Config.from_dict(CFG3)
+    params = oracle.bits_to_f32(oracle.round_f16(oracle.model_init(ocfg, 3)))
+    batch = ragged_decode_batch(B=64, n_layers=ocfg.n_layers, seed=3)
+    B, ps = batch.ctx_len.size, batch.page_size
+    tokens = _dev(np.random.default_rng(3).integers(0, ocfg.vocab_size, size=B).astype(np.int32))
+    model = mla.HipModel(mla.ModelConfig.from_dict(CFG3), params, max_batch=B, page_size=ps)
+    rb = mla.build_metadata(_dev(batch.ctx_len), _dev(batch.q_len), _dev(batch.cu_pages),
+                            _dev(batch.page_ids), ps, batch.max_pages, batch.num_pages,
+                            split_pages=4, placement=True)
+    ws = mla.decode_workspace(rb.max_work, B, ocfg.n_heads, ocfg.kv_lora_rank)
+    out = {}
+    for ahead in (True, False):
+        pools = [_dev(batch.pages[l].view(np.int16)).view(torch.float16)
+                 for l in range(ocfg.n_layers)]
+        logits, nxt = model.step(rb, tokens, _dev(batch.ctx_len), pools, ws, read_ahead=ahead)
+        torch.cuda.synchronize()
+        assert mla.decode_status(ws) == 0
+        out[ahead] = (logits.cpu().numpy(), nxt.cpu().numpy(),
+                      np.stack([p.view(torch.int16).cpu().numpy() for p in pools]))
+        del pools
+    model.close()
+    _say(f"read-ahead vs none: max |logit diff| {np.abs(out[True][0] - out[False][0]).max():.3e}")
+    assert np.array_equal(out[True][0].view(np.uint32), out[False][0].view(np.uint32))
+    assert np.array_equal(out[True][1], out[False][1])
+    assert np.array_equal(out[True][2], out[False][2])
