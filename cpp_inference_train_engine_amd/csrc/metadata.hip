@@ -114,15 +114,25 @@ __device__ void place_sessions(int B, int n, int page_size, Q q, C ctx, S cus, P
     for (int b = tid; b < B; b += kMetaThreads)
         p.weight[b] = q(b) > 0 ? (int32_t)ceil_div_nn((long long)ctx(b) + q(b), page_size) : 0;
     __syncthreads();
-    // rank by (weight desc, session asc): O(B) per session, B <= 256
-    for (int b = tid; b < B; b += kMetaThreads) {
-        const int wb = p.weight[b];
-        int r = 0;
-        for (int c = 0; c < B; ++c) {
-            const int wc = p.weight[c];
-            r += wc > wb || (wc == wb && c < b);
+    // rank by (weight desc, session asc): tps threads per session (a power of two <= 64,
+    // an aligned lane group) each count every tps-th other session, then sum in the group
+    int tps = 64;
+    while (tps > 1 && tps * B > kMetaThreads)
+        tps >>= 1;
+    {
+        const int b = tid / tps, part = tid % tps;
+        int r = 0, wb = 0;
+        if (b < B) {
+            wb = p.weight[b];
+            for (int c = part; c < B; c += tps) {
+                const int wc = p.weight[c];
+                r += wc > wb || (wc == wb && c < b);
+            }
         }
-        p.order[r] = b;
+        for (int off = tps >> 1; off > 0; off >>= 1)
+            r += __shfl_xor(r, off, 64);
+        if (b < B && part == 0)
+            p.order[r] = b;
     }
     __syncthreads();
     if (wave < n) {  // wave x: lane l holds XCD x's session of round q0 + l
