@@ -256,19 +256,24 @@ def test_model_step_mla36m_matches_oracle(gpu, orc, B, max_ctx, seed):
 
 
 @pytest.mark.gpu
-def test_model_step_read_ahead_changes_no_bit(gpu):
+@pytest.mark.parametrize("lengths", ["config3", "short"])
+def test_model_step_read_ahead_changes_no_bit(gpu, lengths):
     """The L2 read-ahead of the attention's pages during qkv_kernel (default) against the
-    same config-3 placed step without it (MLA_STEP_NO_READ_AHEAD), on identical copies of
-    the pools: logits, greedy tokens and every page of every layer (the appended rows
-    included) equal bit for bit.  A read-ahead copy of the page being appended to would
-    make the attention miss the new token."""
+    same placed step without it (MLA_STEP_NO_READ_AHEAD), on identical copies of the pools:
+    logits, greedy tokens and every page of every layer (the appended rows included) equal
+    bit for bit.  A read-ahead copy of the page being appended to would make the attention
+    miss the new token.  config3: 64 sessions of 128-4096 tokens; short: 64 sessions of
+    1-200 tokens, where an item's first page is often the page being appended to (the
+    read-ahead must skip it)."""
     import torch
     import oracle
     import cpp_inference_train_engine_amd as mla
     from cpp_inference_train_engine_amd.workloads import MLA36M as CFG3, ragged_decode_batch
     ocfg = oracle.Config.from_dict(CFG3)
     params = oracle.bits_to_f32(oracle.round_f16(oracle.model_init(ocfg, 3)))
-    batch = ragged_decode_batch(B=64, n_layers=ocfg.n_layers, seed=3)
+    batch = (ragged_decode_batch(B=64, n_layers=ocfg.n_layers, seed=3) if lengths == "config3"
+             else ragged_decode_batch(B=64, n_layers=ocfg.n_layers, min_len=1, max_len=200,
+                                      seed=4))
     B, ps = batch.ctx_len.size, batch.page_size
     tokens = _dev(np.random.default_rng(3).integers(0, ocfg.vocab_size, size=B).astype(np.int32))
     model = mla.HipModel(mla.ModelConfig.from_dict(CFG3), params, max_batch=B, page_size=ps)
