@@ -375,7 +375,8 @@ int mla_model_update_weights(void* model, const float* params, uint64_t* revisio
  * when the metadata was built XCD-placed (the decode attention of each layer is then
  * one launch, see mla_decode_attention: check mla_decode_status on `workspace` after
  * the step, and rerun it without the flag if a bit is set -- the step's appends are
- * idempotent), else 0. */
+ * idempotent), else 0; optionally with MLA_STEP_NO_READ_AHEAD (no L2 read-ahead of the
+ * attention's pages, same results). */
 int mla_model_step(void* model, void* stream, int B, const int32_t* tokens,
                    const int32_t* positions, const int32_t* cu_seqlens_q,
                    const int32_t* page_table, int max_pages, int num_pool_pages,
